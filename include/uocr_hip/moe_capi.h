@@ -1,0 +1,149 @@
+/*
+ * libuocr_hip -- MI355X (gfx950) INT4 MoE expert path, C ABI.
+ *
+ * Drop-in boundary for the reference's MoE operator API
+ * (include/uocr/cuda_ops.h:125-202 in vaachang/unlimited-ocr.cpp) and its
+ * caller GpuDecoder::mlp_block (src/engine/gpu_decoder.cu:518-658).
+ *
+ * Conventions (all entry points):
+ *   - plain pointers and sizes; device pointers unless a parameter says "host";
+ *   - `stream` is a hipStream_t passed as void* (NULL = default stream);
+ *   - work is enqueued asynchronously on `stream`; no entry point synchronizes
+ *     or allocates on the per-call path (creation/upload calls do allocate);
+ *   - every call returns an int status: UOCR_HIP_OK (0) or a negative code;
+ *     uocr_hip_last_error() returns the calling thread's last error text.
+ *     (The reference throws uocr::Error from host checks and silently drops
+ *     overflows, include/uocr/common.h:33-43, moe_device.cu:92; this ABI
+ *     never throws and reports instead.)
+ */
+#ifndef UOCR_HIP_MOE_CAPI_H
+#define UOCR_HIP_MOE_CAPI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define UOCR_HIP_OK 0
+#define UOCR_HIP_EINVAL (-1)      /* bad argument (null, shape, alignment) */
+#define UOCR_HIP_EUNSUPPORTED (-2) /* valid in the reference, not supported by this build */
+#define UOCR_HIP_ENOMEM (-3)      /* device allocation failed (creation calls only) */
+#define UOCR_HIP_EWORKSPACE (-4)  /* caller workspace smaller than the size query */
+#define UOCR_HIP_EHIP (-5)        /* a HIP runtime call failed; see uocr_hip_last_error() */
+
+#define UOCR_HIP_DTYPE_F32 0
+#define UOCR_HIP_DTYPE_BF16 1
+
+/* Error text of the calling thread's most recent failing call ("" if none). */
+const char* uocr_hip_last_error(void);
+
+/* Library version string. */
+const char* uocr_hip_version(void);
+
+/* Host-side INT4 matrix in the reference layout; mirrors uocr::QuantizedMatrix
+ * (include/uocr/quant.h:16-32): packed [rows, ceil(cols/2)] bytes, low nibble =
+ * even column; scales and zeros [rows, ceil(cols/group_size)] f32;
+ * value = (q - zero) * scale (src/runtime/quant.cpp:12-20). */
+typedef struct {
+    const uint8_t* packed;
+    const float* scales;
+    const float* zeros;
+    int rows;
+    int cols;
+    int group_size;
+} uocr_hip_qmatrix;
+
+/* One MoE layer (host pointers). Field names follow uocr::ModelConfig
+ * (include/uocr/config.h:18-33) and uocr::LayerWeights (include/uocr/weights.h).
+ * The shared MLP has width n_shared * inter (src/runtime/weights.cpp:352). */
+typedef struct {
+    int hidden;                 /* hidden_size */
+    int inter;                  /* moe_intermediate_size */
+    int n_experts;              /* n_routed_experts (<= 64 for the fused router) */
+    int top_k;                  /* num_experts_per_tok (<= 8) */
+    int n_shared;               /* n_shared_experts (0 = no shared MLP) */
+    int norm_topk_prob;
+    float routed_scaling_factor;
+    int scoring_sigmoid;        /* 0 = softmax, 1 = sigmoid */
+    const uint16_t* router_bf16;               /* [n_experts, hidden] bf16 bits */
+    const uocr_hip_qmatrix* gate;              /* [n_experts], each [inter, hidden] */
+    const uocr_hip_qmatrix* up;                /* [n_experts], each [inter, hidden] */
+    const uocr_hip_qmatrix* down;              /* [n_experts], each [hidden, inter] */
+    const uocr_hip_qmatrix* shared_gate;       /* [n_shared*inter, hidden] or NULL */
+    const uocr_hip_qmatrix* shared_up;         /* [n_shared*inter, hidden] or NULL */
+    const uocr_hip_qmatrix* shared_down;       /* [hidden, n_shared*inter] or NULL */
+    const float* rms_weight;    /* optional post-attention RMSNorm weight [hidden] */
+    float rms_eps;              /* rms_norm_eps */
+} uocr_hip_layer_desc;
+
+typedef struct uocr_hip_moe_layer uocr_hip_moe_layer;
+
+/* Upload + repack one layer to the current device. Replaces
+ * GpuDecoder::upload_expert_table (src/engine/gpu_decoder.cu:316-358) for the
+ * gate/up/down tables plus the router and shared-expert uploads
+ * (gpu_decoder.cu:185-187). Requirements: hidden and inter multiples of 128,
+ * group_size in {32, 64, 128} dividing inter, symmetric zero point (all
+ * zeros == 8, the layout of quantize_int4_symmetric, src/runtime/quant.cpp:82-116),
+ * |8 * scale| within the f16 range. Scales are stored as bf16 (exact for
+ * bf16-valued scales). Allocates device memory; not for the per-call path. */
+int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* desc, uocr_hip_moe_layer** out);
+int uocr_hip_moe_layer_destroy(uocr_hip_moe_layer* layer);
+
+/* Device bytes of the repacked layer (weights + router + scales). */
+size_t uocr_hip_moe_layer_device_bytes(const uocr_hip_moe_layer* layer);
+
+/* Workspace bytes uocr_hip_moe_layer_forward needs for `seq` tokens (the
+ * reference sizes the same scratch in GpuDecoder::ensure_router_scratch,
+ * src/engine/gpu_decoder.cu:438-474). */
+size_t uocr_hip_moe_layer_workspace_size(const uocr_hip_moe_layer* layer, int seq);
+
+/* One MoE layer for `seq` tokens -- the fused counterpart of the MoE part of
+ * GpuDecoder::mlp_block (src/engine/gpu_decoder.cu:537-657): router logits,
+ * top-k, grouping, routed experts, shared expert and combine.
+ *   x         [seq, hidden], dtype UOCR_HIP_DTYPE_BF16 or _F32
+ *   out       [seq, hidden] f32: moe(x) (routed + shared); for a layer created
+ *             with rms_weight: out = x + moe(rmsnorm(x)) (moe_decoder.cpp:166-179),
+ *             which requires f32 x
+ *   ids_out, weights_out  optional [seq, top_k] routing result (NULL = internal)
+ * Routing ids/weights equal the reference CPU path's bit for bit; `out`
+ * follows it within rel_l2 <= 5e-3 (FP32 accumulation of exact f16 products).
+ * Asynchronous on `stream`, no allocation, graph-capturable for a fixed seq. */
+int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* layer, const void* x, int x_dtype,
+                               int seq, float* out, int* ids_out, float* weights_out,
+                               void* workspace, size_t workspace_bytes, void* stream);
+
+/* Per-stage timing of uocr_hip_moe_layer_forward (benchmark support): when
+ * enabled, forward records HIP events between its stages on its stream.
+ * read_timing synchronizes on the last event and returns the accumulated
+ * milliseconds per stage (router, group, gate_up, down, combine) and the
+ * number of forwards accumulated; it then resets the totals. */
+int uocr_hip_moe_layer_set_timing(uocr_hip_moe_layer* layer, int enable);
+int uocr_hip_moe_layer_read_timing(uocr_hip_moe_layer* layer, float* stage_ms, int n_stages,
+                                   int* n_calls);
+
+/* Which expert kernels forward uses for `seq` tokens: 0 = decode (GEMV-like),
+ * 1 = prefill (LDS-tiled MFMA GEMM). */
+int uocr_hip_moe_layer_path(const uocr_hip_moe_layer* layer, int seq);
+
+/* ---- reference operator mirrors (include/uocr/cuda_ops.h) ---------------- */
+
+/* Mirror of uocr::cuda::moe_router_topk (include/uocr/cuda_ops.h:125-131,
+ * src/kernels/cuda/moe_device.cu:24-98): scoring + greedy top-k from logits
+ * [seq, n_experts], then per-expert assignment tables [n_experts, cap].
+ * Differences, all toward the CPU reference (moe_decoder.cpp:245-289,
+ * gpu_decoder.cu:602-609): probabilities are bit-identical to the CPU
+ * softmax (the CUDA kernel uses __expf and divides); slots are filled in
+ * ascending (token, j) order instead of atomicAdd order; d_count receives
+ * min(count, cap) and need not be zeroed by the caller. */
+int uocr_hip_moe_router_topk(const float* router_logits, int seq, int n_experts, int top_k,
+                             int norm_topk_prob, float routed_scaling_factor,
+                             int scoring_sigmoid, int* d_ids, float* d_weights,
+                             int* d_assign_token, float* d_assign_w, int* d_count, int cap,
+                             void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* UOCR_HIP_MOE_CAPI_H */

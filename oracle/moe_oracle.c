@@ -1,0 +1,366 @@
+/*
+ * CPU restatement of the reference's INT4 MoE layer -- TEST INFRASTRUCTURE ONLY.
+ *
+ * Loaded only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg (as the checker / the timed CPU baseline). The product library never
+ * links it.
+ *
+ * Pinning (how each function is checked against something other than itself):
+ *   orc_bf16_to_f32 / orc_f32_to_bf16  exhaustive vs numpy bit arithmetic + golden vectors
+ *   orc_dequantize / orc_qmatrix_at    bit-exact vs oracle/_ref (reference quant.cpp) + golden
+ *   orc_quantize_*                     bit-exact vs oracle/_ref (reference quant.cpp) + golden
+ *   orc_matmul_t(_bf16)                bit-exact vs oracle/_ref (reference cpu_ops.cpp) + golden
+ *   orc_softmax / orc_silu_mul / orc_rmsnorm  bit-exact vs oracle/_ref + golden
+ *   orc_matmul_int4                    vs float64 brute force over _ref's dequantize (bound),
+ *                                      vs exact integer arithmetic on power-of-two scales
+ *   orc_moe_gate                       known answers of tests/test_moe_gate.cpp:9-63,
+ *                                      composition of _ref matmul_t_bf16 + _ref softmax,
+ *                                      stable-argsort brute force for the greedy top-k
+ *   orc_stable_group                   equals a stable sort of (expert, token) pairs
+ *   orc_moe_layer                      float64 brute force from dequantized weights
+ * The reference's weights.cpp (INT4 matvec) and moe_decoder.cpp (moe_gate) cannot be
+ * linked here: weights.cpp needs nlohmann/json, which this image lacks.
+ */
+#include "moe_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* include/uocr/common.h:49-54 */
+float orc_bf16_to_f32(uint16_t h) {
+    uint32_t bits = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* include/uocr/common.h:56-64 (round to nearest even on the upper 16 bits) */
+uint16_t orc_f32_to_bf16(float f) {
+    uint32_t bits;
+    memcpy(&bits, &f, 4);
+    uint32_t lsb = (bits >> 16) & 1u;
+    bits = (bits + 0x7fffu + lsb) >> 16;
+    return (uint16_t)bits;
+}
+
+static inline int nib(const uint8_t* prow, int c) {
+    uint8_t b = prow[c >> 1];
+    return (c & 1) ? (b >> 4) : (b & 0x0f);
+}
+
+static inline int n_groups(const orc_qmatrix* q) { return (q->cols + q->group_size - 1) / q->group_size; }
+
+/* src/runtime/quant.cpp:12-20 */
+float orc_qmatrix_at(const orc_qmatrix* q, int r, int c) {
+    const int g = c / q->group_size;
+    const int pr = (q->cols + 1) / 2;
+    const size_t gi = (size_t)r * n_groups(q) + g;
+    return ((float)nib(q->packed + (size_t)r * pr, c) - q->zeros[gi]) * q->scales[gi];
+}
+
+/* src/runtime/quant.cpp:22-37 */
+void orc_dequantize(const orc_qmatrix* q, float* out) {
+    const int pr = (q->cols + 1) / 2, ng = n_groups(q);
+    for (int r = 0; r < q->rows; ++r) {
+        const uint8_t* prow = q->packed + (size_t)r * pr;
+        const float* s = q->scales + (size_t)r * ng;
+        const float* z = q->zeros + (size_t)r * ng;
+        for (int c = 0; c < q->cols; ++c) {
+            const int g = c / q->group_size;
+            out[(size_t)r * q->cols + c] = ((float)nib(prow, c) - z[g]) * s[g];
+        }
+    }
+}
+
+static inline void put_nib(uint8_t* prow, int c, int v) {
+    if (c & 1)
+        prow[c / 2] = (uint8_t)((prow[c / 2] & 0x0f) | (v << 4));
+    else
+        prow[c / 2] = (uint8_t)((prow[c / 2] & 0xf0) | v);
+}
+
+static inline float clampf(float v, float lo, float hi) { return v < lo ? lo : (v > hi ? hi : v); }
+static inline int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+/* src/runtime/quant.cpp:39-80 (asymmetric RTN, zero point rounded and clamped to [0,15]) */
+void orc_quantize_int4_awq(const float* w, int rows, int cols, int group, uint8_t* packed,
+                           float* scales, float* zeros) {
+    const int ng = (cols + group - 1) / group, pr = (cols + 1) / 2;
+    memset(packed, 0, (size_t)rows * pr);
+    for (int r = 0; r < rows; ++r) {
+        const float* wr = w + (size_t)r * cols;
+        uint8_t* prow = packed + (size_t)r * pr;
+        for (int g = 0; g < ng; ++g) {
+            const int c0 = g * group, c1 = (c0 + group < cols) ? c0 + group : cols;
+            float mn = wr[c0], mx = wr[c0];
+            for (int c = c0 + 1; c < c1; ++c) {
+                mn = (wr[c] < mn) ? wr[c] : mn;  /* std::min(mn, w) */
+                mx = (mx < wr[c]) ? wr[c] : mx;  /* std::max(mx, w) */
+            }
+            float scale = (mx - mn) / 15.0f;
+            if (scale < 1e-8f) scale = 1e-8f;
+            float zero = clampf(roundf(-mn / scale), 0.0f, 15.0f);
+            scales[(size_t)r * ng + g] = scale;
+            zeros[(size_t)r * ng + g] = zero;
+            for (int c = c0; c < c1; ++c) put_nib(prow, c, clampi((int)lroundf(wr[c] / scale + zero), 0, 15));
+        }
+    }
+}
+
+/* src/runtime/quant.cpp:82-116 (symmetric, zero point fixed at 8) */
+void orc_quantize_int4_symmetric(const float* w, int rows, int cols, int group,
+                                 uint8_t* packed, float* scales, float* zeros) {
+    const int ng = (cols + group - 1) / group, pr = (cols + 1) / 2;
+    memset(packed, 0, (size_t)rows * pr);
+    for (int r = 0; r < rows; ++r) {
+        const float* wr = w + (size_t)r * cols;
+        uint8_t* prow = packed + (size_t)r * pr;
+        for (int g = 0; g < ng; ++g) {
+            const int c0 = g * group, c1 = (c0 + group < cols) ? c0 + group : cols;
+            float amax = 0.0f;
+            for (int c = c0; c < c1; ++c) {
+                const float a = fabsf(wr[c]);
+                amax = (amax < a) ? a : amax;
+            }
+            float scale = amax / 7.0f;
+            if (scale < 1e-8f) scale = 1e-8f;
+            scales[(size_t)r * ng + g] = scale;
+            zeros[(size_t)r * ng + g] = 8.0f;
+            for (int c = c0; c < c1; ++c) put_nib(prow, c, clampi((int)lroundf(wr[c] / scale) + 8, 0, 15));
+        }
+    }
+}
+
+/* src/runtime/weights.cpp:51-72: serial INT4 branch of WeightMatrix::matmul.
+ * Loop order (i, r, c ascending); `acc += x * (q - z) * s` contracts to
+ * fma(x * (q - z), s, acc) under the reference's -march=native build. */
+void orc_matmul_int4(const orc_qmatrix* q, const float* x, float* y, int m) {
+    const int ng = n_groups(q), pr = (q->cols + 1) / 2, gs = q->group_size;
+    for (int i = 0; i < m; ++i) {
+        const float* xi = x + (size_t)i * q->cols;
+        float* yi = y + (size_t)i * q->rows;
+        for (int r = 0; r < q->rows; ++r) {
+            const uint8_t* prow = q->packed + (size_t)r * pr;
+            const float* s = q->scales + (size_t)r * ng;
+            const float* z = q->zeros + (size_t)r * ng;
+            float acc = 0.0f;
+            for (int c = 0; c < q->cols; ++c) {
+                const int g = c / gs;
+                acc = fmaf(xi[c] * ((float)nib(prow, c) - z[g]), s[g], acc);
+            }
+            yi[r] = acc;
+        }
+    }
+}
+
+/* src/kernels/cpu_ops.cpp:11-24 (row-parallel above 2^18 MACs; per-output sequential FMA chain) */
+void orc_matmul_t(const float* x, const float* w, const float* bias, float* y, int m, int n,
+                  int k) {
+#pragma omp parallel for schedule(static) if ((long long)m * n * k > (1 << 18))
+    for (int i = 0; i < m; ++i) {
+        for (int j = 0; j < n; ++j) {
+            const float* wr = w + (size_t)j * k;
+            const float* xr = x + (size_t)i * k;
+            float acc = bias ? bias[j] : 0.0f;
+            for (int t = 0; t < k; ++t) acc = fmaf(xr[t], wr[t], acc);
+            y[(size_t)i * n + j] = acc;
+        }
+    }
+}
+
+/* src/kernels/cpu_ops.cpp:26-39 */
+void orc_matmul_t_bf16(const float* x, const uint16_t* w, const float* bias, float* y, int m,
+                       int n, int k) {
+#pragma omp parallel for schedule(static) if ((long long)m * n * k > (1 << 18))
+    for (int i = 0; i < m; ++i) {
+        for (int j = 0; j < n; ++j) {
+            const uint16_t* wr = w + (size_t)j * k;
+            const float* xr = x + (size_t)i * k;
+            float acc = bias ? bias[j] : 0.0f;
+            for (int t = 0; t < k; ++t) acc = fmaf(xr[t], orc_bf16_to_f32(wr[t]), acc);
+            y[(size_t)i * n + j] = acc;
+        }
+    }
+}
+
+/* src/kernels/cpu_ops.cpp:93-106: max, exp(x - max) summed in order, multiply by 1/sum */
+void orc_softmax(float* x, int rows, int cols) {
+    for (int r = 0; r < rows; ++r) {
+        float* row = x + (size_t)r * cols;
+        float mx = row[0];
+        for (int c = 1; c < cols; ++c) mx = (mx < row[c]) ? row[c] : mx;
+        float sum = 0.0f;
+        for (int c = 0; c < cols; ++c) {
+            row[c] = expf(row[c] - mx);
+            sum += row[c];
+        }
+        const float inv = 1.0f / sum;
+        for (int c = 0; c < cols; ++c) row[c] *= inv;
+    }
+}
+
+/* src/kernels/cpu_ops.cpp:108-113 */
+void orc_silu_mul(const float* gate, const float* up, float* out, long long n) {
+    for (long long i = 0; i < n; ++i) {
+        const float g = gate[i];
+        out[i] = (g / (1.0f + expf(-g))) * up[i];
+    }
+}
+
+/* src/kernels/cpu_ops.cpp:58-67 (`ss += x * x` contracts to fma) */
+void orc_rmsnorm(const float* x, const float* w, float* out, int rows, int cols, float eps) {
+    for (int r = 0; r < rows; ++r) {
+        const float* xr = x + (size_t)r * cols;
+        float ss = 0.0f;
+        for (int c = 0; c < cols; ++c) ss = fmaf(xr[c], xr[c], ss);
+        const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
+        float* o = out + (size_t)r * cols;
+        for (int c = 0; c < cols; ++c) o[c] = xr[c] * inv * w[c];
+    }
+}
+
+/* src/engine/moe_decoder.cpp:258-288: scoring, greedy top-k (strict '>', first
+ * maximum wins, chosen entry set to -1e30), optional renormalisation, scaling. */
+static void gate_select(float* logits, int rows, int n_experts, int top_k, int norm,
+                        float scaling, int sigmoid, int* ids, float* weights) {
+    for (int r = 0; r < rows; ++r) {
+        float* row = logits + (size_t)r * n_experts;
+        if (sigmoid) {
+            for (int e = 0; e < n_experts; ++e) row[e] = 1.0f / (1.0f + expf(-row[e]));
+        } else {
+            orc_softmax(row, 1, n_experts);
+        }
+        for (int j = 0; j < top_k; ++j) {
+            int best = -1;
+            float bestv = -1e30f;
+            for (int e = 0; e < n_experts; ++e)
+                if (row[e] > bestv) {
+                    bestv = row[e];
+                    best = e;
+                }
+            ids[(size_t)r * top_k + j] = best;
+            weights[(size_t)r * top_k + j] = bestv;
+            if (best >= 0) row[best] = -1e30f;
+        }
+        float* w = weights + (size_t)r * top_k;
+        if (top_k > 1 && norm) {
+            float sum = 0.0f;
+            for (int j = 0; j < top_k; ++j) sum += w[j];
+            const float denom = sum + 1e-20f;
+            for (int j = 0; j < top_k; ++j) w[j] = w[j] / denom * scaling;
+        } else {
+            for (int j = 0; j < top_k; ++j) w[j] *= scaling;
+        }
+    }
+}
+
+/* src/engine/moe_decoder.cpp:245-289 with a BF16 router (weights.cpp:48-50 -> cpu_ops.cpp:26-39) */
+void orc_moe_gate(const float* x, const uint16_t* router_bf16, int rows, int hidden,
+                  int n_experts, int top_k, int norm_topk_prob, float scaling, int sigmoid,
+                  int* ids, float* weights) {
+    float* logits = (float*)malloc(sizeof(float) * (size_t)rows * n_experts);
+    orc_matmul_t_bf16(x, router_bf16, NULL, logits, rows, n_experts, hidden);
+    gate_select(logits, rows, n_experts, top_k, norm_topk_prob, scaling, sigmoid, ids, weights);
+    free(logits);
+}
+
+/* Same with an F32 router (weights.cpp:42-44 -> cpu_ops.cpp:11-24); used by the
+ * known-answer tests of tests/test_moe_gate.cpp, whose router is F32_OWNED. */
+void orc_moe_gate_f32router(const float* x, const float* router_f32, int rows, int hidden,
+                            int n_experts, int top_k, int norm_topk_prob, float scaling,
+                            int sigmoid, int* ids, float* weights) {
+    float* logits = (float*)malloc(sizeof(float) * (size_t)rows * n_experts);
+    orc_matmul_t(x, router_f32, NULL, logits, rows, n_experts, hidden);
+    gate_select(logits, rows, n_experts, top_k, norm_topk_prob, scaling, sigmoid, ids, weights);
+    free(logits);
+}
+
+/* src/engine/gpu_decoder.cu:602-609: for t, for j: e_tokens[ids[t,j]].push_back(t)
+ * -- a stable counting sort of the (t, j) entries by expert. */
+void orc_stable_group(const int* ids, int seq, int top_k, int n_experts, int* counts,
+                      int* offsets, int* perm_token, int* perm_j) {
+    memset(counts, 0, sizeof(int) * n_experts);
+    for (int i = 0; i < seq * top_k; ++i) counts[ids[i]]++;
+    offsets[0] = 0;
+    for (int e = 0; e < n_experts; ++e) offsets[e + 1] = offsets[e] + counts[e];
+    int* fill = (int*)calloc((size_t)n_experts, sizeof(int));
+    for (int t = 0; t < seq; ++t)
+        for (int j = 0; j < top_k; ++j) {
+            const int e = ids[t * top_k + j];
+            const int s = offsets[e] + fill[e]++;
+            perm_token[s] = t;
+            if (perm_j) perm_j[s] = j;
+        }
+    free(fill);
+}
+
+/* src/engine/moe_decoder.cpp:45-60 (mlp_forward: gate, up, silu_mul, down) */
+void orc_mlp(const orc_qmatrix* gate, const orc_qmatrix* up, const orc_qmatrix* down,
+             const float* x, float* out, int m) {
+    const int inter = gate->rows;
+    float* g = (float*)malloc(sizeof(float) * (size_t)m * inter);
+    float* u = (float*)malloc(sizeof(float) * (size_t)m * inter);
+    float* a = (float*)malloc(sizeof(float) * (size_t)m * inter);
+    orc_matmul_int4(gate, x, g, m);
+    orc_matmul_int4(up, x, u, m);
+    orc_silu_mul(g, u, a, (long long)m * inter);
+    orc_matmul_int4(down, a, out, m);
+    free(g);
+    free(u);
+    free(a);
+}
+
+/* src/engine/moe_decoder.cpp:62-74 */
+void orc_routed_expert(const orc_layer* L, const float* x, float* out, int e) {
+    orc_mlp(&L->gate[e], &L->up[e], &L->down[e], x, out, 1);
+}
+
+/* One token of src/engine/moe_decoder.cpp:76-113 (+ residual, :166-179). */
+static void layer_token(const orc_layer* L, const float* x, const float* h, const int* ids,
+                        const float* w, float* out_row) {
+    const int H = L->hidden;
+    float* acc = (float*)malloc(sizeof(float) * H);
+    float* moe = (float*)calloc((size_t)H, sizeof(float));
+    float* sh = (float*)malloc(sizeof(float) * H);
+    for (int j = 0; j < L->top_k; ++j) {
+        orc_routed_expert(L, x, acc, ids[j]);
+        for (int d = 0; d < H; ++d) moe[d] = fmaf(w[j], acc[d], moe[d]);
+    }
+    orc_mlp(&L->shared_gate, &L->shared_up, &L->shared_down, x, sh, 1);
+    for (int d = 0; d < H; ++d) moe[d] += sh[d];
+    if (h)
+        for (int d = 0; d < H; ++d) out_row[d] = h[d] + moe[d];
+    else
+        memcpy(out_row, moe, sizeof(float) * H);
+    free(acc);
+    free(moe);
+    free(sh);
+}
+
+void orc_moe_layer(const orc_layer* L, const float* h, int seq, const int* sel, int n_sel,
+                   int threads, int* ids, float* weights, float* out) {
+    const int H = L->hidden;
+    const float* x = h;
+    float* xn = NULL;
+    if (L->rms_weight) {
+        xn = (float*)malloc(sizeof(float) * (size_t)seq * H);
+        orc_rmsnorm(h, L->rms_weight, xn, seq, H, L->rms_eps);
+        x = xn;
+    }
+    orc_moe_gate(x, L->router_bf16, seq, H, L->n_experts, L->top_k, L->norm_topk_prob,
+                 L->routed_scaling_factor, L->scoring_sigmoid, ids, weights);
+    const int n = sel ? n_sel : seq;
+    (void)threads;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1)
+    for (int i = 0; i < n; ++i) {
+        const int t = sel ? sel[i] : i;
+        layer_token(L, x + (size_t)t * H, L->rms_weight ? h + (size_t)t * H : NULL,
+                    ids + (size_t)t * L->top_k, weights + (size_t)t * L->top_k,
+                    out + (size_t)t * H);
+    }
+    free(xn);
+}

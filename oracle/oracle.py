@@ -1,0 +1,204 @@
+"""ctypes wrapper of the CPU oracle (liboracle.so) and of oracle/_ref.
+
+TEST INFRASTRUCTURE: only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg import this module, as the checker or the timed CPU
+baseline. The product path (libuocr_hip) never touches it.
+"""
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "liboracle.so")
+REF_LIB = os.path.join(HERE, "_ref", "libuocr_ref.so")
+_lib = None
+_ref = None
+
+f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+
+
+class QMatC(C.Structure):
+    _fields_ = [("packed", C.c_void_p), ("scales", C.c_void_p), ("zeros", C.c_void_p),
+                ("rows", C.c_int), ("cols", C.c_int), ("group_size", C.c_int)]
+
+
+class LayerC(C.Structure):
+    _fields_ = [("hidden", C.c_int), ("inter", C.c_int), ("shared_inter", C.c_int),
+                ("n_experts", C.c_int), ("top_k", C.c_int), ("norm_topk_prob", C.c_int),
+                ("routed_scaling_factor", C.c_float), ("scoring_sigmoid", C.c_int),
+                ("router_bf16", C.c_void_p), ("gate", C.POINTER(QMatC)), ("up", C.POINTER(QMatC)),
+                ("down", C.POINTER(QMatC)), ("shared_gate", QMatC), ("shared_up", QMatC),
+                ("shared_down", QMatC), ("rms_weight", C.c_void_p), ("rms_eps", C.c_float)]
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            build()
+        L = C.CDLL(LIB)
+        L.orc_bf16_to_f32.restype = C.c_float
+        L.orc_bf16_to_f32.argtypes = [C.c_uint16]
+        L.orc_f32_to_bf16.restype = C.c_uint16
+        L.orc_f32_to_bf16.argtypes = [C.c_float]
+        L.orc_qmatrix_at.restype = C.c_float
+        L.orc_qmatrix_at.argtypes = [C.POINTER(QMatC), C.c_int, C.c_int]
+        L.orc_dequantize.argtypes = [C.POINTER(QMatC), f32p]
+        for q in ("orc_quantize_int4_awq", "orc_quantize_int4_symmetric"):
+            getattr(L, q).argtypes = [f32p, C.c_int, C.c_int, C.c_int, u8p, f32p, f32p]
+        L.orc_matmul_int4.argtypes = [C.POINTER(QMatC), f32p, f32p, C.c_int]
+        L.orc_matmul_t.argtypes = [f32p, f32p, C.c_void_p, f32p, C.c_int, C.c_int, C.c_int]
+        L.orc_matmul_t_bf16.argtypes = [f32p, u16p, C.c_void_p, f32p, C.c_int, C.c_int, C.c_int]
+        L.orc_softmax.argtypes = [f32p, C.c_int, C.c_int]
+        L.orc_silu_mul.argtypes = [f32p, f32p, f32p, C.c_longlong]
+        L.orc_rmsnorm.argtypes = [f32p, f32p, f32p, C.c_int, C.c_int, C.c_float]
+        L.orc_moe_gate.argtypes = [f32p, u16p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                   C.c_float, C.c_int, i32p, f32p]
+        L.orc_moe_gate_f32router.argtypes = [f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int,
+                                             C.c_int, C.c_float, C.c_int, i32p, f32p]
+        L.orc_stable_group.argtypes = [i32p, C.c_int, C.c_int, C.c_int, i32p, i32p, i32p, C.c_void_p]
+        L.orc_moe_layer.argtypes = [C.POINTER(LayerC), f32p, C.c_int, C.c_void_p, C.c_int, C.c_int,
+                                    i32p, f32p, f32p]
+        _lib = L
+    return _lib
+
+
+def ref():
+    """oracle/_ref/libuocr_ref.so (the reference's own quant.cpp + cpu_ops.cpp), or None."""
+    global _ref
+    if _ref is None and os.path.exists(REF_LIB):
+        R = C.CDLL(REF_LIB)
+        R.ref_dequantize.argtypes = [u8p, f32p, f32p, C.c_int, C.c_int, C.c_int, f32p]
+        R.ref_qat.restype = C.c_float
+        R.ref_qat.argtypes = [u8p, f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]
+        for q in ("ref_quantize_awq", "ref_quantize_symmetric"):
+            getattr(R, q).argtypes = [f32p, C.c_int, C.c_int, C.c_int, u8p, f32p, f32p]
+        R.ref_matmul_t.argtypes = [f32p, f32p, C.c_void_p, f32p, C.c_int, C.c_int, C.c_int]
+        R.ref_matmul_t_bf16.argtypes = [f32p, u16p, C.c_void_p, f32p, C.c_int, C.c_int, C.c_int]
+        R.ref_softmax.argtypes = [f32p, C.c_int, C.c_int]
+        R.ref_silu_mul.argtypes = [f32p, f32p, f32p, C.c_longlong]
+        R.ref_rmsnorm.argtypes = [f32p, f32p, f32p, C.c_int, C.c_int, C.c_float]
+        R.ref_f32_to_bf16.restype = C.c_uint16
+        R.ref_f32_to_bf16.argtypes = [C.c_float]
+        R.ref_bf16_to_f32.restype = C.c_float
+        R.ref_bf16_to_f32.argtypes = [C.c_uint16]
+        _ref = R
+    return _ref
+
+
+def _qc(q, keep):
+    p = np.ascontiguousarray(q.packed, np.uint8)
+    s = np.ascontiguousarray(q.scales, np.float32)
+    z = np.ascontiguousarray(q.zeros, np.float32)
+    keep += [p, s, z]
+    return QMatC(p.ctypes.data, s.ctypes.data, z.ctypes.data, q.rows, q.cols, q.group)
+
+
+def qmat_c(q):
+    keep = []
+    return _qc(q, keep), keep
+
+
+def dequantize(q):
+    qc, keep = qmat_c(q)
+    out = np.empty((q.rows, q.cols), np.float32)
+    lib().orc_dequantize(C.byref(qc), out)
+    return out
+
+
+def matmul_int4(q, x):
+    x = np.ascontiguousarray(x, np.float32)
+    m = x.shape[0]
+    qc, keep = qmat_c(q)
+    y = np.empty((m, q.rows), np.float32)
+    lib().orc_matmul_int4(C.byref(qc), x, y, m)
+    return y
+
+
+def moe_gate(x, router_bf16, top_k, norm=0, scaling=1.0, sigmoid=0):
+    x = np.ascontiguousarray(x, np.float32)
+    rows, hidden = x.shape
+    E = router_bf16.shape[0]
+    ids = np.empty((rows, top_k), np.int32)
+    w = np.empty((rows, top_k), np.float32)
+    lib().orc_moe_gate(x, np.ascontiguousarray(router_bf16, np.uint16), rows, hidden, E, top_k,
+                       int(norm), float(scaling), int(sigmoid), ids, w)
+    return ids, w
+
+
+def moe_gate_f32router(x, router, top_k, norm=0, scaling=1.0, sigmoid=0):
+    x = np.ascontiguousarray(x, np.float32)
+    rows, hidden = x.shape
+    E = router.shape[0]
+    ids = np.empty((rows, top_k), np.int32)
+    w = np.empty((rows, top_k), np.float32)
+    lib().orc_moe_gate_f32router(x, np.ascontiguousarray(router, np.float32), rows, hidden, E,
+                                 top_k, int(norm), float(scaling), int(sigmoid), ids, w)
+    return ids, w
+
+
+def stable_group(ids, n_experts):
+    ids = np.ascontiguousarray(ids, np.int32)
+    seq, k = ids.shape
+    counts = np.empty(n_experts, np.int32)
+    offs = np.empty(n_experts + 1, np.int32)
+    perm = np.empty(seq * k, np.int32)
+    lib().orc_stable_group(ids, seq, k, n_experts, counts, offs, perm, None)
+    return counts, offs, perm
+
+
+def rmsnorm(x, w, eps):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    lib().orc_rmsnorm(x, np.ascontiguousarray(w, np.float32), out, x.shape[0], x.shape[1], eps)
+    return out
+
+
+def layer_c(L):
+    """orc_layer view of a synth.Layer (and the arrays it points into)."""
+    keep = []
+    E = L.n_experts
+    gate = (QMatC * E)(*[_qc(q, keep) for q in L.gate])
+    up = (QMatC * E)(*[_qc(q, keep) for q in L.up])
+    down = (QMatC * E)(*[_qc(q, keep) for q in L.down])
+    keep += [gate, up, down]
+    empty = QMatC(None, None, None, 0, 0, 1)
+    sg = _qc(L.shared_gate, keep) if L.n_shared else empty
+    su = _qc(L.shared_up, keep) if L.n_shared else empty
+    sd = _qc(L.shared_down, keep) if L.n_shared else empty
+    router = np.ascontiguousarray(L.router_bf16, np.uint16)
+    keep.append(router)
+    rms = None
+    if L.rms_weight is not None:
+        rms = np.ascontiguousarray(L.rms_weight, np.float32)
+        keep.append(rms)
+    lc = LayerC(L.hidden, L.inter, L.n_shared * L.inter, E, L.top_k, L.norm_topk_prob,
+                L.routed_scaling_factor, L.scoring_sigmoid, router.ctypes.data, gate, up, down,
+                sg, su, sd, rms.ctypes.data if rms is not None else None, L.rms_eps)
+    return lc, keep
+
+
+def moe_layer(L, h, sel=None, threads=1):
+    """Reference CPU layer: routing for all rows, outputs for rows in `sel`
+    (all rows when None). Returns ids, weights, out (unselected rows = NaN)."""
+    h = np.ascontiguousarray(h, np.float32)
+    seq = h.shape[0]
+    lc, keep = layer_c(L)
+    ids = np.empty((seq, L.top_k), np.int32)
+    w = np.empty((seq, L.top_k), np.float32)
+    out = np.full((seq, L.hidden), np.nan, np.float32)
+    if sel is None:
+        lib().orc_moe_layer(C.byref(lc), h, seq, None, 0, threads, ids, w, out)
+    else:
+        s = np.ascontiguousarray(sel, np.int32)
+        lib().orc_moe_layer(C.byref(lc), h, seq, s.ctypes.data, len(s), threads, ids, w, out)
+    return ids, w, out

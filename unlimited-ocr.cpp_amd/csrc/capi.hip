@@ -1,0 +1,547 @@
+// C ABI of libuocr_hip: layer upload/repack, workspace planning and the fused
+// forward (the counterpart of GpuDecoder::mlp_block's MoE branch,
+// src/engine/gpu_decoder.cu:537-657, in the reference).
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "launch.hpp"
+#include "uocr_hip/moe_capi.h"
+
+extern "C" {
+extern const uint32_t uocr_expf_fix_entries[];
+extern const uint32_t uocr_expf_fix_count;
+extern const uint32_t uocr_expf_fix_offsets[65537];
+}
+
+using namespace uocr_hip;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(UOCR_HIP_EHIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                         \
+    do {                                            \
+        hipError_t _e = (expr);                     \
+        if (_e != hipSuccess) return hip_fail(_e, what); \
+    } while (0)
+
+struct FixTables {
+    uint32_t* offsets = nullptr;
+    uint32_t* entries = nullptr;
+};
+
+std::mutex g_fix_mu;
+std::map<int, FixTables> g_fix;
+
+// Device copy of the expf fix-up table, once per device.
+int fix_tables(FixTables* out) {
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
+    std::lock_guard<std::mutex> lk(g_fix_mu);
+    auto it = g_fix.find(dev);
+    if (it != g_fix.end()) {
+        *out = it->second;
+        return UOCR_HIP_OK;
+    }
+    FixTables t;
+    const size_t ob = sizeof(uint32_t) * 65537, eb = sizeof(uint32_t) * (uocr_expf_fix_count + 1);
+    HIP_TRY(hipMalloc(&t.offsets, ob), "hipMalloc(expf fix offsets)");
+    HIP_TRY(hipMalloc(&t.entries, eb), "hipMalloc(expf fix entries)");
+    HIP_TRY(hipMemcpy(t.offsets, uocr_expf_fix_offsets, ob, hipMemcpyHostToDevice), "copy fix offsets");
+    HIP_TRY(hipMemcpy(t.entries, uocr_expf_fix_entries, eb, hipMemcpyHostToDevice), "copy fix entries");
+    g_fix[dev] = t;
+    *out = t;
+    return UOCR_HIP_OK;
+}
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+uint16_t f32_to_bf16_rne(float f) {
+    uint32_t b;
+    std::memcpy(&b, &f, 4);
+    b = (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
+    return (uint16_t)b;
+}
+
+// Repack rows [row0, row0 + R) x columns [col0, col0 + K) of a reference-layout
+// INT4 matrix into the tile-16x128 device layout (common.hpp).
+int repack(const uocr_hip_qmatrix& q, int row0, int R, int col0, int K, uint8_t* dst,
+           uint16_t* dsts, std::string* err) {
+    const int G = q.group_size, gpt = kTileK / G, KT = K / kTileK, RB = R / kTileRows;
+    const int pr = (q.cols + 1) / 2, ng = (q.cols + G - 1) / G;
+    for (int rb = 0; rb < RB; ++rb)
+        for (int kt = 0; kt < KT; ++kt) {
+            uint8_t* tile = dst + ((size_t)rb * KT + kt) * kTileBytes;
+            for (int lane = 0; lane < 64; ++lane) {
+                const int r = row0 + rb * kTileRows + (lane & 15);
+                const uint8_t* prow = q.packed + (size_t)r * pr;
+                for (int s = 0; s < 4; ++s) {
+                    uint32_t w = 0;
+                    for (int i = 0; i < 8; ++i) {
+                        const int c = col0 + kt * kTileK + s * 32 + 8 * (lane >> 4) + i;
+                        const uint8_t byte = prow[c >> 1];
+                        const uint32_t nib = (c & 1) ? (byte >> 4) : (byte & 0x0f);
+                        w |= nib << ((i & 1) * 16 + (i >> 1) * 4);
+                    }
+                    std::memcpy(tile + lane * 16 + s * 4, &w, 4);
+                }
+            }
+            for (int rr = 0; rr < kTileRows; ++rr) {
+                const int r = row0 + rb * kTileRows + rr;
+                for (int gi = 0; gi < gpt; ++gi) {
+                    const int g = (col0 + kt * kTileK) / G + gi;
+                    const size_t idx = (size_t)r * ng + g;
+                    const float z = q.zeros[idx], s = q.scales[idx];
+                    if (z != 8.0f) {
+                        *err = "zero point " + std::to_string(z) + " at row " + std::to_string(r) +
+                               " group " + std::to_string(g) +
+                               ": only the symmetric layout (zeros == 8) is supported";
+                        return UOCR_HIP_EUNSUPPORTED;
+                    }
+                    if (!std::isfinite(s) || std::fabs(s) * 8.0f > 65504.0f) {
+                        *err = "scale outside the f16 range at row " + std::to_string(r);
+                        return UOCR_HIP_EUNSUPPORTED;
+                    }
+                    dsts[(((size_t)rb * KT + kt) * kTileRows + rr) * gpt + gi] = f32_to_bf16_rne(s);
+                }
+            }
+        }
+    return UOCR_HIP_OK;
+}
+
+}  // namespace
+
+struct uocr_hip_moe_layer {
+    int hidden = 0, inter = 0, n_experts = 0, top_k = 0, n_virtual = 0, group = 0;
+    int norm_topk_prob = 0, scoring_sigmoid = 0;
+    float scaling = 1.0f, rms_eps = 1e-6f;
+    int device = 0;
+    uint16_t* router_t = nullptr;
+    float* rms_weight = nullptr;
+    uint8_t* gate = nullptr;   // [Ev][inter x hidden] tile layout
+    uint8_t* up = nullptr;
+    uint8_t* down = nullptr;   // [Ev][hidden x inter]
+    uint16_t* gate_s = nullptr;
+    uint16_t* up_s = nullptr;
+    uint16_t* down_s = nullptr;
+    long long gu_wstride = 0, gu_sstride = 0, dn_wstride = 0, dn_sstride = 0;
+    size_t device_bytes = 0;
+    FixTables fix;
+    bool timing = false;
+    hipEvent_t ev[6] = {};
+    float stage_ms[5] = {};
+    int timed_calls = 0;
+    bool pending = false;
+};
+
+namespace {
+
+void free_layer(uocr_hip_moe_layer* L) {
+    if (!L) return;
+    void* ptrs[] = {L->router_t, L->rms_weight, L->gate, L->up, L->down, L->gate_s, L->up_s, L->down_s};
+    for (void* p : ptrs)
+        if (p) (void)hipFree(p);
+    for (auto& e : L->ev)
+        if (e) (void)hipEventDestroy(e);
+    delete L;
+}
+
+int check_qm(const uocr_hip_qmatrix* q, int rows, int cols, int group, const char* what) {
+    if (!q || !q->packed || !q->scales || !q->zeros)
+        return fail(UOCR_HIP_EINVAL, std::string(what) + ": null matrix pointer");
+    if (q->rows != rows || q->cols != cols)
+        return fail(UOCR_HIP_EINVAL, std::string(what) + ": shape " + std::to_string(q->rows) + "x" +
+                                         std::to_string(q->cols) + ", expected " + std::to_string(rows) +
+                                         "x" + std::to_string(cols));
+    if (q->group_size != group)
+        return fail(UOCR_HIP_EINVAL, std::string(what) + ": mixed group sizes in one layer");
+    return UOCR_HIP_OK;
+}
+
+struct WsPlan {
+    size_t x16, ids, wts, counts, offsets, ntiles, slot_tok, slot_w, pos, tile_e, tile_m0, act, y, total;
+    int slots, max_tiles, bm;
+};
+
+bool use_prefill(const uocr_hip_moe_layer* L, int seq) {
+    (void)L;
+    (void)seq;
+    return false;
+}
+
+WsPlan plan(const uocr_hip_moe_layer* L, int seq) {
+    WsPlan p{};
+    const int Ev = L->n_experts + L->n_virtual;
+    p.slots = seq * (L->top_k + L->n_virtual);
+    p.bm = use_prefill(L, seq) ? 128 : 64;
+    p.max_tiles = (seq * L->top_k) / p.bm + L->n_experts + L->n_virtual * ((seq + p.bm - 1) / p.bm) + 1;
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = o;
+        o = align_up(o + bytes, 256);
+        return at;
+    };
+    p.x16 = take((size_t)seq * L->hidden * 2);
+    p.ids = take((size_t)seq * L->top_k * 4);
+    p.wts = take((size_t)seq * L->top_k * 4);
+    p.counts = take((size_t)Ev * 4);
+    p.offsets = take((size_t)(Ev + 1) * 4);
+    p.ntiles = take(4);
+    p.slot_tok = take((size_t)p.slots * 4);
+    p.slot_w = take((size_t)p.slots * 4);
+    p.pos = take((size_t)seq * L->top_k * 4);
+    p.tile_e = take((size_t)p.max_tiles * 4);
+    p.tile_m0 = take((size_t)p.max_tiles * 4);
+    p.act = take((size_t)p.slots * L->inter * 2);
+    p.y = take((size_t)p.slots * L->hidden * 4);
+    p.total = o;
+    return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* uocr_hip_last_error(void) { return g_err.c_str(); }
+
+const char* uocr_hip_version(void) { return "uocr_hip 0.1 (gfx950)"; }
+
+int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer** out) {
+    if (!d || !out) return fail(UOCR_HIP_EINVAL, "null argument");
+    *out = nullptr;
+    const int H = d->hidden, I = d->inter, E = d->n_experts;
+    if (H <= 0 || I <= 0 || H % kTileK || I % kTileK)
+        return fail(UOCR_HIP_EINVAL, "hidden and inter must be positive multiples of 128");
+    if (E <= 0 || E > 64) return fail(UOCR_HIP_EINVAL, "n_experts must be in [1, 64]");
+    if (d->top_k <= 0 || d->top_k > kMaxTopK || d->top_k > E)
+        return fail(UOCR_HIP_EINVAL, "top_k must be in [1, min(8, n_experts)]");
+    if (d->n_shared < 0 || E + d->n_shared > kMaxExperts) return fail(UOCR_HIP_EINVAL, "bad n_shared");
+    if (!d->router_bf16 || !d->gate || !d->up || !d->down) return fail(UOCR_HIP_EINVAL, "null weight pointer");
+    const int G = d->gate[0].group_size;
+    if (G != 32 && G != 64 && G != 128) return fail(UOCR_HIP_EUNSUPPORTED, "group_size must be 32, 64 or 128");
+    int rc;
+    for (int e = 0; e < E; ++e) {
+        if ((rc = check_qm(&d->gate[e], I, H, G, "gate"))) return rc;
+        if ((rc = check_qm(&d->up[e], I, H, G, "up"))) return rc;
+        if ((rc = check_qm(&d->down[e], H, I, G, "down"))) return rc;
+    }
+    const int S = d->n_shared;
+    if (S > 0) {
+        if ((rc = check_qm(d->shared_gate, S * I, H, G, "shared_gate"))) return rc;
+        if ((rc = check_qm(d->shared_up, S * I, H, G, "shared_up"))) return rc;
+        if ((rc = check_qm(d->shared_down, H, S * I, G, "shared_down"))) return rc;
+    }
+
+    auto* L = new uocr_hip_moe_layer();
+    L->hidden = H;
+    L->inter = I;
+    L->n_experts = E;
+    L->top_k = d->top_k;
+    L->n_virtual = S;
+    L->group = G;
+    L->norm_topk_prob = d->norm_topk_prob;
+    L->scoring_sigmoid = d->scoring_sigmoid;
+    L->scaling = d->routed_scaling_factor;
+    L->rms_eps = d->rms_eps;
+    if ((rc = fix_tables(&L->fix))) {
+        free_layer(L);
+        return rc;
+    }
+    (void)hipGetDevice(&L->device);
+
+    const int Ev = E + S;
+    L->gu_wstride = (long long)I * H / 2;
+    L->gu_sstride = (long long)I * (H / G);
+    L->dn_wstride = (long long)H * I / 2;
+    L->dn_sstride = (long long)H * (I / G);
+    std::vector<uint8_t> hg((size_t)Ev * L->gu_wstride), hu(hg.size()), hd((size_t)Ev * L->dn_wstride);
+    std::vector<uint16_t> hgs((size_t)Ev * L->gu_sstride), hus(hgs.size()), hds((size_t)Ev * L->dn_sstride);
+
+    // repack experts in parallel (virtual experts E..E+S-1 are slices of the shared MLP)
+    std::vector<int> codes(Ev, UOCR_HIP_OK);
+    std::vector<std::string> errs(Ev);
+    auto work = [&](int e) {
+        std::string* err = &errs[e];
+        int c;
+        if (e < E) {
+            if ((c = repack(d->gate[e], 0, I, 0, H, &hg[e * L->gu_wstride], &hgs[e * L->gu_sstride], err))) goto done;
+            if ((c = repack(d->up[e], 0, I, 0, H, &hu[e * L->gu_wstride], &hus[e * L->gu_sstride], err))) goto done;
+            c = repack(d->down[e], 0, H, 0, I, &hd[e * L->dn_wstride], &hds[e * L->dn_sstride], err);
+        } else {
+            const int v = e - E;
+            if ((c = repack(*d->shared_gate, v * I, I, 0, H, &hg[e * L->gu_wstride], &hgs[e * L->gu_sstride], err))) goto done;
+            if ((c = repack(*d->shared_up, v * I, I, 0, H, &hu[e * L->gu_wstride], &hus[e * L->gu_sstride], err))) goto done;
+            c = repack(*d->shared_down, 0, H, v * I, I, &hd[e * L->dn_wstride], &hds[e * L->dn_sstride], err);
+        }
+    done:
+        codes[e] = c;
+    };
+    {
+        const unsigned nt = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+        std::vector<std::thread> pool;
+        for (unsigned w = 0; w < nt; ++w)
+            pool.emplace_back([&, w] {
+                for (int e = (int)w; e < Ev; e += (int)nt) work(e);
+            });
+        for (auto& th : pool) th.join();
+    }
+    for (int e = 0; e < Ev; ++e)
+        if (codes[e]) {
+            const std::string m = (e < E ? "expert " + std::to_string(e) : "shared expert") + ": " + errs[e];
+            free_layer(L);
+            return fail(codes[e], m);
+        }
+
+    // router W as [H/8][E][8] so lane e's 16-byte loads are coalesced across the wave
+    std::vector<uint16_t> rt((size_t)H * E);
+    for (int c8 = 0; c8 < H / 8; ++c8)
+        for (int e = 0; e < E; ++e)
+            for (int i = 0; i < 8; ++i) rt[((size_t)c8 * E + e) * 8 + i] = d->router_bf16[(size_t)e * H + c8 * 8 + i];
+
+    auto up_copy = [&](void** dst, const void* src, size_t bytes, const char* what) -> int {
+        hipError_t e = hipMalloc(dst, bytes);
+        if (e != hipSuccess) return fail(UOCR_HIP_ENOMEM, std::string("hipMalloc(") + what + "): " + hipGetErrorString(e));
+        e = hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) return hip_fail(e, what);
+        L->device_bytes += bytes;
+        return UOCR_HIP_OK;
+    };
+    if ((rc = up_copy((void**)&L->router_t, rt.data(), rt.size() * 2, "router")) ||
+        (rc = up_copy((void**)&L->gate, hg.data(), hg.size(), "gate")) ||
+        (rc = up_copy((void**)&L->up, hu.data(), hu.size(), "up")) ||
+        (rc = up_copy((void**)&L->down, hd.data(), hd.size(), "down")) ||
+        (rc = up_copy((void**)&L->gate_s, hgs.data(), hgs.size() * 2, "gate scales")) ||
+        (rc = up_copy((void**)&L->up_s, hus.data(), hus.size() * 2, "up scales")) ||
+        (rc = up_copy((void**)&L->down_s, hds.data(), hds.size() * 2, "down scales")) ||
+        (d->rms_weight && (rc = up_copy((void**)&L->rms_weight, d->rms_weight, (size_t)H * 4, "rms weight")))) {
+        free_layer(L);
+        return rc;
+    }
+    *out = L;
+    return UOCR_HIP_OK;
+}
+
+int uocr_hip_moe_layer_destroy(uocr_hip_moe_layer* layer) {
+    free_layer(layer);
+    return UOCR_HIP_OK;
+}
+
+size_t uocr_hip_moe_layer_device_bytes(const uocr_hip_moe_layer* layer) {
+    return layer ? layer->device_bytes : 0;
+}
+
+size_t uocr_hip_moe_layer_workspace_size(const uocr_hip_moe_layer* layer, int seq) {
+    if (!layer || seq <= 0) return 0;
+    return plan(layer, seq).total;
+}
+
+int uocr_hip_moe_layer_path(const uocr_hip_moe_layer* layer, int seq) {
+    return (layer && use_prefill(layer, seq)) ? 1 : 0;
+}
+
+int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x_dtype, int seq,
+                               float* out, int* ids_out, float* weights_out, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+    if (!L || !x || !out) return fail(UOCR_HIP_EINVAL, "null argument");
+    if (seq <= 0) return fail(UOCR_HIP_EINVAL, "seq must be positive");
+    if (x_dtype != UOCR_HIP_DTYPE_BF16 && x_dtype != UOCR_HIP_DTYPE_F32) return fail(UOCR_HIP_EINVAL, "bad x_dtype");
+    if (L->rms_weight && x_dtype != UOCR_HIP_DTYPE_F32)
+        return fail(UOCR_HIP_EINVAL, "a layer with rms_weight adds the residual and needs f32 x");
+    if ((uintptr_t)x % 16 || (uintptr_t)out % 16) return fail(UOCR_HIP_EINVAL, "x and out must be 16-byte aligned");
+    const WsPlan p = plan(L, seq);
+    if (!workspace || workspace_bytes < p.total)
+        return fail(UOCR_HIP_EWORKSPACE, "workspace too small: need " + std::to_string(p.total) + " bytes");
+    if ((uintptr_t)workspace % 256) return fail(UOCR_HIP_EINVAL, "workspace must be 256-byte aligned");
+    hipStream_t st = (hipStream_t)stream;
+    char* ws = (char*)workspace;
+    int* ids = ids_out ? ids_out : (int*)(ws + p.ids);
+    float* wts = weights_out ? weights_out : (float*)(ws + p.wts);
+    f16* x16 = (f16*)(ws + p.x16);
+    auto* Lm = const_cast<uocr_hip_moe_layer*>(L);
+    const bool timing = L->timing;
+    auto mark = [&](int i) {
+        if (timing) (void)hipEventRecord(Lm->ev[i], st);
+    };
+
+    mark(0);
+    RouterArgs ra{};
+    ra.x = x;
+    ra.seq = seq;
+    ra.hidden = L->hidden;
+    ra.n_experts = L->n_experts;
+    ra.top_k = L->top_k;
+    ra.rms_weight = L->rms_weight;
+    ra.rms_eps = L->rms_eps;
+    ra.router_t = L->router_t;
+    ra.norm_topk_prob = L->norm_topk_prob;
+    ra.scoring_sigmoid = L->scoring_sigmoid;
+    ra.scaling = L->scaling;
+    ra.fix_offsets = L->fix.offsets;
+    ra.fix_entries = L->fix.entries;
+    ra.x16 = x16;
+    ra.ids = ids;
+    ra.weights = wts;
+    HIP_TRY(launch_router(ra, x_dtype == UOCR_HIP_DTYPE_BF16, st), "router launch");
+    mark(1);
+
+    GroupArgs g{};
+    g.ids = ids;
+    g.weights = wts;
+    g.seq = seq;
+    g.top_k = L->top_k;
+    g.n_experts = L->n_experts;
+    g.n_virtual = L->n_virtual;
+    g.bm = p.bm;
+    g.counts = (int*)(ws + p.counts);
+    g.offsets = (int*)(ws + p.offsets);
+    g.slot_tok = (int*)(ws + p.slot_tok);
+    g.slot_w = (float*)(ws + p.slot_w);
+    g.pos = (int*)(ws + p.pos);
+    g.tile_e = (int*)(ws + p.tile_e);
+    g.tile_m0 = (int*)(ws + p.tile_m0);
+    g.n_tiles = (int*)(ws + p.ntiles);
+    HIP_TRY(launch_group(g, st), "group launch");
+    mark(2);
+
+    const bool pre = use_prefill(L, seq);
+    ExpertArgs gu{};
+    gu.a = x16;
+    gu.gather = 1;
+    gu.w0 = L->gate;
+    gu.s0 = L->gate_s;
+    gu.w1 = L->up;
+    gu.s1 = L->up_s;
+    gu.w_stride = L->gu_wstride;
+    gu.s_stride = L->gu_sstride;
+    gu.n_rows = L->inter;
+    gu.k = L->hidden;
+    gu.group = L->group;
+    gu.slot_tok = g.slot_tok;
+    gu.counts = g.counts;
+    gu.offsets = g.offsets;
+    gu.tile_e = g.tile_e;
+    gu.tile_m0 = g.tile_m0;
+    gu.n_tiles = g.n_tiles;
+    gu.act_out = (f16*)(ws + p.act);
+    HIP_TRY(pre ? launch_experts_prefill(gu, true, p.max_tiles, st) : launch_experts_decode(gu, true, p.max_tiles, st),
+            "gate/up launch");
+    mark(3);
+
+    ExpertArgs dn = gu;
+    dn.a = gu.act_out;
+    dn.gather = 0;
+    dn.w0 = L->down;
+    dn.s0 = L->down_s;
+    dn.w1 = nullptr;
+    dn.s1 = nullptr;
+    dn.w_stride = L->dn_wstride;
+    dn.s_stride = L->dn_sstride;
+    dn.n_rows = L->hidden;
+    dn.k = L->inter;
+    dn.act_out = nullptr;
+    dn.y_out = (float*)(ws + p.y);
+    HIP_TRY(pre ? launch_experts_prefill(dn, false, p.max_tiles, st) : launch_experts_decode(dn, false, p.max_tiles, st),
+            "down launch");
+    mark(4);
+
+    CombineArgs c{};
+    c.y = dn.y_out;
+    c.pos = g.pos;
+    c.weights = wts;
+    c.offsets = g.offsets;
+    c.residual = L->rms_weight ? (const float*)x : nullptr;
+    c.out = out;
+    c.seq = seq;
+    c.hidden = L->hidden;
+    c.top_k = L->top_k;
+    c.n_experts = L->n_experts;
+    c.n_virtual = L->n_virtual;
+    HIP_TRY(launch_combine(c, st), "combine launch");
+    mark(5);
+    if (timing) Lm->pending = true;
+    return UOCR_HIP_OK;
+}
+
+int uocr_hip_moe_layer_set_timing(uocr_hip_moe_layer* L, int enable) {
+    if (!L) return fail(UOCR_HIP_EINVAL, "null layer");
+    if (enable && !L->ev[0])
+        for (auto& e : L->ev) HIP_TRY(hipEventCreate(&e), "hipEventCreate");
+    L->timing = enable != 0;
+    return UOCR_HIP_OK;
+}
+
+int uocr_hip_moe_layer_read_timing(uocr_hip_moe_layer* L, float* stage_ms, int n_stages, int* n_calls) {
+    if (!L || !stage_ms) return fail(UOCR_HIP_EINVAL, "null argument");
+    if (L->pending) {
+        HIP_TRY(hipEventSynchronize(L->ev[5]), "hipEventSynchronize");
+        for (int i = 0; i < 5; ++i) {
+            float ms = 0.0f;
+            HIP_TRY(hipEventElapsedTime(&ms, L->ev[i], L->ev[i + 1]), "hipEventElapsedTime");
+            L->stage_ms[i] += ms;
+        }
+        L->timed_calls++;
+        L->pending = false;
+    }
+    for (int i = 0; i < n_stages && i < 5; ++i) stage_ms[i] = L->stage_ms[i];
+    if (n_calls) *n_calls = L->timed_calls;
+    std::memset(L->stage_ms, 0, sizeof(L->stage_ms));
+    L->timed_calls = 0;
+    return UOCR_HIP_OK;
+}
+
+int uocr_hip_moe_router_topk(const float* logits, int seq, int n_experts, int top_k, int norm_topk_prob,
+                             float scaling, int scoring_sigmoid, int* d_ids, float* d_weights,
+                             int* d_assign_token, float* d_assign_w, int* d_count, int cap, void* stream) {
+    if (seq == 0 || n_experts == 0) return UOCR_HIP_OK;  // reference: early return (moe_device.cu:275)
+    if (!logits || !d_ids || !d_weights || !d_assign_token || !d_assign_w || !d_count)
+        return fail(UOCR_HIP_EINVAL, "null argument");
+    if (seq < 0 || n_experts < 0 || n_experts > kMaxExperts || top_k <= 0 || top_k > kMaxTopK || top_k > n_experts ||
+        cap <= 0)
+        return fail(UOCR_HIP_EINVAL, "bad shape (n_experts <= 128, 1 <= top_k <= min(8, n_experts), cap > 0)");
+    FixTables ft;
+    int rc;
+    if ((rc = fix_tables(&ft))) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    RouterArgs ra{};
+    ra.seq = seq;
+    ra.n_experts = n_experts;
+    ra.top_k = top_k;
+    ra.norm_topk_prob = norm_topk_prob;
+    ra.scoring_sigmoid = scoring_sigmoid;
+    ra.scaling = scaling;
+    ra.fix_offsets = ft.offsets;
+    ra.fix_entries = ft.entries;
+    ra.ids = d_ids;
+    ra.weights = d_weights;
+    HIP_TRY(launch_router_from_logits(ra, logits, st), "router launch");
+    GroupArgs g{};
+    g.ids = d_ids;
+    g.weights = d_weights;
+    g.seq = seq;
+    g.top_k = top_k;
+    g.n_experts = n_experts;
+    g.bm = 1;
+    g.assign_token = d_assign_token;
+    g.assign_w = d_assign_w;
+    g.assign_count = d_count;
+    g.cap = cap;
+    HIP_TRY(launch_group(g, st), "group launch");
+    return UOCR_HIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,87 @@
+// Kernel argument blocks and host-side launchers (internal to libuocr_hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.hpp"
+
+namespace uocr_hip {
+
+constexpr int kMaxExperts = 128;  // routed + virtual (shared-expert) groups
+constexpr int kMaxTopK = 8;
+
+struct RouterArgs {
+    const void* x;            // [seq, hidden] bf16 bits or f32
+    int seq, hidden, n_experts, top_k;
+    const float* rms_weight;  // optional [hidden]
+    float rms_eps;
+    const uint16_t* router_t; // router W as [hidden/8][n_experts][8] bf16
+    int norm_topk_prob, scoring_sigmoid;
+    float scaling;
+    const uint32_t* fix_offsets;
+    const uint32_t* fix_entries;
+    f16* x16;                 // out [seq, hidden] f16 expert input
+    int* ids;                 // out [seq, top_k]
+    float* weights;           // out [seq, top_k]
+};
+
+struct GroupArgs {
+    const int* ids;
+    const float* weights;
+    int seq, top_k, n_experts, n_virtual, bm;
+    // grouped-slot outputs (fused layer path); any may be null
+    int* counts;     // [n_experts + n_virtual]
+    int* offsets;    // [n_experts + n_virtual + 1]
+    int* slot_tok;   // [slots]
+    float* slot_w;   // [slots]
+    int* pos;        // [seq * top_k] slot of entry (t, j)
+    int* tile_e;     // [max tiles]
+    int* tile_m0;    // [max tiles]
+    int* n_tiles;    // [1]
+    // reference [n_experts, cap] assignment tables (moe_router_topk mirror)
+    int* assign_token;
+    float* assign_w;
+    int* assign_count;
+    int cap;
+};
+
+// Grouped INT4 expert GEMM over the tile-16x128 device layout.
+struct ExpertArgs {
+    const f16* a;            // activations: x16 [seq, K] (gathered via slot_tok) or act [slots, K]
+    int gather;              // 1: row = slot_tok[slot], 0: row = slot
+    const uint8_t* w0;       // packed weights, per expert stride w_stride bytes (gate or down)
+    const uint16_t* s0;      // bf16 scales, per expert stride s_stride elements
+    const uint8_t* w1;       // second matrix (up) for the fused gate/up pass, else null
+    const uint16_t* s1;
+    long long w_stride, s_stride;
+    int n_rows;              // output features (N)
+    int k;                   // input features (K)
+    int group;
+    const int* slot_tok;
+    const int* counts;
+    const int* offsets;
+    const int* tile_e;
+    const int* tile_m0;
+    const int* n_tiles;
+    f16* act_out;            // gate/up: [slots, n_rows] f16
+    float* y_out;            // down: [slots, n_rows] f32
+};
+
+struct CombineArgs {
+    const float* y;        // [slots, hidden]
+    const int* pos;        // [seq, top_k]
+    const float* weights;  // [seq, top_k]
+    const int* offsets;    // virtual groups start at offsets[n_experts + v]
+    const float* residual; // optional [seq, hidden]
+    float* out;            // [seq, hidden]
+    int seq, hidden, top_k, n_experts, n_virtual;
+};
+
+hipError_t launch_router(const RouterArgs& a, bool x_is_bf16, hipStream_t st);
+hipError_t launch_router_from_logits(const RouterArgs& a, const float* logits, hipStream_t st);
+hipError_t launch_group(const GroupArgs& g, hipStream_t st);
+hipError_t launch_experts_decode(const ExpertArgs& a, bool gate_up, int max_tiles, hipStream_t st);
+hipError_t launch_experts_prefill(const ExpertArgs& a, bool gate_up, int max_tiles, hipStream_t st);
+hipError_t launch_combine(const CombineArgs& c, hipStream_t st);
+
+}  // namespace uocr_hip

@@ -1,0 +1,91 @@
+"""ctypes loader and signatures for libuocr_hip.so."""
+import ctypes as C
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libuocr_hip.so")
+_lib = None
+
+OK = 0
+EINVAL = -1
+EUNSUPPORTED = -2
+ENOMEM = -3
+EWORKSPACE = -4
+EHIP = -5
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
+
+class HipError(RuntimeError):
+    """A libuocr_hip entry point returned a non-zero status."""
+
+    def __init__(self, code, msg):
+        super().__init__(f"libuocr_hip error {code}: {msg}")
+        self.code = code
+
+
+class QMatrixC(C.Structure):
+    """uocr_hip_qmatrix (mirrors uocr::QuantizedMatrix, include/uocr/quant.h:16-32)."""
+
+    _fields_ = [("packed", C.c_void_p), ("scales", C.c_void_p), ("zeros", C.c_void_p),
+                ("rows", C.c_int), ("cols", C.c_int), ("group_size", C.c_int)]
+
+
+class LayerDescC(C.Structure):
+    _fields_ = [("hidden", C.c_int), ("inter", C.c_int), ("n_experts", C.c_int),
+                ("top_k", C.c_int), ("n_shared", C.c_int), ("norm_topk_prob", C.c_int),
+                ("routed_scaling_factor", C.c_float), ("scoring_sigmoid", C.c_int),
+                ("router_bf16", C.c_void_p), ("gate", C.POINTER(QMatrixC)),
+                ("up", C.POINTER(QMatrixC)), ("down", C.POINTER(QMatrixC)),
+                ("shared_gate", C.POINTER(QMatrixC)), ("shared_up", C.POINTER(QMatrixC)),
+                ("shared_down", C.POINTER(QMatrixC)), ("rms_weight", C.c_void_p),
+                ("rms_eps", C.c_float)]
+
+
+def lib_path():
+    return _LIB_PATH
+
+
+# name -> (restype, argtypes); every entry is declared in include/uocr_hip/moe_capi.h
+SIGNATURES = {
+    "uocr_hip_last_error": (C.c_char_p, []),
+    "uocr_hip_version": (C.c_char_p, []),
+    "uocr_hip_moe_layer_create": (C.c_int, [C.POINTER(LayerDescC), C.POINTER(C.c_void_p)]),
+    "uocr_hip_moe_layer_destroy": (C.c_int, [C.c_void_p]),
+    "uocr_hip_moe_layer_device_bytes": (C.c_size_t, [C.c_void_p]),
+    "uocr_hip_moe_layer_workspace_size": (C.c_size_t, [C.c_void_p, C.c_int]),
+    "uocr_hip_moe_layer_path": (C.c_int, [C.c_void_p, C.c_int]),
+    "uocr_hip_moe_layer_forward": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
+                                              C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
+                                              C.c_void_p]),
+    "uocr_hip_moe_layer_set_timing": (C.c_int, [C.c_void_p, C.c_int]),
+    "uocr_hip_moe_layer_read_timing": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int,
+                                                  C.POINTER(C.c_int)]),
+    "uocr_hip_moe_router_topk": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int,
+                                            C.c_float, C.c_int, C.c_void_p, C.c_void_p,
+                                            C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
+                                            C.c_void_p]),
+}
+
+
+def load():
+    """Load libuocr_hip.so (built by __graft_entry__.build()); raise if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(_LIB_PATH):
+        raise FileNotFoundError(
+            f"{_LIB_PATH} is missing: build it first (python -c 'import __graft_entry__ as g; g.build()')")
+    lib = C.CDLL(_LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(rc):
+    if rc != OK:
+        raise HipError(rc, load().uocr_hip_last_error().decode())
+    return rc

@@ -1,0 +1,111 @@
+"""MoELayerInt4: a device-resident INT4 MoE layer behind the C ABI."""
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+from ._lib import DTYPE_BF16, DTYPE_F32, LayerDescC, QMatrixC, check, load
+
+STAGES = ("router", "group", "gate_up", "down", "combine")
+
+
+class QMatrix:
+    """Keeps a reference-layout INT4 matrix alive and exposes its C view."""
+
+    def __init__(self, qm):
+        self.packed = np.ascontiguousarray(qm.packed, np.uint8)
+        self.scales = np.ascontiguousarray(qm.scales, np.float32)
+        self.zeros = np.ascontiguousarray(qm.zeros, np.float32)
+        self.c = QMatrixC(self.packed.ctypes.data, self.scales.ctypes.data, self.zeros.ctypes.data,
+                          qm.rows, qm.cols, qm.group)
+
+
+def _qarray(qms):
+    keep = [QMatrix(q) for q in qms]
+    arr = (QMatrixC * len(keep))(*[k.c for k in keep])
+    return arr, keep
+
+
+class MoELayerInt4:
+    """Uploads a `synth.Layer`-like object (reference host layout) once, then runs
+    `forward` on torch device tensors through uocr_hip_moe_layer_forward."""
+
+    def __init__(self, L):
+        lib = load()
+        self.lib = lib
+        keep = []
+        gate, k1 = _qarray(L.gate)
+        up, k2 = _qarray(L.up)
+        down, k3 = _qarray(L.down)
+        keep += [gate, up, down, k1, k2, k3]
+        sg = su = sd = None
+        if L.n_shared:
+            sg, k4 = _qarray([L.shared_gate])
+            su, k5 = _qarray([L.shared_up])
+            sd, k6 = _qarray([L.shared_down])
+            keep += [sg, su, sd, k4, k5, k6]
+        router = np.ascontiguousarray(L.router_bf16, np.uint16)
+        keep.append(router)
+        rms = None
+        if L.rms_weight is not None:
+            rms = np.ascontiguousarray(L.rms_weight, np.float32)
+            keep.append(rms)
+        d = LayerDescC(L.hidden, L.inter, L.n_experts, L.top_k, L.n_shared, L.norm_topk_prob,
+                       L.routed_scaling_factor, L.scoring_sigmoid, router.ctypes.data,
+                       gate, up, down, sg, su, sd, rms.ctypes.data if rms is not None else None,
+                       L.rms_eps)
+        h = C.c_void_p()
+        check(lib.uocr_hip_moe_layer_create(C.byref(d), C.byref(h)))
+        self.handle = h
+        self.hidden, self.top_k, self.has_rms = L.hidden, L.top_k, L.rms_weight is not None
+        del keep  # host copies are no longer needed once uploaded
+
+    def close(self):
+        if self.handle:
+            self.lib.uocr_hip_moe_layer_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def device_bytes(self):
+        return self.lib.uocr_hip_moe_layer_device_bytes(self.handle)
+
+    def workspace_size(self, seq):
+        return self.lib.uocr_hip_moe_layer_workspace_size(self.handle, seq)
+
+    def path(self, seq):
+        return "prefill" if self.lib.uocr_hip_moe_layer_path(self.handle, seq) else "decode"
+
+    def alloc_workspace(self, seq, device="cuda"):
+        import torch
+        n = self.workspace_size(seq)
+        return torch.empty(n + 256, dtype=torch.uint8, device=device)
+
+    def forward(self, x, out, workspace, ids=None, weights=None, stream=None):
+        """x: torch [seq, hidden] bf16 or f32 (cuda); out: torch f32 [seq, hidden]."""
+        import torch
+        seq = x.shape[0]
+        dt = DTYPE_BF16 if x.dtype == torch.bfloat16 else DTYPE_F32
+        if x.dtype not in (torch.bfloat16, torch.float32):
+            raise TypeError("x must be bf16 or f32")
+        ws_ptr = (workspace.data_ptr() + 255) // 256 * 256
+        ws_bytes = workspace.numel() - (ws_ptr - workspace.data_ptr())
+        st = stream if stream is not None else torch.cuda.current_stream().cuda_stream
+        check(self.lib.uocr_hip_moe_layer_forward(
+            self.handle, x.data_ptr(), dt, seq, out.data_ptr(),
+            ids.data_ptr() if ids is not None else None,
+            weights.data_ptr() if weights is not None else None,
+            ws_ptr, ws_bytes, st))
+
+    def set_timing(self, enable):
+        check(self.lib.uocr_hip_moe_layer_set_timing(self.handle, 1 if enable else 0))
+
+    def read_timing(self):
+        ms = (C.c_float * 5)()
+        n = C.c_int()
+        check(self.lib.uocr_hip_moe_layer_read_timing(self.handle, ms, 5, C.byref(n)))
+        return dict(zip(STAGES, list(ms))), n.value
