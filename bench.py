@@ -1,0 +1,239 @@
+"""Benchmark: one Unlimited-OCR INT4 MoE layer on one MI355X.
+
+Headline (`value`): BASELINE config 1 -- batched decode, 16 tokens, one INT4
+g32 MoE layer (router + top-6 of 64 + 2 shared experts + combine) -- as
+tokens/s with inputs and weights resident in HBM. Each timed step runs the layer
+on the next of R distinct weight replicas, so the ~128 MB layer is streamed
+from HBM rather than from the 256 MB Infinity Cache.
+
+Roofline: the dominant kernel is the fused gate/up expert pass. Its average
+duration comes from HIP events that libuocr_hip records around that launch on
+the layer's stream (uocr_hip_moe_layer_set_timing) over the same steps;
+achieved = algorithmic bytes per launch / that duration.
+
+Extra configs (0, 2, 3, 4) are reported under "configs" in the same line.
+cpu_baseline: the CPU oracle (a restatement of the reference's CPU path) on the
+host cores, bounded sample of config 1.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "unlimited-ocr.cpp_amd"))
+
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # dense bf16/f16
+
+
+def layer_bytes(L, counts, seq):
+    """Algorithmic HBM bytes of one layer call: every touched expert's packed
+    nibbles + bf16 scales once (zero point implicit), shared expert, router,
+    bf16 input and f32 output."""
+    H, I, G = L.hidden, L.inter, L.group
+    gu_e = 2 * (I * H // 2 + I * (H // G) * 2)
+    dn_e = H * I // 2 + H * (I // G) * 2
+    U = int((counts > 0).sum())
+    S = L.n_shared
+    shared_gu, shared_dn = S * gu_e, S * dn_e
+    io = seq * H * 2 + seq * H * 4 + L.n_experts * H * 2
+    return {"U": U, "gate_up": U * gu_e + shared_gu + seq * H * 2,
+            "down": U * dn_e + shared_dn, "total": U * (gu_e + dn_e) + shared_gu + shared_dn + io}
+
+
+def layer_flops(L, seq):
+    H, I = L.hidden, L.inter
+    per_tok = L.top_k * 3 * 2 * I * H + 3 * 2 * (L.n_shared * I) * H + 2 * L.n_experts * H
+    return seq * per_tok, seq * (L.top_k + L.n_shared) * 2 * 2 * I * H
+
+
+def run_config(cfg, steps, warmup, replicas, group=32, graph=False):
+    import numpy as np
+    import torch
+    from uocr_hip import MoELayerInt4, synth
+
+    dev = torch.device("cuda:0")
+    if cfg == 4:
+        wl = synth.make_config(4, group=group)
+        layers_np = wl.layers
+        stack = True
+    else:
+        base = synth.make_config(cfg, group=group)
+        layers_np = [base.layers[0]]
+        for r in range(1, replicas):
+            bias = synth.zipf_bias() if cfg == 3 else None
+            layers_np.append(synth.random_layer(9000 + 100 * cfg + r, group=group, router_bias=bias))
+        wl = base
+        stack = False
+    seq = wl.seq
+    layers = [MoELayerInt4(L) for L in layers_np]
+    x = torch.from_numpy(wl.x).to(dev)
+    x_in = x.float() if stack else x.to(torch.bfloat16)
+    outs = [torch.empty(seq, wl.layers[0].hidden, dtype=torch.float32, device=dev) for _ in range(2)]
+    ids = [torch.empty(seq, 6, dtype=torch.int32, device=dev) for _ in layers]
+    wts = [torch.empty(seq, 6, dtype=torch.float32, device=dev) for _ in layers]
+    ws = layers[0].alloc_workspace(seq, dev)
+
+    def step(i):
+        if stack:  # 12 layers: h <- h + moe(rmsnorm(h))
+            h = x_in
+            for li, lay in enumerate(layers):
+                lay.forward(h, outs[li % 2], ws, ids[li], wts[li])
+                h = outs[li % 2]
+        else:
+            li = i % len(layers)
+            layers[li].forward(x_in, outs[0], ws, ids[li], wts[li])
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    g = None
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step(0)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            step(0)
+        g.replay()
+        torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for i in range(steps):
+        if g is not None:
+            g.replay()
+        else:
+            step(i)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+
+    # per-stage durations (HIP events around each launch), same step sequence
+    stage = None
+    if not stack:
+        for lay in layers:
+            lay.set_timing(True)
+            lay.read_timing()
+        tot = {}
+        n = 0
+        for i in range(steps):
+            step(i)
+            lay = layers[i % len(layers)]
+            st, c = lay.read_timing()
+            for k, v in st.items():
+                tot[k] = tot.get(k, 0.0) + v
+            n += c
+        for lay in layers:
+            lay.set_timing(False)
+        stage = {k: v / max(n, 1) for k, v in tot.items()}
+
+    torch.cuda.synchronize()
+    counts = [np.bincount(t.cpu().numpy().ravel(), minlength=64) for t in ids]
+    res = {"config": cfg, "workload": wl.name, "seq": seq, "group": group, "ms_per_step": ms,
+           "graph": bool(graph)}
+    if stack:
+        tb = sum(layer_bytes(L, c, seq)["total"] for L, c in zip(layers_np, counts))
+        res.update(tokens_per_s=seq / (ms * 1e-3), layers=len(layers),
+                   hbm_gbs=tb / (ms * 1e-3) / 1e9, hbm_frac=tb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS)
+    else:
+        lb = [layer_bytes(L, c, seq) for L, c in zip(layers_np, counts)]
+        avg = {k: float(np.mean([b[k] for b in lb])) for k in lb[0]}
+        fl, fl_gu = layer_flops(layers_np[0], seq)
+        res.update(tokens_per_s=seq / (ms * 1e-3), touched_experts=avg["U"],
+                   layer_hbm_gbs=avg["total"] / (ms * 1e-3) / 1e9,
+                   layer_tflops=fl / (ms * 1e-3) / 1e12, stage_ms=stage,
+                   gate_up_bytes=avg["gate_up"], gate_up_flops=fl_gu)
+        if stage:
+            gu = stage["gate_up"] * 1e-3
+            res["gate_up_gbs"] = avg["gate_up"] / gu / 1e9
+            res["gate_up_tflops"] = fl_gu / gu / 1e12
+            res["gate_up_hbm_frac"] = res["gate_up_gbs"] / HBM_PEAK_GBS
+            res["gate_up_mfma_frac"] = res["gate_up_tflops"] / MFMA_PEAK_TFLOPS
+    for lay in layers:
+        lay.close()
+    return res
+
+
+def cpu_baseline(seconds=10.0):
+    """Oracle (port of the reference CPU path) on config 1's 16 tokens, repeated
+    for ~`seconds`, all host threads (tokens run in parallel)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    from uocr_hip import synth
+
+    wl = synth.make_config(1)
+    threads = min(16, os.cpu_count() or 1)
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        O.moe_layer(wl.layers[0], wl.x, threads=threads)
+        n += 1
+        if time.perf_counter() - t0 > seconds:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": n * wl.seq / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"config 1 layer (16 tokens, all routed+shared experts) x{n} runs, {dt:.1f}s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--replicas", type=int, default=6)
+    ap.add_argument("--extra", default="0,2,3,4", help="extra configs to report ('' = none)")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU only (the MoE path is benchmarked on a "
+              "single MI355X; multi-GPU expert parallelism is design-only)", file=sys.stderr)
+        sys.exit(2)
+
+    main_res = run_config(1, args.steps, args.warmup, args.replicas)
+    extras = {}
+    for c in [int(v) for v in args.extra.split(",") if v.strip()]:
+        if c == 4:
+            for g in (32, 128):
+                r = run_config(4, max(args.steps // 10, 5), 3, 1, group=g, graph=True)
+                extras[f"4_g{g}"] = r
+        else:
+            extras[str(c)] = run_config(c, max(args.steps // (10 if c >= 2 else 1), 10),
+                                        max(args.warmup // 4, 3), 3 if c >= 2 else args.replicas)
+    cpu = None if args.no_cpu else cpu_baseline()
+    gu_ms = main_res["stage_ms"]["gate_up"]
+    line = {
+        "metric": "INT4 MoE layer tokens/s (batch-16 decode, config 1)",
+        "value": main_res["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": main_res["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded INT4 g32 experts, bf16 N(0,1) hidden states)",
+        "config": {"workload": "config1_decode_t16_g32", "tokens": 16, "hidden": 1280,
+                   "experts": "64 routed top-6 + 2 shared", "inter": 896, "group": 32,
+                   "weight_replicas": args.replicas},
+        "roofline": {"bound": "hbm", "kernel": "experts_decode_kernel (gate+up)",
+                     "achieved": main_res["gate_up_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": main_res["gate_up_gbs"] / HBM_PEAK_GBS, "traffic": None,
+                     "avg_launch_ms": gu_ms, "algorithmic_bytes": main_res["gate_up_bytes"]},
+        "layer_hbm_frac": main_res["layer_hbm_gbs"] / HBM_PEAK_GBS,
+        "stage_ms": main_res["stage_ms"],
+        "cpu_baseline": cpu,
+        "configs": extras,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

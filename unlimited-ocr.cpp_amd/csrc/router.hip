@@ -418,11 +418,13 @@ hipError_t launch_router(const RouterArgs& a, bool x_is_bf16, hipStream_t st) {
     const int tokens_per_block = waves * tpw;
     const dim3 grid((a.seq + tokens_per_block - 1) / tokens_per_block);
     const size_t lds = ((size_t)waves * tpw * a.hidden + waves * 64) * sizeof(float);
+    // the large-T variant needs > 64 KiB of dynamic LDS; raise the limit once per kernel
 #define UOCR_ROUTER_CASE(XT, R, TPW)                                                                 \
     {                                                                                                \
-        hipError_t e_ = hipFuncSetAttribute((const void*)router_kernel<XT, R, TPW>,                  \
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);   \
-        if (e_ != hipSuccess) return e_;                                                             \
+        static hipError_t attr_ = hipFuncSetAttribute((const void*)router_kernel<XT, R, TPW>,        \
+                                                      hipFuncAttributeMaxDynamicSharedMemorySize,    \
+                                                      160 * 1024);                                   \
+        if (attr_ != hipSuccess) return attr_;                                                       \
         hipLaunchKernelGGL((router_kernel<XT, R, TPW>), grid, dim3(64 * waves), lds, st, a);         \
     }
     if (x_is_bf16) {
