@@ -78,6 +78,20 @@ uint16_t f32_to_bf16_rne(float f) {
     return (uint16_t)b;
 }
 
+// Device scale: the reference scale rounded to bf16 (the BASELINE scale format),
+// then stored as the equal f16 value (exact for normal f16; tiny scales round
+// into the f16 subnormal range, an absolute error below 3e-8).
+uint16_t scale_to_device(float s) {
+    const uint16_t b = f32_to_bf16_rne(s);
+    uint32_t bits = (uint32_t)b << 16;
+    float f;
+    std::memcpy(&f, &bits, 4);
+    const _Float16 h = (_Float16)f;
+    uint16_t out;
+    std::memcpy(&out, &h, 2);
+    return out;
+}
+
 // Repack rows [row0, row0 + R) x columns [col0, col0 + K) of a reference-layout
 // INT4 matrix into the tile-16x128 device layout (common.hpp).
 int repack(const uocr_hip_qmatrix& q, int row0, int R, int col0, int K, uint8_t* dst,
@@ -105,6 +119,7 @@ int repack(const uocr_hip_qmatrix& q, int row0, int R, int col0, int K, uint8_t*
                 const int r = row0 + rb * kTileRows + rr;
                 for (int gi = 0; gi < gpt; ++gi) {
                     const int g = (col0 + kt * kTileK) / G + gi;
+                    const int gl = kt * gpt + gi;  // group index within the slice
                     const size_t idx = (size_t)r * ng + g;
                     const float z = q.zeros[idx], s = q.scales[idx];
                     if (z != 8.0f) {
@@ -117,7 +132,7 @@ int repack(const uocr_hip_qmatrix& q, int row0, int R, int col0, int K, uint8_t*
                         *err = "scale outside the f16 range at row " + std::to_string(r);
                         return UOCR_HIP_EUNSUPPORTED;
                     }
-                    dsts[(((size_t)rb * KT + kt) * kTileRows + rr) * gpt + gi] = f32_to_bf16_rne(s);
+                    dsts[((size_t)rb * kTileRows + rr) * scale_row_stride(K, G) + gl] = scale_to_device(s);
                 }
             }
         }
@@ -188,7 +203,7 @@ WsPlan plan(const uocr_hip_moe_layer* L, int seq) {
     WsPlan p{};
     const int Ev = L->n_experts + L->n_virtual;
     p.slots = seq * (L->top_k + L->n_virtual);
-    p.bm = use_prefill(L, seq) ? 128 : 64;
+    p.bm = use_prefill(L, seq) ? kPrefillTileRows : kDecodeTileRows;
     p.max_tiles = (seq * L->top_k) / p.bm + L->n_experts + L->n_virtual * ((seq + p.bm - 1) / p.bm) + 1;
     size_t o = 0;
     auto take = [&](size_t bytes) {
@@ -227,6 +242,8 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
     const int H = d->hidden, I = d->inter, E = d->n_experts;
     if (H <= 0 || I <= 0 || H % kTileK || I % kTileK)
         return fail(UOCR_HIP_EINVAL, "hidden and inter must be positive multiples of 128");
+    if (router_smem_bytes(H) > 160 * 1024 || H > 1792 || I > 1792)
+        return fail(UOCR_HIP_EUNSUPPORTED, "hidden/inter above 1792 are not supported by this build");
     if (E <= 0 || E > 64) return fail(UOCR_HIP_EINVAL, "n_experts must be in [1, 64]");
     if (d->top_k <= 0 || d->top_k > kMaxTopK || d->top_k > E)
         return fail(UOCR_HIP_EINVAL, "top_k must be in [1, min(8, n_experts)]");
@@ -266,9 +283,9 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
 
     const int Ev = E + S;
     L->gu_wstride = (long long)I * H / 2;
-    L->gu_sstride = (long long)I * (H / G);
+    L->gu_sstride = (long long)I * scale_row_stride(H, G);
     L->dn_wstride = (long long)H * I / 2;
-    L->dn_sstride = (long long)H * (I / G);
+    L->dn_sstride = (long long)H * scale_row_stride(I, G);
     std::vector<uint8_t> hg((size_t)Ev * L->gu_wstride), hu(hg.size()), hd((size_t)Ev * L->dn_wstride);
     std::vector<uint16_t> hgs((size_t)Ev * L->gu_sstride), hus(hgs.size()), hds((size_t)Ev * L->dn_sstride);
 
@@ -396,8 +413,6 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     ra.x16 = x16;
     ra.ids = ids;
     ra.weights = wts;
-    HIP_TRY(launch_router(ra, x_dtype == UOCR_HIP_DTYPE_BF16, st), "router launch");
-    mark(1);
 
     GroupArgs g{};
     g.ids = ids;
@@ -415,6 +430,8 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     g.tile_e = (int*)(ws + p.tile_e);
     g.tile_m0 = (int*)(ws + p.tile_m0);
     g.n_tiles = (int*)(ws + p.ntiles);
+    HIP_TRY(launch_router(ra, x_dtype == UOCR_HIP_DTYPE_BF16, st), "router launch");
+    mark(1);
     HIP_TRY(launch_group(g, st), "group launch");
     mark(2);
 

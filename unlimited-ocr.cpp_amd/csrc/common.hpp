@@ -32,10 +32,15 @@ constexpr int kWave = 64;
 // integer ulp), ready for the v_mfma_f32_16x16x32_f16 B operand, and one
 // 1 KiB tile is one fully coalesced wave load.
 //
-// Scales: bf16 per (row, group), stored [rb][kt][16 rows][128 / group]; the
-// zero point is the implicit 8 of the reference's symmetric layout
-// (src/runtime/quant.cpp:82-116).
+// Scales: one per (row, group), stored as f16 (the bf16-valued reference
+// scales convert exactly whenever they are normal f16 numbers), row-major
+// [rows][scale_row_stride(K, group)] (K / group rounded up to 8, so every row
+// starts 16-byte aligned and a lane fetches all scales of its row with whole
+// 16-byte loads); the zero point is the implicit 8 of the reference's
+// symmetric layout (src/runtime/quant.cpp:82-116).
 // ---------------------------------------------------------------------------
+__host__ __device__ constexpr int scale_row_stride(int k, int group) { return ((k / group) + 7) / 8 * 8; }
+
 constexpr int kTileRows = 16;
 constexpr int kTileK = 128;
 constexpr int kTileBytes = 1024;
@@ -43,8 +48,10 @@ constexpr int kTileBytes = 1024;
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
 __device__ __forceinline__ f16x2 nib_pair(uint32_t w) {
-    // (w & 0x000F000F) | 0x64006400 holds two f16 values 1024 + q
-    const uint32_t v = (w & 0x000F000Fu) | 0x64006400u;
+    // (w & 0x000F000F) | 0x64006400 holds two f16 values 1024 + q; one
+    // v_bfi_b32 (the high nibbles of 0x64006400 are zero where the mask is set)
+    uint32_t v;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(v) : "v"(0x000F000Fu), "v"(w), "v"(0x64006400u));
     f16x2 h;
     __builtin_memcpy(&h, &v, 4);
     return h;
@@ -67,10 +74,7 @@ __device__ __forceinline__ f16x8 dequant8(uint32_t w, f16x2 s2) {
     return r;
 }
 
-__device__ __forceinline__ f16x2 scale2(uint32_t bf16_bits) {
-    const f16 s = (f16)bf16_bits_to_f32(bf16_bits);
-    return f16x2{s, s};
-}
+__device__ __forceinline__ f16x2 scale2(f16 s) { return f16x2{s, s}; }
 
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -78,10 +82,12 @@ __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
 
 __device__ __forceinline__ float silu_mul_f(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
 
-// Global-memory loads that bypass nothing but keep the intent explicit.
-template <typename T>
-__device__ __forceinline__ T ldg(const T* p) {
-    return *p;
+// gfx950 direct global->LDS load: each active lane copies 16 bytes from `src`
+// to lds_base + 16 * lane (lds_base must be wave-uniform). No VGPRs are used;
+// completion is tracked by vmcnt like any global load.
+__device__ __forceinline__ void load_lds16(const void* src, void* lds_base) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
 }
 
 }  // namespace uocr_hip

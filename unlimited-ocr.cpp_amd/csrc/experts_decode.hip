@@ -5,108 +5,123 @@
 // each weight row once per assigned token. Here a wave owns one 16-row block
 // of one expert's matrix, streams its tile-16x128 bytes once with 16-byte
 // loads (1 KiB per wave instruction), unpacks the nibbles in registers, and
-// multiplies them against ALL of that expert's tokens (up to 64 slots = four
-// 16-row MFMA A tiles) with v_mfma_f32_16x16x32_f16. Work items come from the
+// multiplies them against the tile's tokens (up to 16 slots = one 16-row MFMA
+// A operand) with v_mfma_f32_16x16x32_f16. Work items come from the
 // device tile list, so the grid depends only on static shapes (graph-capturable);
 // tiles beyond the live count exit at once.
 #include "launch.hpp"
 
+#if defined(UOCR_DECODE_PROFILE)
+__device__ unsigned long long uocr_dbg_ts[4096 * 8];
+extern "C" hipError_t uocr_dbg_read(void* host, size_t bytes) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(uocr_dbg_ts), bytes, 0, hipMemcpyDeviceToHost);
+}
+#define DBG_TS(i)                                                                                  \
+    if (GU && threadIdx.x == 0) uocr_dbg_ts[(blockIdx.x + blockIdx.y * gridDim.x) * 8 + (i)] = wall_clock64();
+#else
+#define DBG_TS(i)
+#endif
+
 namespace uocr_hip {
 
-constexpr int kDecodeBM = 64;
+constexpr int kDecodeBM = 16;
 
-template <int GPT>
-__device__ __forceinline__ uint32_t scale_bits(const uint16_t* sp, int s) {
-    // group index inside the 128-column tile for MFMA step s
-    return sp[(s * GPT) >> 2];
+// Weight stream loads (read once per call). UOCR_NT_LOADS selects the
+// non-temporal variant.
+__device__ __forceinline__ u32x4 stream_load(const u32x4* p) {
+#if defined(UOCR_NT_LOADS)
+    return __builtin_nontemporal_load(p);
+#else
+    return *p;
+#endif
 }
 
+// One workgroup = one m-tile (<= 16 slots of one expert) x 4 row blocks (one
+// per wave). The activation rows and the wave's scale rows are copied straight
+// into LDS with direct global->LDS loads (no registers); the activations land
+// in MFMA A-fragment order (1 KiB per 16x32 fragment, lane-contiguous) for
+// conflict-free reads. The wave's weight tiles stream into registers. All of
+// it is issued before the first wait. Only live rows are loaded (rows beyond
+// the tile's count only feed output rows that are never stored).
 template <int GPT, int KT, bool GU>
 __global__ __launch_bounds__(256) void experts_decode_kernel(ExpertArgs a) {
+    constexpr int K = KT * kTileK;
+    constexpr int NG = scale_row_stride(K, kTileK / GPT);  // padded groups per row
+    constexpr int SROW = kTileRows * NG;                    // f16 scales per row block
+    __shared__ __attribute__((aligned(16))) f16 As[KT * 4 * 64 * 8];
+    __shared__ __attribute__((aligned(16))) f16 Ss[4][GU ? 2 : 1][SROW];
+    DBG_TS(0)
     const int tile = blockIdx.x;
-    if (tile >= *a.n_tiles) return;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int rb = blockIdx.y * 4 + wave;
-    if (rb * kTileRows >= a.n_rows) return;
+    // the tile list is sized for the worst case, so its entries can be read
+    // together with the live count (one memory latency instead of two)
+    const int n_tiles = *a.n_tiles;
     const int e = a.tile_e[tile], m0 = a.tile_m0[tile];
+    DBG_TS(1)
+    if (tile >= n_tiles) return;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int rb = blockIdx.y * 4 + wave;
+    const bool wave_live = rb * kTileRows < a.n_rows;
     const int rows = min(kDecodeBM, a.counts[e] - m0);
     const int slot0 = a.offsets[e] + m0;
-    const int K = KT * kTileK;
-    const int nsub = (rows + 15) >> 4;
+    const int r = lane & 15;
 
-    const size_t toff = (size_t)rb * KT * kTileBytes + (size_t)lane * 16;
-    const uint8_t* w0 = a.w0 + (size_t)e * a.w_stride + toff;
-    const uint8_t* w1 = GU ? a.w1 + (size_t)e * a.w_stride + toff : nullptr;
-    const size_t soff = (size_t)rb * KT * kTileRows * GPT + (size_t)(lane & 15) * GPT;
-    const uint16_t* s0 = a.s0 + (size_t)e * a.s_stride + soff;
-    const uint16_t* s1 = GU ? a.s1 + (size_t)e * a.s_stride + soff : nullptr;
-
-    const f16* arow[4];
-    bool aval[4];
+    // activations: this wave fills fragments (kt, s = wave) with row r = lane % 16
+    if (r < rows) {
+        const int row = a.gather ? a.slot_tok[slot0 + r] : slot0 + r;
+        const f16* src = a.a + (size_t)row * K + wave * 32 + 8 * (lane >> 4);
 #pragma unroll
-    for (int sub = 0; sub < 4; ++sub) {
-        const int m = sub * 16 + (lane & 15);
-        aval[sub] = m < rows;
-        const int slot = slot0 + (aval[sub] ? m : 0);
-        const int row = a.gather ? a.slot_tok[slot] : slot;
-        arow[sub] = a.a + (size_t)row * K + 8 * (lane >> 4);
+        for (int kt = 0; kt < KT; ++kt) load_lds16(src + kt * kTileK, As + (size_t)(kt * 4 + wave) * 64 * 8);
     }
-
-    // issue every weight load of the wave up front
     u32x4 bw0[KT], bw1[KT];
+    if (wave_live) {
+        // this wave's 16 scale rows are one contiguous block of SROW f16
+        const size_t sb = (size_t)e * a.s_stride + (size_t)rb * SROW;
+        for (int i = lane; i * 8 < SROW; i += 64) {
+            load_lds16(a.s0 + sb + i * 8, &Ss[wave][0][(i & ~63) * 8]);
+            if constexpr (GU) load_lds16(a.s1 + sb + i * 8, &Ss[wave][GU ? 1 : 0][(i & ~63) * 8]);
+        }
+        const size_t toff = (size_t)rb * KT * kTileBytes + (size_t)lane * 16;
+        const uint8_t* w0 = a.w0 + (size_t)e * a.w_stride + toff;
+        const uint8_t* w1 = GU ? a.w1 + (size_t)e * a.w_stride + toff : nullptr;
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+            bw0[kt] = stream_load(reinterpret_cast<const u32x4*>(w0 + (size_t)kt * kTileBytes));
+            if constexpr (GU) bw1[kt] = stream_load(reinterpret_cast<const u32x4*>(w1 + (size_t)kt * kTileBytes));
+        }
+    }
+    DBG_TS(2)
+    __builtin_amdgcn_s_waitcnt(0);  // direct-to-LDS data of this wave has landed
+    __syncthreads();
+    DBG_TS(3)
+    if (!wave_live) return;
+
+    const f16* srow0 = &Ss[wave][0][r * NG];
+    const f16* srow1 = &Ss[wave][GU ? 1 : 0][r * NG];
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
-        bw0[kt] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(w0 + (size_t)kt * kTileBytes));
-        if constexpr (GU)
-            bw1[kt] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(w1 + (size_t)kt * kTileBytes));
-    }
-
-    f32x4 acc0[4], acc1[4];
-#pragma unroll
-    for (int sub = 0; sub < 4; ++sub) {
-        acc0[sub] = f32x4{0.f, 0.f, 0.f, 0.f};
-        acc1[sub] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    const f16x8 zero8 = {};
-
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-        const uint16_t* sp0 = s0 + kt * kTileRows * GPT;
-        const uint16_t* sp1 = GU ? s1 + kt * kTileRows * GPT : nullptr;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            const f16x8 b0 = dequant8(bw0[kt][s], scale2(scale_bits<GPT>(sp0, s)));
-            f16x8 b1;
-            if constexpr (GU) b1 = dequant8(bw1[kt][s], scale2(scale_bits<GPT>(sp1, s)));
-#pragma unroll
-            for (int sub = 0; sub < 4; ++sub) {
-                if (sub < nsub) {
-                    const f16x8 av =
-                        aval[sub] ? *reinterpret_cast<const f16x8*>(arow[sub] + kt * kTileK + s * 32) : zero8;
-                    acc0[sub] = mfma16(av, b0, acc0[sub]);
-                    if constexpr (GU) acc1[sub] = mfma16(av, b1, acc1[sub]);
-                }
-            }
+            const int g = kt * GPT + ((s * GPT) >> 2);  // group of MFMA step (kt, s)
+            const f16x8 av = *reinterpret_cast<const f16x8*>(As + ((size_t)(kt * 4 + s) * 64 + lane) * 8);
+            acc0 = mfma16(av, dequant8(bw0[kt][s], scale2(srow0[g])), acc0);
+            if constexpr (GU) acc1 = mfma16(av, dequant8(bw1[kt][s], scale2(srow1[g])), acc1);
         }
     }
 
     const int col = rb * kTileRows + (lane & 15);
 #pragma unroll
-    for (int sub = 0; sub < 4; ++sub) {
-        if (sub < nsub) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = sub * 16 + 4 * (lane >> 4) + i;
-                if (m < rows) {
-                    const size_t o = (size_t)(slot0 + m) * a.n_rows + col;
-                    if constexpr (GU)
-                        a.act_out[o] = (f16)silu_mul_f(acc0[sub][i], acc1[sub][i]);
-                    else
-                        a.y_out[o] = acc0[sub][i];
-                }
-            }
+    for (int i = 0; i < 4; ++i) {
+        const int m = 4 * (lane >> 4) + i;
+        if (m < rows) {
+            const size_t o = (size_t)(slot0 + m) * a.n_rows + col;
+            if constexpr (GU)
+                a.act_out[o] = (f16)silu_mul_f(acc0[i], acc1[i]);
+            else
+                a.y_out[o] = acc0[i];
         }
     }
+    DBG_TS(4)
 }
 
 // out[t] = residual[t] + (sum_j fma(w[t,j], y[pos[t,j]]) in j order) + shared(t)

@@ -78,6 +78,9 @@ struct CombineArgs {
 };
 
 hipError_t launch_router(const RouterArgs& a, bool x_is_bf16, hipStream_t st);
+size_t router_smem_bytes(int hidden);
+constexpr int kDecodeTileRows = 16;
+constexpr int kPrefillTileRows = 128;
 hipError_t launch_router_from_logits(const RouterArgs& a, const float* logits, hipStream_t st);
 hipError_t launch_group(const GroupArgs& g, hipStream_t st);
 hipError_t launch_experts_decode(const ExpertArgs& a, bool gate_up, int max_tiles, hipStream_t st);

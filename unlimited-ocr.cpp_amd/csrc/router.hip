@@ -38,8 +38,28 @@ __device__ __forceinline__ float apply_expf_fix(float x, float y, const uint32_t
     return y;
 }
 
+// glibc expf bits: correctly rounded exp, corrected from the fix-up table only
+// when the binary64 value sits within 1/256 ulp of a rounding midpoint.
 __device__ __forceinline__ float ref_expf(float x, const uint32_t* offs, const uint32_t* ent) {
-    return apply_expf_fix(x, uocr_uexpf(x), offs, ent);
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return INFINITY;
+    if (x < -103.97208404541015625f) return 0.0f;
+    const double yd = uocr_uexp_d(x);
+    const float y = (float)yd;
+    return uocr_uexpf_near_tie_d(yd) ? apply_expf_fix(x, y, offs, ent) : y;
+}
+
+// Greedy top-k of the reference (strict '>' scan, first maximum wins,
+// moe_decoder.cpp:264-277) selects experts in order of (p descending, index
+// ascending); lane e's position in that order is the number of experts that
+// beat it. p[] holds the scores in LDS; returns the rank of `pe` (lane e).
+__device__ __forceinline__ int greedy_rank(const float* p, int E, int e, float pe) {
+    int rank = 0;
+    for (int j = 0; j < E; ++j) {
+        const float q = p[j];
+        rank += (q > pe || (q == pe && j < e)) ? 1 : 0;
+    }
+    return rank;
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -85,146 +105,299 @@ __device__ __forceinline__ void load8_f32<float>(const float* p, float* out) {
     }
 }
 
-// One wave routes TPW tokens; lane e owns expert e (E <= 64).
-// LDS: [waves][TPW][H] f32 activations + [waves][64] scratch.
-template <typename XT, bool RMS, int TPW>
-__global__ __launch_bounds__(256) void router_kernel(RouterArgs a) {
-    extern __shared__ float lds[];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int H = a.hidden, E = a.n_experts, K = a.top_k;
-    float* xs = lds + (size_t)wave * TPW * H;
-    float* scr = lds + (size_t)(blockDim.x >> 6) * TPW * H + wave * 64;
-    const int t0 = (blockIdx.x * (blockDim.x >> 6) + wave) * TPW;
-    const XT* x = static_cast<const XT*>(a.x);
+// ---------------------------------------------------------------------------
+// Stable grouping body (one workgroup of 1024 threads), shared by the
+// stand-alone group kernel and the router kernel's fused tail.
+// ---------------------------------------------------------------------------
+constexpr int kGroupThreads = 1024;
+constexpr int kGroupWaves = kGroupThreads / 64;
 
-    // 1. stage the activations as f32
+struct GroupLds {
+    int hist[kMaxExperts];
+    int offs[kMaxExperts + 1];
+    int tile0[kMaxExperts + 1];
+    int run[kMaxExperts];
+    int wcnt[kGroupWaves][kMaxExperts];
+};
+
+// Exclusive prefix sum of v[0..n) (n <= 128) by wave 0; out[n] = total.
+__device__ __forceinline__ void wave0_exclusive_scan(const int* v, int* out, int n) {
+    const int lane = threadIdx.x & 63;
+    const int a = (2 * lane < n) ? v[2 * lane] : 0;
+    const int b = (2 * lane + 1 < n) ? v[2 * lane + 1] : 0;
+    int inc = a + b;
 #pragma unroll
-    for (int tt = 0; tt < TPW; ++tt) {
-        const int t = t0 + tt;
-        for (int c = lane * 8; c < H; c += 64 * 8) {
-            float v[8];
-            if (t < a.seq) {
-                load8_f32<XT>(x + (size_t)t * H + c, v);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) xs[tt * H + c + i] = v[i];
-        }
+    for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(inc, o, kWave);
+        if (lane >= o) inc += u;
+    }
+    const int ex = inc - a - b;
+    if (2 * lane < n) out[2 * lane] = ex;
+    if (2 * lane + 1 < n) out[2 * lane + 1] = ex + a;
+    if (lane == 63) out[n] = inc;
+}
+
+// `ids` / `wts` may live in global memory or LDS. Must be called by all 1024 threads.
+__device__ void group_body(const int* ids, const float* wts, const GroupArgs& g, GroupLds& s) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int E = g.n_experts, N = g.seq * g.top_k;
+    const int Ev = E + g.n_virtual;
+
+    for (int e = tid; e < kMaxExperts; e += kGroupThreads) {
+        s.hist[e] = 0;
+        s.run[e] = 0;
     }
     __syncthreads();
+    for (int i = tid; i < N; i += kGroupThreads) {
+        const int e = ids[i];
+        if (e >= 0 && e < E) atomicAdd(&s.hist[e], 1);
+    }
+    __syncthreads();
+    if (wave == 0) {
+        for (int e = lane; e < g.n_virtual; e += 64) s.hist[E + e] = g.seq;  // virtual groups: all tokens
+    }
+    __syncthreads();
+    if (wave == 0) wave0_exclusive_scan(s.hist, s.offs, Ev);
+    if (wave == 1 && g.tile_e) {
+        // tiles per expert into run[] (reset below), then scan into tile0[]
+        for (int e = lane; e < Ev; e += 64) s.run[e] = (s.hist[e] + g.bm - 1) / g.bm;
+    }
+    __syncthreads();
+    if (g.tile_e && wave == 1) wave0_exclusive_scan(s.run, s.tile0, Ev);
+    __syncthreads();
+    if (g.counts) {
+        for (int e = tid; e < Ev; e += kGroupThreads) {
+            g.counts[e] = s.hist[e];
+            g.offsets[e] = s.offs[e];
+        }
+        if (tid == 0) g.offsets[Ev] = s.offs[Ev];
+    }
+    if (g.tile_e) {
+        if (tid == 0) *g.n_tiles = s.tile0[Ev];
+        for (int e = wave; e < Ev; e += kGroupWaves) {
+            const int nt = s.tile0[e + 1] - s.tile0[e];
+            for (int m = lane; m < nt; m += 64) {
+                g.tile_e[s.tile0[e] + m] = e;
+                g.tile_m0[s.tile0[e] + m] = m * g.bm;
+            }
+        }
+    }
+    for (int e = tid; e < kMaxExperts; e += kGroupThreads) s.run[e] = 0;
+    __syncthreads();
+    // stable placement of the routed entries, kGroupThreads entries per round
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int base = 0; base < N; base += kGroupThreads) {
+        for (int i = tid; i < kGroupWaves * kMaxExperts; i += kGroupThreads) (&s.wcnt[0][0])[i] = 0;
+        __syncthreads();
+        const int i = base + tid;
+        const int e = (i < N) ? ids[i] : -1;
+        const bool valid = e >= 0 && e < E;
+        uint64_t m = __ballot(valid);
+#pragma unroll
+        for (int b = 0; b < 7; ++b) {
+            const bool bit = valid && ((e >> b) & 1);
+            const uint64_t bal = __ballot(bit);
+            m &= bit ? bal : ~bal;
+        }
+        const int rank = __popcll(m & below);
+        if (valid && rank == 0) s.wcnt[wave][e] = __popcll(m);
+        __syncthreads();
+        for (int ee = tid; ee < E; ee += kGroupThreads) {
+            int acc = s.run[ee];
+            for (int w = 0; w < kGroupWaves; ++w) {
+                const int c = s.wcnt[w][ee];
+                s.wcnt[w][ee] = acc;
+                acc += c;
+            }
+            s.run[ee] = acc;
+        }
+        __syncthreads();
+        if (valid) {
+            const int r = s.wcnt[wave][e] + rank;  // position within expert e
+            const float w = wts[i];
+            if (g.slot_tok) {
+                const int sl = s.offs[e] + r;
+                g.slot_tok[sl] = i / g.top_k;
+                g.slot_w[sl] = w;
+                if (g.pos) g.pos[i] = sl;
+            }
+            if (g.assign_token && r < g.cap) {
+                g.assign_token[(size_t)e * g.cap + r] = i / g.top_k;
+                g.assign_w[(size_t)e * g.cap + r] = w;
+            }
+        }
+        __syncthreads();
+    }
+    if (g.assign_count)
+        for (int e = tid; e < E; e += kGroupThreads) g.assign_count[e] = min(s.hist[e], g.cap);
+    if (g.slot_tok) {
+        for (int v = 0; v < g.n_virtual; ++v)
+            for (int t = tid; t < g.seq; t += kGroupThreads) {
+                g.slot_tok[s.offs[E + v] + t] = t;
+                g.slot_w[s.offs[E + v] + t] = 1.0f;
+            }
+    }
+}
 
-    // 2. RMSNorm: one lane per token runs the reference's sequential chain
+__global__ __launch_bounds__(kGroupThreads) void group_kernel(GroupArgs g) {
+    __shared__ GroupLds s;
+    group_body(g.ids, g.weights, g, s);
+}
+
+// ---------------------------------------------------------------------------
+// Router: one wave per token, lane e owns expert e (E <= 64); a workgroup of W
+// waves routes W tokens (W = 4 for small batches, so the FMA chains of
+// different tokens run on different SIMDs and CUs; W = 16 for large batches,
+// so each streamed weight chunk serves 16 tokens). The router matrix
+// ([H/8][E][8] bf16) streams through LDS in double-buffered 128-column chunks,
+// so every lane's FMA chain reads its weights from LDS instead of issuing one
+// dependent global load per 8 columns.
+// ---------------------------------------------------------------------------
+constexpr int kChunkC8 = 16;  // 128 columns per chunk
+
+__host__ __device__ constexpr size_t router_lds_bytes(int H, int waves) {
+    return (size_t)waves * H * 4          // xs
+           + 2ull * kChunkC8 * 64 * 16    // W chunks (E <= 64)
+           + (size_t)waves * 64 * 4       // per-wave scores
+           + (size_t)waves * 16 * 4;      // per-wave top-k values
+}
+
+constexpr int kMaxChunks = 14;  // hidden <= 1792
+
+template <typename XT, bool RMS, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void router_kernel(RouterArgs a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    constexpr int NT = WAVES * 64;
+    constexpr int UPT = kChunkC8 * 64 / NT;  // 16-byte chunk units per thread (E <= 64)
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, tid = threadIdx.x;
+    const int H = a.hidden, E = a.n_experts, K = a.top_k;
+    float* xs = reinterpret_cast<float*>(smem) + (size_t)wave * H;
+    u32x4* wb = reinterpret_cast<u32x4*>(smem + (size_t)WAVES * H * 4);
+    float* scr = reinterpret_cast<float*>(wb + 2 * kChunkC8 * 64) + wave * 64;
+    float* topv = reinterpret_cast<float*>(wb + 2 * kChunkC8 * 64) + WAVES * 64 + wave * 16;
+    const int t = blockIdx.x * WAVES + wave;
+    const bool live = t < a.seq;
+    const XT* x = static_cast<const XT*>(a.x);
+    const int chunk_units = kChunkC8 * E;
+    const u32x4* wsrc = reinterpret_cast<const u32x4*>(a.router_t);
+    const int n_chunks = H / (kChunkC8 * 8);
+
+    // every router-weight load of this thread, all chunks, issued at once
+    u32x4 wreg[kMaxChunks][UPT];
+#pragma unroll
+    for (int ch = 0; ch < kMaxChunks; ++ch)
+#pragma unroll
+        for (int j = 0; j < UPT; ++j) {
+            const int u = tid + j * NT;
+            if (ch < n_chunks && u < chunk_units) wreg[ch][j] = wsrc[(size_t)ch * chunk_units + u];
+        }
+    // this wave's token row, as f32
+    for (int c = lane * 8; c < H; c += 64 * 8) {
+        float v[8];
+        if (live) {
+            load8_f32<XT>(x + (size_t)t * H + c, v);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+        }
+        *reinterpret_cast<f32x4*>(xs + c) = f32x4{v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<f32x4*>(xs + c + 4) = f32x4{v[4], v[5], v[6], v[7]};
+    }
+#pragma unroll
+    for (int j = 0; j < UPT; ++j)
+        if (tid + j * NT < chunk_units) wb[tid + j * NT] = wreg[0][j];
+    __syncthreads();
+
     if constexpr (RMS) {
-        if (lane < TPW) {
-            const float* xr = xs + lane * H;
+        if (lane == 0) {
             float ss = 0.0f;
             for (int c = 0; c < H; c += 4) {
-                const f32x4 v = *reinterpret_cast<const f32x4*>(xr + c);
+                const f32x4 v = *reinterpret_cast<const f32x4*>(xs + c);
                 ss = fmaf(v[0], v[0], ss);
                 ss = fmaf(v[1], v[1], ss);
                 ss = fmaf(v[2], v[2], ss);
                 ss = fmaf(v[3], v[3], ss);
             }
-            scr[lane] = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)H) + a.rms_eps));
+            scr[0] = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)H) + a.rms_eps));
         }
         __syncthreads();
-#pragma unroll
-        for (int tt = 0; tt < TPW; ++tt) {
-            const float inv = scr[tt];
-            for (int c = lane; c < H; c += 64) xs[tt * H + c] = xs[tt * H + c] * inv * a.rms_weight[c];
-        }
+        const float inv = scr[0];
+        for (int c = lane; c < H; c += 64) xs[c] = xs[c] * inv * a.rms_weight[c];
         __syncthreads();
     }
 
-    // 3. f16 copy of the expert input for the MFMA kernels
-#pragma unroll
-    for (int tt = 0; tt < TPW; ++tt) {
-        const int t = t0 + tt;
-        if (t < a.seq) {
-            for (int c = lane * 8; c < H; c += 64 * 8) {
-                f16x8 h;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) h[i] = (f16)xs[tt * H + c + i];
-                *reinterpret_cast<f16x8*>(a.x16 + (size_t)t * H + c) = h;
-            }
+    if (live) {
+        for (int c = lane * 8; c < H; c += 64 * 8) {
+            const f32x4 p = *reinterpret_cast<const f32x4*>(xs + c);
+            const f32x4 q = *reinterpret_cast<const f32x4*>(xs + c + 4);
+            f16x8 h = {(f16)p[0], (f16)p[1], (f16)p[2], (f16)p[3], (f16)q[0], (f16)q[1], (f16)q[2], (f16)q[3]};
+            *reinterpret_cast<f16x8*>(a.x16 + (size_t)t * H + c) = h;
         }
     }
 
-    // 4. logits: lane e, sequential fmaf over k (router W stored [H/8][E][8])
-    float acc[TPW];
+    // logits: lane e runs the sequential fmaf chain over all H columns
+    float acc = 0.0f;
 #pragma unroll
-    for (int tt = 0; tt < TPW; ++tt) acc[tt] = 0.0f;
-    if (lane < E) {
-        const uint16_t* wp = a.router_t + (size_t)lane * 8;
-        for (int c8 = 0; c8 < H / 8; ++c8) {
-            float w[8];
-            load8_f32<uint16_t>(wp + (size_t)c8 * E * 8, w);
-#pragma unroll
-            for (int tt = 0; tt < TPW; ++tt) {
-                const f32x4 xa = *reinterpret_cast<const f32x4*>(xs + tt * H + c8 * 8);
-                const f32x4 xb = *reinterpret_cast<const f32x4*>(xs + tt * H + c8 * 8 + 4);
-                float s = acc[tt];
-                s = fmaf(xa[0], w[0], s);
-                s = fmaf(xa[1], w[1], s);
-                s = fmaf(xa[2], w[2], s);
-                s = fmaf(xa[3], w[3], s);
-                s = fmaf(xb[0], w[4], s);
-                s = fmaf(xb[1], w[5], s);
-                s = fmaf(xb[2], w[6], s);
-                s = fmaf(xb[3], w[7], s);
-                acc[tt] = s;
+    for (int ch = 0; ch < kMaxChunks; ++ch) {
+        if (ch < n_chunks) {
+            const u32x4* cur = wb + (ch & 1) * kChunkC8 * 64;
+            if (lane < E) {
+#pragma unroll 4
+                for (int c8 = 0; c8 < kChunkC8; ++c8) {
+                    const u32x4 wv = cur[c8 * E + lane];
+                    const float* xp = xs + (ch * kChunkC8 + c8) * 8;
+                    const f32x4 xa = *reinterpret_cast<const f32x4*>(xp);
+                    const f32x4 xb = *reinterpret_cast<const f32x4*>(xp + 4);
+                    acc = fmaf(xa[0], __uint_as_float(wv[0] << 16), acc);
+                    acc = fmaf(xa[1], __uint_as_float(wv[0] & 0xffff0000u), acc);
+                    acc = fmaf(xa[2], __uint_as_float(wv[1] << 16), acc);
+                    acc = fmaf(xa[3], __uint_as_float(wv[1] & 0xffff0000u), acc);
+                    acc = fmaf(xb[0], __uint_as_float(wv[2] << 16), acc);
+                    acc = fmaf(xb[1], __uint_as_float(wv[2] & 0xffff0000u), acc);
+                    acc = fmaf(xb[2], __uint_as_float(wv[3] << 16), acc);
+                    acc = fmaf(xb[3], __uint_as_float(wv[3] & 0xffff0000u), acc);
+                }
             }
-        }
-    }
-
-    // 5. scoring + greedy top-k, one token at a time
+            if (ch + 1 < kMaxChunks && ch + 1 < n_chunks) {
 #pragma unroll
-    for (int tt = 0; tt < TPW; ++tt) {
-        const int t = t0 + tt;
-        const float l = acc[tt];
-        float p;
-        if (a.scoring_sigmoid) {
-            p = __fdiv_rn(1.0f, 1.0f + ref_expf(-l, a.fix_offsets, a.fix_entries));
-        } else {
-            const float mx = wave_max(lane < E ? l : -INFINITY);
-            const float ev = ref_expf(l - mx, a.fix_offsets, a.fix_entries);
-            scr[lane] = ev;
+                for (int j = 0; j < UPT; ++j)
+                    if (tid + j * NT < chunk_units) wb[((ch + 1) & 1) * kChunkC8 * 64 + tid + j * NT] = wreg[ch + 1][j];
+            }
             __syncthreads();
+        }
+    }
+
+    // scoring (softmax over experts in index order, or sigmoid)
+    float p;
+    if (a.scoring_sigmoid) {
+        p = __fdiv_rn(1.0f, 1.0f + ref_expf(-acc, a.fix_offsets, a.fix_entries));
+    } else {
+        const float mx = wave_max(lane < E ? acc : -INFINITY);
+        const float ev = ref_expf(acc - mx, a.fix_offsets, a.fix_entries);
+        scr[lane] = ev;
+        __syncthreads();
+        float sum = 0.0f;
+        for (int e = 0; e < E; ++e) sum += scr[e];  // expert order, same bits in every lane
+        p = ev * __fdiv_rn(1.0f, sum);
+        __syncthreads();
+    }
+    scr[lane] = p;
+    __syncthreads();
+    const int rank = lane < E ? greedy_rank(scr, E, lane, p) : 64;
+    if (rank < K) topv[rank] = p;
+    __syncthreads();
+    if (live && lane < K) {
+        float wj = topv[lane];
+        if (K > 1 && a.norm_topk_prob) {  // moe_decoder.cpp:280-284
             float sum = 0.0f;
-            for (int e = 0; e < E; ++e) sum += scr[e];  // every lane: same order, same bits
-            p = ev * __fdiv_rn(1.0f, sum);
-            __syncthreads();
-        }
-        float sel = lane < E ? p : -INFINITY;
-        float wj = 0.0f;
-        int idj = 0;
-        for (int j = 0; j < K; ++j) {
-            float v = sel;
-            int i = lane;
-            wave_argmax(v, i);
-            if (!(v > -1e30f)) i = -1;  // reference: no candidate above -1e30
-            if (lane == j) {
-                idj = i;
-                wj = v;
-            }
-            if (lane == i) sel = -1e30f;
-        }
-        // renormalisation / scaling (moe_decoder.cpp:280-287)
-        if (K > 1 && a.norm_topk_prob) {
-            float s = 0.0f;
-            for (int j = 0; j < K; ++j) s += __shfl(wj, j, kWave);
-            const float denom = s + 1e-20f;
-            wj = __fdiv_rn(wj, denom) * a.scaling;
+            for (int j = 0; j < K; ++j) sum += topv[j];
+            wj = __fdiv_rn(wj, sum + 1e-20f) * a.scaling;
         } else {
             wj *= a.scaling;
         }
-        if (t < a.seq && lane < K) {
-            a.ids[(size_t)t * K + lane] = idj;
-            a.weights[(size_t)t * K + lane] = wj;
-        }
+        a.weights[(size_t)t * K + lane] = wj;
     }
+    if (live && rank < K) a.ids[(size_t)t * K + rank] = lane;
 }
 
 // Router from precomputed logits [seq, E] (mirror of moe_router_topk,
@@ -288,160 +461,35 @@ __global__ __launch_bounds__(256) void router_from_logits_kernel(RouterArgs a, c
 }
 
 // ---------------------------------------------------------------------------
-// Stable grouping (one workgroup of 1024 threads).
-// ---------------------------------------------------------------------------
-constexpr int kGroupThreads = 1024;
-constexpr int kGroupWaves = kGroupThreads / 64;
-
-__global__ __launch_bounds__(kGroupThreads) void group_kernel(GroupArgs g) {
-    __shared__ int hist[kMaxExperts];
-    __shared__ int offs[kMaxExperts + 1];
-    __shared__ int run[kMaxExperts];
-    __shared__ int wcnt[kGroupWaves][kMaxExperts];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int E = g.n_experts, N = g.seq * g.top_k;
-    const int Ev = E + g.n_virtual;
-
-    for (int e = tid; e < kMaxExperts; e += kGroupThreads) {
-        hist[e] = 0;
-        run[e] = 0;
-    }
-    __syncthreads();
-    for (int i = tid; i < N; i += kGroupThreads) {
-        const int e = g.ids[i];
-        if (e >= 0 && e < E) atomicAdd(&hist[e], 1);
-    }
-    __syncthreads();
-    if (tid == 0) {
-        int s = 0;
-        for (int e = 0; e < Ev; ++e) {
-            offs[e] = s;
-            s += (e < E) ? hist[e] : g.seq;
-        }
-        offs[Ev] = s;
-    }
-    __syncthreads();
-    if (g.counts) {
-        for (int e = tid; e < Ev; e += kGroupThreads) {
-            g.counts[e] = (e < E) ? hist[e] : g.seq;
-            g.offsets[e] = offs[e];
-        }
-        if (tid == 0) g.offsets[Ev] = offs[Ev];
-    }
-    // m-tile list: tiles of BM slots per expert, experts in index order
-    if (g.tile_e) {
-        if (tid == 0) {
-            int nt = 0;
-            for (int e = 0; e < Ev; ++e) {
-                const int c = offs[e + 1] - offs[e];
-                run[e] = nt;  // temporarily: first tile of e
-                nt += (c + g.bm - 1) / g.bm;
-            }
-            *g.n_tiles = nt;
-        }
-        __syncthreads();
-        for (int e = tid; e < Ev; e += kGroupThreads) {
-            const int c = offs[e + 1] - offs[e];
-            const int nt = (c + g.bm - 1) / g.bm;
-            for (int m = 0; m < nt; ++m) {
-                g.tile_e[run[e] + m] = e;
-                g.tile_m0[run[e] + m] = m * g.bm;
-            }
-        }
-        __syncthreads();
-        for (int e = tid; e < kMaxExperts; e += kGroupThreads) run[e] = 0;
-        __syncthreads();
-    }
-    // stable placement of the routed entries, kGroupThreads entries per round
-    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    for (int base = 0; base < N; base += kGroupThreads) {
-        for (int i = tid; i < kGroupWaves * kMaxExperts; i += kGroupThreads) (&wcnt[0][0])[i] = 0;
-        __syncthreads();
-        const int i = base + tid;
-        const int e = (i < N) ? g.ids[i] : -1;
-        const bool valid = e >= 0 && e < E;
-        uint64_t m = __ballot(valid);
-#pragma unroll
-        for (int b = 0; b < 7; ++b) {
-            const uint64_t bal = __ballot(valid && ((e >> b) & 1));
-            m &= (valid && ((e >> b) & 1)) ? bal : ~bal;
-        }
-        const int rank = __popcll(m & below);
-        if (valid && rank == 0) wcnt[wave][e] = __popcll(m);
-        __syncthreads();
-        for (int ee = tid; ee < E; ee += kGroupThreads) {
-            int acc = run[ee];
-            for (int w = 0; w < kGroupWaves; ++w) {
-                const int c = wcnt[w][ee];
-                wcnt[w][ee] = acc;
-                acc += c;
-            }
-            run[ee] = acc;
-        }
-        __syncthreads();
-        if (valid) {
-            const int r = wcnt[wave][e] + rank;  // position within expert e
-            const float w = g.weights[i];
-            if (g.slot_tok) {
-                const int s = offs[e] + r;
-                g.slot_tok[s] = i / g.top_k;
-                g.slot_w[s] = w;
-                if (g.pos) g.pos[i] = s;
-            }
-            if (g.assign_token && r < g.cap) {
-                g.assign_token[(size_t)e * g.cap + r] = i / g.top_k;
-                g.assign_w[(size_t)e * g.cap + r] = w;
-            }
-        }
-        __syncthreads();
-    }
-    if (g.assign_count)
-        for (int e = tid; e < E; e += kGroupThreads) g.assign_count[e] = min(hist[e], g.cap);
-    // virtual (shared-expert) groups: every token, weight 1
-    if (g.slot_tok) {
-        for (int v = 0; v < g.n_virtual; ++v)
-            for (int t = tid; t < g.seq; t += kGroupThreads) {
-                g.slot_tok[offs[E + v] + t] = t;
-                g.slot_w[offs[E + v] + t] = 1.0f;
-            }
-    }
-}
-
-// ---------------------------------------------------------------------------
 // host launchers
 // ---------------------------------------------------------------------------
-hipError_t launch_router(const RouterArgs& a, bool x_is_bf16, hipStream_t st) {
-    const int waves = 4;
-    const bool rms = a.rms_weight != nullptr;
-    const bool big = a.seq >= 1024;
-    const int tpw = big ? 4 : 1;
-    const int tokens_per_block = waves * tpw;
-    const dim3 grid((a.seq + tokens_per_block - 1) / tokens_per_block);
-    const size_t lds = ((size_t)waves * tpw * a.hidden + waves * 64) * sizeof(float);
-    // the large-T variant needs > 64 KiB of dynamic LDS; raise the limit once per kernel
-#define UOCR_ROUTER_CASE(XT, R, TPW)                                                                 \
-    {                                                                                                \
-        static hipError_t attr_ = hipFuncSetAttribute((const void*)router_kernel<XT, R, TPW>,        \
-                                                      hipFuncAttributeMaxDynamicSharedMemorySize,    \
-                                                      160 * 1024);                                   \
-        if (attr_ != hipSuccess) return attr_;                                                       \
-        hipLaunchKernelGGL((router_kernel<XT, R, TPW>), grid, dim3(64 * waves), lds, st, a);         \
-    }
-    if (x_is_bf16) {
-        if (rms) {
-            if (big) UOCR_ROUTER_CASE(uint16_t, true, 4) else UOCR_ROUTER_CASE(uint16_t, true, 1)
-        } else {
-            if (big) UOCR_ROUTER_CASE(uint16_t, false, 4) else UOCR_ROUTER_CASE(uint16_t, false, 1)
-        }
-    } else {
-        if (rms) {
-            if (big) UOCR_ROUTER_CASE(float, true, 4) else UOCR_ROUTER_CASE(float, true, 1)
-        } else {
-            if (big) UOCR_ROUTER_CASE(float, false, 4) else UOCR_ROUTER_CASE(float, false, 1)
-        }
-    }
-#undef UOCR_ROUTER_CASE
+size_t router_smem_bytes(int hidden) { return router_lds_bytes(hidden, 16); }
+
+template <typename XT, bool RMS, int WAVES>
+static hipError_t launch_router_t(const RouterArgs& a, hipStream_t st) {
+    // > 64 KiB of dynamic LDS: raise the limit once per kernel
+    static hipError_t attr = hipFuncSetAttribute((const void*)router_kernel<XT, RMS, WAVES>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != hipSuccess) return attr;
+    const dim3 grid((a.seq + WAVES - 1) / WAVES);
+    hipLaunchKernelGGL((router_kernel<XT, RMS, WAVES>), grid, dim3(WAVES * 64), router_lds_bytes(a.hidden, WAVES),
+                       st, a);
     return hipGetLastError();
+}
+
+template <typename XT, bool RMS>
+static hipError_t launch_router_w(const RouterArgs& a, hipStream_t st) {
+    // small batches: 4 tokens per workgroup spreads the FMA chains over CUs;
+    // large batches: 16 tokens per workgroup amortise the router-weight stream
+    return a.seq >= 256 ? launch_router_t<XT, RMS, 16>(a, st) : launch_router_t<XT, RMS, 4>(a, st);
+}
+
+hipError_t launch_router(const RouterArgs& a, bool x_is_bf16, hipStream_t st) {
+    if (a.n_experts > 64 || a.hidden > kMaxChunks * kChunkC8 * 8 || a.hidden % (kChunkC8 * 8))
+        return hipErrorInvalidValue;
+    const bool rms = a.rms_weight != nullptr;
+    if (x_is_bf16) return rms ? launch_router_w<uint16_t, true>(a, st) : launch_router_w<uint16_t, false>(a, st);
+    return rms ? launch_router_w<float, true>(a, st) : launch_router_w<float, false>(a, st);
 }
 
 hipError_t launch_router_from_logits(const RouterArgs& a, const float* logits, hipStream_t st) {

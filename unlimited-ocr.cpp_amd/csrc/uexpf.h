@@ -19,10 +19,8 @@
 #define UEXPF_QUAL static inline
 #endif
 
-UEXPF_QUAL float uocr_uexpf(float xf) {
-    if (xf != xf) return xf;
-    if (xf > 88.72283935546875f) return INFINITY;
-    if (xf < -103.97208404541015625f) return 0.0f;
+// binary64 value of exp(xf) before the final rounding (finite, in-range xf)
+UEXPF_QUAL double uocr_uexp_d(float xf) {
     const double x = (double)xf;
     const double kd = rint(x * 1.4426950408889634);
     double r = fma(-kd, 0x1.62e42fefa39efp-1, x);
@@ -41,5 +39,34 @@ UEXPF_QUAL float uocr_uexpf(float xf) {
     p = fma(p, r, 0.5);
     p = fma(p, r, 1.0);
     p = fma(p, r, 1.0);
-    return (float)ldexp(p, (int)kd);
+    return ldexp(p, (int)kd);
+}
+
+UEXPF_QUAL float uocr_uexpf(float xf) {
+    if (xf != xf) return xf;
+    if (xf > 88.72283935546875f) return INFINITY;
+    if (xf < -103.97208404541015625f) return 0.0f;
+    return (float)uocr_uexp_d(xf);
+}
+
+// True when the binary64 value lies within 1/256 ulp of a binary32 rounding
+// midpoint. glibc's expf can only round differently from the correctly rounded
+// result in that band (its pre-rounding error is 1.69 * 2^-34 relative, i.e.
+// <= 0.0017 ulp); the table generator verifies on all 2^32 inputs that every
+// listed difference passes this test, so callers may skip the fix-up table
+// whenever it is false.
+UEXPF_QUAL int uocr_uexpf_near_tie_d(double yd) {
+    const float yf = (float)yd;
+    unsigned int b;
+    __builtin_memcpy(&b, &yf, 4);
+    b = (yd >= (double)yf) ? b + 1u : b - 1u;
+    float nb;
+    __builtin_memcpy(&nb, &b, 4);
+    const double mid = ((double)yf + (double)nb) * 0.5;
+    return fabs(yd - mid) < fabs((double)nb - (double)yf) * (1.0 / 256.0);
+}
+
+UEXPF_QUAL int uocr_uexpf_near_tie(float xf) {
+    if (xf != xf || xf > 88.72283935546875f || xf < -103.97208404541015625f) return 0;
+    return uocr_uexpf_near_tie_d(uocr_uexp_d(xf));
 }

@@ -3,7 +3,8 @@ import ctypes as C
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libuocr_hip.so")
+# UOCR_HIP_LIB overrides the in-tree library (used to compare builds)
+_LIB_PATH = os.environ.get("UOCR_HIP_LIB") or os.path.join(os.path.dirname(_HERE), "lib", "libuocr_hip.so")
 _lib = None
 
 OK = 0
