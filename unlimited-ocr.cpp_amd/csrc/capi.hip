@@ -193,10 +193,14 @@ struct WsPlan {
     int slots, max_tiles, bm;
 };
 
+// Prefill (LDS-tiled MFMA GEMM, 128-slot m-tiles) once experts see enough
+// tokens to fill its tiles; the decode kernels (16-slot tiles, weights streamed
+// once per tile) below that.
+constexpr int kPrefillMinSeq = 256;
+
 bool use_prefill(const uocr_hip_moe_layer* L, int seq) {
     (void)L;
-    (void)seq;
-    return false;
+    return seq >= kPrefillMinSeq;
 }
 
 WsPlan plan(const uocr_hip_moe_layer* L, int seq) {
