@@ -207,7 +207,8 @@ WsPlan plan(const uocr_hip_moe_layer* L, int seq) {
     WsPlan p{};
     const int Ev = L->n_experts + L->n_virtual;
     p.slots = seq * (L->top_k + L->n_virtual);
-    p.bm = use_prefill(L, seq) ? kPrefillTileRows : kDecodeTileRows;
+    p.bm = !use_prefill(L, seq) ? kDecodeTileRows
+                                : (prefill_big_ok(L->hidden, L->inter) ? kPrefillBigTileRows : kPrefillTileRows);
     p.max_tiles = (seq * L->top_k) / p.bm + L->n_experts + L->n_virtual * ((seq + p.bm - 1) / p.bm) + 1;
     size_t o = 0;
     auto take = [&](size_t bytes) {
@@ -452,6 +453,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     gu.n_rows = L->inter;
     gu.k = L->hidden;
     gu.group = L->group;
+    gu.bm = p.bm;
     gu.slot_tok = g.slot_tok;
     gu.counts = g.counts;
     gu.offsets = g.offsets;

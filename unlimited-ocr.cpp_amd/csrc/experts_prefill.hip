@@ -19,8 +19,9 @@
 
 namespace uocr_hip {
 
-constexpr int kPreBM = kPrefillTileRows;  // 128 slots per m-tile
+constexpr int kPreBM = 128;               // slots per m-tile (generic kernel)
 constexpr int kPreBN = 128;               // weight rows per workgroup
+constexpr int kBigBM = kPrefillBigTileRows; // slots per m-tile (large-tile kernel)
 constexpr int kFragHalfs = 64 * 8;        // f16 per 1 KiB fragment
 
 template <int GPT, bool GU>
@@ -154,10 +155,217 @@ __global__ __launch_bounds__(256) void experts_prefill_kernel(ExpertArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Large-tile variant (K = 896 or 1280): 256 slots x 256 weight rows per
+// workgroup, v_mfma_f32_32x32x16_f16 (the faster gfx950 f16 MFMA shape).
+//   * the 4 waves stack along M (64 slots each) and each covers all 256 weight
+//     rows (8 32-row blocks, 256 accumulator registers), so every activation
+//     byte fetched from L2 feeds 256 output columns and every weight is
+//     dequantised once per workgroup -- one dequant per 8 MFMAs -- into LDS in
+//     32x32x16 B-fragment order, double-buffered one k-tile ahead;
+//   * activation fragments are private to a wave, so they go global ->
+//     registers (gathered through the slot->token list) one k-tile ahead and
+//     never touch LDS;
+//   * the k-tile loop is fully unrolled (exact waits) and blockIdx is remapped
+//     so the n-tiles of one m-tile share an XCD's L2.
+// Output layout of the 32x32x16 MFMA (verified on gfx950): lane l, register r
+// holds C[8 * (r / 4) + 4 * (l / 32) + r % 4][l % 32].
+// ---------------------------------------------------------------------------
+constexpr int kBigBN = 256;  // weight rows per workgroup
+constexpr int kBigNB = kBigBN / 32;
+
+__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+template <int GPT, bool GU, int KT>
+__global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) {
+    // B fragments: [buffer][k-step 0..7][n-block 0..7][64 lanes][8 f16]
+    __shared__ __attribute__((aligned(16))) f16 Bs[2][8 * kBigNB * kFragHalfs];
+    constexpr int K = KT * kTileK;
+    constexpr int NG = scale_row_stride(K, kTileK / GPT);
+    constexpr int UNITS = kBigBN / kTileRows * 64 / 256;  // dequant units per thread (4)
+    const int n_ntiles = GU ? (a.n_rows / (kBigBN / 2)) : (a.n_rows / kBigBN);
+    const int b = blockIdx.x, xcd = b & 7, local = b >> 3;
+    const int tile = (local / n_ntiles) * 8 + xcd, ntile = local % n_ntiles;
+    const int n_tiles = *a.n_tiles;
+    const int tile_c = min(tile, n_tiles > 0 ? n_tiles - 1 : 0);
+    const int e = a.tile_e[tile_c], m0 = a.tile_m0[tile_c];
+    if (tile >= n_tiles) return;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int rows = min(kBigBM, a.counts[e] - m0);
+    const int slot0 = a.offsets[e] + m0;
+
+    // A: wave rows wave*64 + j*32 + lane%32 (j = 0, 1); k offset 8 * (lane / 32) in a k-step
+    const f16* arow[2];
+    bool alive[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int m = wave * 64 + j * 32 + (lane & 31);
+        alive[j] = m < rows;
+        const int slot = slot0 + (alive[j] ? m : 0);
+        const int row = a.gather ? a.slot_tok[slot] : slot;
+        arow[j] = a.a + (size_t)row * K + 8 * (lane >> 5);
+    }
+    // B dequant units: u = tid + 256 i -> local row block rbl = u / 64, tile lane q = u % 64
+    // (GU: row blocks 0..7 are gate rows of the n-tile's 128 act columns, 8..15 the same up rows)
+    const uint8_t* bsrc[UNITS];
+    const f16* ssrc[UNITS];
+    int bdst[UNITS][4];  // LDS f16 offset of each of the unit's four 8-column runs
+#pragma unroll
+    for (int i = 0; i < UNITS; ++i) {
+        const int u = tid + 256 * i, rbl = u >> 6, q = u & 63;
+        int grow;
+        const uint8_t* wbase;
+        const uint16_t* sbase;
+        if constexpr (GU) {
+            grow = ntile * 8 + (rbl & 7);
+            wbase = (rbl < 8 ? a.w0 : a.w1) + (size_t)e * a.w_stride;
+            sbase = (rbl < 8 ? a.s0 : a.s1) + (size_t)e * a.s_stride;
+        } else {
+            grow = ntile * 16 + rbl;
+            wbase = a.w0 + (size_t)e * a.w_stride;
+            sbase = a.s0 + (size_t)e * a.s_stride;
+        }
+        bsrc[i] = wbase + (size_t)grow * KT * kTileBytes + (size_t)q * 16;
+        ssrc[i] = reinterpret_cast<const f16*>(sbase) + (size_t)(grow * kTileRows + (q & 15)) * NG;
+        const int n = rbl * 16 + (q & 15);  // local weight row 0..255
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int kloc = s * 32 + 8 * (q >> 4);  // first column of this run in the k-tile
+            const int ks = kloc >> 4, half = (kloc >> 3) & 1;
+            bdst[i][s] = ((ks * kBigNB + (n >> 5)) * 64 + (n & 31) + 32 * half) * 8;
+        }
+    }
+
+    // raw weights + this k-tile's GPT scales of the unit's row (one load each)
+    u32x4 braw[KT][UNITS];
+    uint32_t bscr[KT][UNITS][(GPT + 1) / 2];
+    auto load_b = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < UNITS; ++i) {
+            braw[kt][i] = *reinterpret_cast<const u32x4*>(bsrc[i] + (size_t)kt * kTileBytes);
+            const f16* sp = ssrc[i] + kt * GPT;
+            if constexpr (GPT == 4) {
+                const u32x2 v = *reinterpret_cast<const u32x2*>(sp);
+                bscr[kt][i][0] = v[0];
+                bscr[kt][i][1] = v[1];
+            } else if constexpr (GPT == 2) {
+                bscr[kt][i][0] = *reinterpret_cast<const uint32_t*>(sp);
+            } else {
+                bscr[kt][i][0] = *reinterpret_cast<const uint16_t*>(sp);
+            }
+        }
+    };
+    auto scale_of = [&](int kt, int i, int s) -> f16 {
+        const int g = (s * GPT) >> 2;  // group within the k-tile
+        const uint32_t w = bscr[kt][i][g >> 1];
+        const uint16_t h = (uint16_t)((g & 1) ? (w >> 16) : (w & 0xffffu));
+        return __builtin_bit_cast(f16, h);
+    };
+    // dequantise unit i of k-tile kt into its LDS buffer
+    auto stage_unit = [&](int kt, int i) {
+        f16* dst = Bs[kt & 1];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            *reinterpret_cast<f16x8*>(dst + bdst[i][s]) = dequant8(braw[kt][i][s], scale2(scale_of(kt, i, s)));
+    };
+    auto stage_b = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < UNITS; ++i) stage_unit(kt, i);
+    };
+    f16x8 areg[KT][2][8];
+    auto load_a = [&](int kt) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks)
+                if (alive[j]) areg[kt][j][ks] = *reinterpret_cast<const f16x8*>(arow[j] + kt * kTileK + ks * 16);
+    };
+
+    f32x16 acc[2][kBigNB];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int nb = 0; nb < kBigNB; ++nb) acc[j][nb] = f32x16{};
+
+    load_a(0);
+    load_b(0);
+    if (KT > 1) load_b(1);
+    stage_b(0);
+    __syncthreads();
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+        if (kt + 1 < KT) load_a(kt + 1);
+        if (kt + 2 < KT) load_b(kt + 2);
+        const f16* Bb = Bs[kt & 1];
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+#pragma unroll
+            for (int nb = 0; nb < kBigNB; ++nb) {
+                const f16x8 bf = *reinterpret_cast<const f16x8*>(Bb + ((size_t)(ks * kBigNB + nb) * 64 + lane) * 8);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[j][nb] = mfma32(areg[kt][j][ks], bf, acc[j][nb]);
+            }
+            // next k-tile's weights go to the other buffer (last read before the
+            // previous barrier), one unit after every other k-step so the VALU
+            // work interleaves with the MFMAs in flight
+            if (kt + 1 < KT && (ks & 1)) stage_unit(kt + 1, ks >> 1);
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = wave * 64 + j * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (m >= rows) continue;
+            const size_t orow = (size_t)(slot0 + m) * a.n_rows;
+            if constexpr (GU) {
+#pragma unroll
+                for (int nb = 0; nb < kBigNB / 2; ++nb) {
+                    const int col = ntile * (kBigBN / 2) + nb * 32 + (lane & 31);
+                    a.act_out[orow + col] = (f16)silu_mul_f(acc[j][nb][r], acc[j][nb + kBigNB / 2][r]);
+                }
+            } else {
+#pragma unroll
+                for (int nb = 0; nb < kBigNB; ++nb) {
+                    const int col = ntile * kBigBN + nb * 32 + (lane & 31);
+                    a.y_out[orow + col] = acc[j][nb][r];
+                }
+            }
+        }
+    }
+}
+
+template <int GPT, bool GU>
+static bool launch_big(const ExpertArgs& a, int max_tiles, hipStream_t st) {
+    const int n_ntiles = GU ? (a.n_rows / (kBigBN / 2)) : (a.n_rows / kBigBN);
+    if (n_ntiles * (GU ? kBigBN / 2 : kBigBN) != a.n_rows) return false;
+    const dim3 grid(((max_tiles + 7) / 8) * 8 * n_ntiles);
+    switch (a.k / kTileK) {
+        case 7: hipLaunchKernelGGL((experts_prefill_big_kernel<GPT, GU, 7>), grid, dim3(256), 0, st, a); return true;
+        case 10: hipLaunchKernelGGL((experts_prefill_big_kernel<GPT, GU, 10>), grid, dim3(256), 0, st, a); return true;
+        default: return false;
+    }
+}
+
 template <bool GU>
 static hipError_t launch_prefill_g(const ExpertArgs& a, int max_tiles, hipStream_t st) {
     const int n_ntiles = GU ? (a.n_rows / (kPreBN / 2)) : (a.n_rows / kPreBN);
     const dim3 grid(max_tiles * n_ntiles);
+    if (a.bm == kBigBM) {
+        bool done = false;
+        switch (a.group) {
+            case 32: done = launch_big<4, GU>(a, max_tiles, st); break;
+            case 64: done = launch_big<2, GU>(a, max_tiles, st); break;
+            case 128: done = launch_big<1, GU>(a, max_tiles, st); break;
+            default: return hipErrorInvalidValue;
+        }
+        return done ? hipGetLastError() : hipErrorInvalidValue;
+    }
+    if (a.bm != kPreBM) return hipErrorInvalidValue;
     switch (a.group) {
         case 32: hipLaunchKernelGGL((experts_prefill_kernel<4, GU>), grid, dim3(256), 0, st, a); break;
         case 64: hipLaunchKernelGGL((experts_prefill_kernel<2, GU>), grid, dim3(256), 0, st, a); break;

@@ -57,6 +57,7 @@ struct ExpertArgs {
     int n_rows;              // output features (N)
     int k;                   // input features (K)
     int group;
+    int bm;                  // slots per m-tile of the tile list
     const int* slot_tok;
     const int* counts;
     const int* offsets;
@@ -80,7 +81,14 @@ struct CombineArgs {
 hipError_t launch_router(const RouterArgs& a, bool x_is_bf16, hipStream_t st);
 size_t router_smem_bytes(int hidden);
 constexpr int kDecodeTileRows = 16;
-constexpr int kPrefillTileRows = 128;
+constexpr int kPrefillTileRows = 128;     // generic prefill kernel
+constexpr int kPrefillBigTileRows = 256;  // large-tile prefill kernel (K in {896, 1280})
+// the large-tile kernel is instantiated for 7 and 10 k-tiles and tiles its
+// output in 128 act columns (gate/up) and 256 hidden columns (down)
+inline bool prefill_big_ok(int hidden, int inter) {
+    return (hidden == 896 || hidden == 1280) && (inter == 896 || inter == 1280) && inter % 128 == 0 &&
+           hidden % 256 == 0;
+}
 hipError_t launch_router_from_logits(const RouterArgs& a, const float* logits, hipStream_t st);
 hipError_t launch_group(const GroupArgs& g, hipStream_t st);
 hipError_t launch_experts_decode(const ExpertArgs& a, bool gate_up, int max_tiles, hipStream_t st);
