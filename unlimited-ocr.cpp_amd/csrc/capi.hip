@@ -190,6 +190,7 @@ int check_qm(const uocr_hip_qmatrix* q, int rows, int cols, int group, const cha
 
 struct WsPlan {
     size_t x16, ids, wts, counts, offsets, ntiles, slot_tok, slot_w, pos, tile_e, tile_m0, act, y, total;
+    size_t lrank, chunk_count, chunk_base;
     int slots, max_tiles, bm;
 };
 
@@ -229,6 +230,10 @@ WsPlan plan(const uocr_hip_moe_layer* L, int seq) {
     p.tile_m0 = take((size_t)p.max_tiles * 4);
     p.act = take((size_t)p.slots * L->inter * 2);
     p.y = take((size_t)p.slots * L->hidden * 4);
+    const int chunks = group_chunks(seq, L->top_k);
+    p.lrank = take((size_t)seq * L->top_k * 4);
+    p.chunk_count = take((size_t)chunks * L->n_experts * 4);
+    p.chunk_base = take((size_t)chunks * L->n_experts * 4);
     p.total = o;
     return p;
 }
@@ -435,6 +440,9 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     g.tile_e = (int*)(ws + p.tile_e);
     g.tile_m0 = (int*)(ws + p.tile_m0);
     g.n_tiles = (int*)(ws + p.ntiles);
+    g.lrank = (int*)(ws + p.lrank);
+    g.chunk_count = (int*)(ws + p.chunk_count);
+    g.chunk_base = (int*)(ws + p.chunk_base);
     HIP_TRY(launch_router(ra, x_dtype == UOCR_HIP_DTYPE_BF16, st), "router launch");
     mark(1);
     HIP_TRY(launch_group(g, st), "group launch");

@@ -117,7 +117,8 @@ struct GroupLds {
     int offs[kMaxExperts + 1];
     int tile0[kMaxExperts + 1];
     int run[kMaxExperts];
-    int wcnt[kGroupWaves][kMaxExperts];
+    int wcnt[kGroupWaves][kMaxExperts];   // per-wave counts of the round
+    int wbase[kGroupWaves][kMaxExperts];  // exclusive per-wave prefix of the round
 };
 
 // Exclusive prefix sum of v[0..n) (n <= 128) by wave 0; out[n] = total.
@@ -185,12 +186,20 @@ __device__ void group_body(const int* ids, const float* wts, const GroupArgs& g,
     for (int e = tid; e < kMaxExperts; e += kGroupThreads) s.run[e] = 0;
     __syncthreads();
     // stable placement of the routed entries, kGroupThreads entries per round
+    // (entry i = base + tid, so lane order, then wave order, is (t, j) order)
     const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int nid = (tid < N) ? ids[tid] : -1;
+    float nw = (tid < N) ? wts[tid] : 0.0f;
     for (int base = 0; base < N; base += kGroupThreads) {
-        for (int i = tid; i < kGroupWaves * kMaxExperts; i += kGroupThreads) (&s.wcnt[0][0])[i] = 0;
-        __syncthreads();
         const int i = base + tid;
-        const int e = (i < N) ? ids[i] : -1;
+        const int e = nid;
+        const float w = nw;
+        if (base + kGroupThreads + tid < N) {  // next round's entry, in flight during this round
+            nid = ids[base + kGroupThreads + tid];
+            nw = wts[base + kGroupThreads + tid];
+        }
+        for (int k = tid; k < kGroupWaves * kMaxExperts; k += kGroupThreads) (&s.wcnt[0][0])[k] = 0;
+        __syncthreads();
         const bool valid = e >= 0 && e < E;
         uint64_t m = __ballot(valid);
 #pragma unroll
@@ -202,19 +211,17 @@ __device__ void group_body(const int* ids, const float* wts, const GroupArgs& g,
         const int rank = __popcll(m & below);
         if (valid && rank == 0) s.wcnt[wave][e] = __popcll(m);
         __syncthreads();
-        for (int ee = tid; ee < E; ee += kGroupThreads) {
+        // exclusive prefix over waves, one thread per (wave, expert)
+        for (int ee = lane; ee < E; ee += 64) {
             int acc = s.run[ee];
-            for (int w = 0; w < kGroupWaves; ++w) {
-                const int c = s.wcnt[w][ee];
-                s.wcnt[w][ee] = acc;
-                acc += c;
-            }
-            s.run[ee] = acc;
+            for (int w2 = 0; w2 < wave; ++w2) acc += s.wcnt[w2][ee];
+            s.wbase[wave][ee] = acc;
         }
         __syncthreads();
+        if (wave == kGroupWaves - 1)
+            for (int ee = lane; ee < E; ee += 64) s.run[ee] = s.wbase[wave][ee] + s.wcnt[wave][ee];
         if (valid) {
-            const int r = s.wcnt[wave][e] + rank;  // position within expert e
-            const float w = wts[i];
+            const int r = s.wbase[wave][e] + rank;  // position within expert e
             if (g.slot_tok) {
                 const int sl = s.offs[e] + r;
                 g.slot_tok[sl] = i / g.top_k;
@@ -242,6 +249,119 @@ __device__ void group_body(const int* ids, const float* wts, const GroupArgs& g,
 __global__ __launch_bounds__(kGroupThreads) void group_kernel(GroupArgs g) {
     __shared__ GroupLds s;
     group_body(g.ids, g.weights, g, s);
+}
+
+// ---------------------------------------------------------------------------
+// Multi-workgroup stable grouping for large batches: three launches, each of
+// which finishes all of its loads before its first store (on gfx9 the vmcnt
+// wait for a load also waits for every earlier store).
+//   rank:  per 1024-entry chunk, stable rank of each entry among the chunk's
+//          entries of the same expert + the chunk's per-expert counts;
+//   scan:  expert totals, offsets, tile list and per-(chunk, expert) bases;
+//   place: slot = base[chunk][expert] + rank.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kGroupThreads) void group_rank_kernel(GroupArgs g) {
+    __shared__ int wcnt[kGroupWaves][kMaxExperts];
+    __shared__ int wbase[kGroupWaves][kMaxExperts];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int E = g.n_experts, N = g.seq * g.top_k;
+    const int i = blockIdx.x * kGroupThreads + tid;
+    const int e = (i < N) ? g.ids[i] : -1;
+    for (int k = tid; k < kGroupWaves * kMaxExperts; k += kGroupThreads) (&wcnt[0][0])[k] = 0;
+    __syncthreads();
+    const bool valid = e >= 0 && e < E;
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    uint64_t m = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 7; ++b) {
+        const bool bit = valid && ((e >> b) & 1);
+        const uint64_t bal = __ballot(bit);
+        m &= bit ? bal : ~bal;
+    }
+    const int rank = __popcll(m & below);
+    if (valid && rank == 0) wcnt[wave][e] = __popcll(m);
+    __syncthreads();
+    for (int ee = lane; ee < E; ee += 64) {
+        int acc = 0;
+        for (int w2 = 0; w2 < wave; ++w2) acc += wcnt[w2][ee];
+        wbase[wave][ee] = acc;
+    }
+    __syncthreads();
+    if (i < N) g.lrank[i] = valid ? wbase[wave][e] + rank : 0;
+    if (wave == kGroupWaves - 1)
+        for (int ee = lane; ee < E; ee += 64)
+            g.chunk_count[(size_t)blockIdx.x * E + ee] = wbase[wave][ee] + wcnt[wave][ee];
+}
+
+__global__ __launch_bounds__(kGroupThreads) void group_scan_kernel(GroupArgs g, int n_chunks) {
+    extern __shared__ int cc[];  // [n_chunks][E] counts, then bases
+    __shared__ int hist[kMaxExperts], offs[kMaxExperts + 1], ntl[kMaxExperts], tile0[kMaxExperts + 1];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int E = g.n_experts, Ev = E + g.n_virtual;
+    for (int k = tid; k < n_chunks * E; k += kGroupThreads) cc[k] = g.chunk_count[k];
+    __syncthreads();
+    for (int e = tid; e < Ev; e += kGroupThreads) {
+        int acc = 0;
+        if (e < E)
+            for (int c = 0; c < n_chunks; ++c) {
+                const int v = cc[c * E + e];
+                cc[c * E + e] = acc;  // exclusive base within expert e
+                acc += v;
+            }
+        else
+            acc = g.seq;
+        hist[e] = acc;
+        ntl[e] = (acc + g.bm - 1) / g.bm;
+    }
+    __syncthreads();
+    if (wave == 0) wave0_exclusive_scan(hist, offs, Ev);
+    if (wave == 1) wave0_exclusive_scan(ntl, tile0, Ev);
+    __syncthreads();
+    for (int k = tid; k < n_chunks * E; k += kGroupThreads) g.chunk_base[k] = cc[k] + (g.slot_tok ? offs[k % E] : 0);
+    for (int e = tid; e < Ev; e += kGroupThreads) {
+        if (g.counts) {
+            g.counts[e] = hist[e];
+            g.offsets[e] = offs[e];
+        }
+        if (g.assign_count && e < E) g.assign_count[e] = min(hist[e], g.cap);
+    }
+    if (tid == 0 && g.counts) g.offsets[Ev] = offs[Ev];
+    if (g.tile_e) {
+        if (tid == 0) *g.n_tiles = tile0[Ev];
+        for (int e = wave; e < Ev; e += kGroupWaves) {
+            const int nt = tile0[e + 1] - tile0[e];
+            for (int m = lane; m < nt; m += 64) {
+                g.tile_e[tile0[e] + m] = e;
+                g.tile_m0[tile0[e] + m] = m * g.bm;
+            }
+        }
+    }
+    // virtual (shared-expert) groups: every token, weight 1
+    if (g.slot_tok)
+        for (int v = 0; v < g.n_virtual; ++v)
+            for (int t = tid; t < g.seq; t += kGroupThreads) {
+                g.slot_tok[offs[E + v] + t] = t;
+                g.slot_w[offs[E + v] + t] = 1.0f;
+            }
+}
+
+__global__ __launch_bounds__(256) void group_place_kernel(GroupArgs g) {
+    const int E = g.n_experts, N = g.seq * g.top_k;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N) return;
+    const int e = g.ids[i];
+    if (e < 0 || e >= E) return;
+    const int r = g.chunk_base[(size_t)(i / kGroupThreads) * E + e] + g.lrank[i];
+    const float w = g.weights[i];
+    if (g.slot_tok) {  // r is the slot (bases include the expert offset)
+        g.slot_tok[r] = i / g.top_k;
+        g.slot_w[r] = w;
+        if (g.pos) g.pos[i] = r;
+    }
+    if (g.assign_token && r < g.cap) {  // r is the position within expert e
+        g.assign_token[(size_t)e * g.cap + r] = i / g.top_k;
+        g.assign_w[(size_t)e * g.cap + r] = w;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -500,8 +620,24 @@ hipError_t launch_router_from_logits(const RouterArgs& a, const float* logits, h
     return hipGetLastError();
 }
 
+int group_chunks(int seq, int top_k) { return (seq * top_k + kGroupThreads - 1) / kGroupThreads; }
+
 hipError_t launch_group(const GroupArgs& g, hipStream_t st) {
-    hipLaunchKernelGGL(group_kernel, dim3(1), dim3(kGroupThreads), 0, st, g);
+    const int n_chunks = group_chunks(g.seq, g.top_k);
+    if (n_chunks <= 1 || !g.lrank) {
+        hipLaunchKernelGGL(group_kernel, dim3(1), dim3(kGroupThreads), 0, st, g);
+        return hipGetLastError();
+    }
+    if (g.slot_tok && g.assign_token) return hipErrorInvalidValue;  // bases are slots or positions, not both
+    hipLaunchKernelGGL(group_rank_kernel, dim3(n_chunks), dim3(kGroupThreads), 0, st, g);
+    const size_t lds = (size_t)n_chunks * g.n_experts * sizeof(int);
+    if (lds > 96 * 1024) return hipErrorInvalidValue;
+    static hipError_t attr = hipFuncSetAttribute((const void*)group_scan_kernel,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL(group_scan_kernel, dim3(1), dim3(kGroupThreads), lds, st, g, n_chunks);
+    const int n = g.seq * g.top_k;
+    hipLaunchKernelGGL(group_place_kernel, dim3((n + 255) / 256), dim3(256), 0, st, g);
     return hipGetLastError();
 }
 
