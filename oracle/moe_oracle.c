@@ -157,7 +157,12 @@ void orc_matmul_int4(const orc_qmatrix* q, const float* x, float* y, int m) {
     }
 }
 
-/* src/kernels/cpu_ops.cpp:11-24 (row-parallel above 2^18 MACs; per-output sequential FMA chain) */
+/* src/kernels/cpu_ops.cpp:11-24 (row-parallel above 2^18 MACs; per-output sequential chain).
+ * Unlike matmul_t_bf16, the reference build does NOT contract this loop: GCC 11
+ * -O3 -march=native vectorises the products (vmulps, 8 then 4 lanes) and adds them in order
+ * (vaddss), so each step is round(acc + round(x * w)); only the scalar tail
+ * of k % 4 terms is fused (vfmadd231ss). Pinned bit-exact against
+ * oracle/_ref and tests/golden/ref_vectors.npz (mmt_*). */
 void orc_matmul_t(const float* x, const float* w, const float* bias, float* y, int m, int n,
                   int k) {
 #pragma omp parallel for schedule(static) if ((long long)m * n * k > (1 << 18))
@@ -166,7 +171,9 @@ void orc_matmul_t(const float* x, const float* w, const float* bias, float* y, i
             const float* wr = w + (size_t)j * k;
             const float* xr = x + (size_t)i * k;
             float acc = bias ? bias[j] : 0.0f;
-            for (int t = 0; t < k; ++t) acc = fmaf(xr[t], wr[t], acc);
+            const int k4 = k & ~3;
+            for (int t = 0; t < k4; ++t) acc = acc + xr[t] * wr[t];
+            for (int t = k4; t < k; ++t) acc = fmaf(xr[t], wr[t], acc);
             y[(size_t)i * n + j] = acc;
         }
     }
@@ -216,7 +223,12 @@ void orc_rmsnorm(const float* x, const float* w, float* out, int rows, int cols,
     for (int r = 0; r < rows; ++r) {
         const float* xr = x + (size_t)r * cols;
         float ss = 0.0f;
-        for (int c = 0; c < cols; ++c) ss = fmaf(xr[c], xr[c], ss);
+        /* the reference build vectorises x*x (vmulps) and sums in order
+         * (vaddss); the scalar tail of cols % 4 terms is fused (vfmadd231ss).
+         * Pinned against oracle/_ref and tests/golden (rms_*). */
+        const int c4 = cols & ~3;
+        for (int c = 0; c < c4; ++c) ss = ss + xr[c] * xr[c];
+        for (int c = c4; c < cols; ++c) ss = fmaf(xr[c], xr[c], ss);
         const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
         float* o = out + (size_t)r * cols;
         for (int c = 0; c < cols; ++c) o[c] = xr[c] * inv * w[c];
@@ -330,8 +342,10 @@ static void layer_token(const orc_layer* L, const float* x, const float* h, cons
         orc_routed_expert(L, x, acc, ids[j]);
         for (int d = 0; d < H; ++d) moe[d] = fmaf(w[j], acc[d], moe[d]);
     }
-    orc_mlp(&L->shared_gate, &L->shared_up, &L->shared_down, x, sh, 1);
-    for (int d = 0; d < H; ++d) moe[d] += sh[d];
+    if (L->shared_inter > 0) { /* add_rows(out, shared) (moe_decoder.cpp:110-112) */
+        orc_mlp(&L->shared_gate, &L->shared_up, &L->shared_down, x, sh, 1);
+        for (int d = 0; d < H; ++d) moe[d] += sh[d];
+    }
     if (h)
         for (int d = 0; d < H; ++d) out_row[d] = h[d] + moe[d];
     else

@@ -202,3 +202,71 @@ def moe_layer(L, h, sel=None, threads=1):
         s = np.ascontiguousarray(sel, np.int32)
         lib().orc_moe_layer(C.byref(lc), h, seq, s.ctypes.data, len(s), threads, ids, w, out)
     return ids, w, out
+
+
+def bf16_to_f32(h):
+    return lib().orc_bf16_to_f32(int(h))
+
+
+def f32_to_bf16(f):
+    return lib().orc_f32_to_bf16(float(f))
+
+
+def qmatrix_at(q, r, c):
+    qc, keep = qmat_c(q)
+    return lib().orc_qmatrix_at(C.byref(qc), r, c)
+
+
+def _quantize(fn, w, group):
+    w = np.ascontiguousarray(w, np.float32)
+    rows, cols = w.shape
+    ng = (cols + group - 1) // group
+    packed = np.empty((rows, (cols + 1) // 2), np.uint8)
+    scales = np.empty((rows, ng), np.float32)
+    zeros = np.empty((rows, ng), np.float32)
+    fn(w, rows, cols, group, packed, scales, zeros)
+    return packed, scales, zeros
+
+
+def quantize_int4_awq(w, group):
+    return _quantize(lib().orc_quantize_int4_awq, w, group)
+
+
+def quantize_int4_symmetric(w, group):
+    return _quantize(lib().orc_quantize_int4_symmetric, w, group)
+
+
+def matmul_t(x, w, bias=None):
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    m, k = x.shape
+    n = w.shape[0]
+    y = np.empty((m, n), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib().orc_matmul_t(x, w, None if b is None else b.ctypes.data, y, m, n, k)
+    return y
+
+
+def matmul_t_bf16(x, w_bits, bias=None):
+    x = np.ascontiguousarray(x, np.float32)
+    w_bits = np.ascontiguousarray(w_bits, np.uint16)
+    m, k = x.shape
+    n = w_bits.shape[0]
+    y = np.empty((m, n), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib().orc_matmul_t_bf16(x, w_bits, None if b is None else b.ctypes.data, y, m, n, k)
+    return y
+
+
+def softmax(x):
+    y = np.array(x, np.float32, copy=True, order="C")
+    lib().orc_softmax(y, y.shape[0], y.shape[1])
+    return y
+
+
+def silu_mul(g, u):
+    g = np.ascontiguousarray(g, np.float32)
+    u = np.ascontiguousarray(u, np.float32)
+    o = np.empty_like(g)
+    lib().orc_silu_mul(g, u, o, g.size)
+    return o
