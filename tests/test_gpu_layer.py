@@ -82,6 +82,41 @@ def test_config3_prefill_t4096_zipf(dev):
     assert counts.max() > 1000, counts  # the skew the config asks for
 
 
+def test_config4_rmsnorm_residual_t64(dev):
+    """Config 4's layer form: out = h + moe(rmsnorm(h)) with f32 h, 64 tokens;
+    the second layer takes the oracle's f32 output of the first (not bf16-valued)."""
+    import oracle as O
+    from uocr_hip import synth
+    w = synth.make_config(4, n_layers=2)
+    check_parity(w.layers[0], w.x, dev, dtype="f32", label="cfg4-l0")
+    _, _, h1 = O.moe_layer(w.layers[0], w.x, threads=16)
+    check_parity(w.layers[1], h1, dev, dtype="f32", label="cfg4-l1")
+
+
+@pytest.mark.parametrize("seq", [2, 63, 64, 65, 100, 255])
+def test_decode_batch_sizes(dev, seq):
+    """Both decode routers (one workgroup per token up to 64 tokens, LDS-shared
+    router weights above) and the multi-m-tile expert loop (up to 16 tiles)."""
+    from uocr_hip import synth
+    L = synth.random_layer(500 + seq, group=32)
+    x = synth.bf16_normal(np.random.default_rng(seq), (seq, L.hidden), 1.0)
+    check_parity(L, x, dev, sample=24, label=f"decode-t{seq}")
+
+
+def test_decode_group64_and_one_hot_expert(dev):
+    """group 64, and a router that sends every token to the same experts
+    (one expert with the whole batch: 48 tokens = 3 m-tiles)."""
+    from uocr_hip import synth
+    L = synth.random_layer(77, group=64)
+    rb = L.router_bf16.copy()
+    rb[:, 0] = synth.f32_to_bf16_bits(np.linspace(-8.0, 8.0, 64, dtype=np.float32))
+    L.router_bf16 = rb
+    x = synth.bf16_normal(np.random.default_rng(1), (48, L.hidden), 1.0)
+    x[:, 0] = 64.0
+    ids, _, _ = check_parity(L, x, dev, label="decode-onehot")
+    assert (ids[:, 0] == 63).all()
+
+
 def test_permutation_bit_exact(dev):
     """Grouped slot order equals the reference host grouping
     (gpu_decoder.cu:602-609): checked through the mirror router's

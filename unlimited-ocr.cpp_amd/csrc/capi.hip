@@ -13,11 +13,6 @@
 #include "launch.hpp"
 #include "uocr_hip/moe_capi.h"
 
-extern "C" {
-extern const uint32_t uocr_expf_fix_entries[];
-extern const uint32_t uocr_expf_fix_count;
-extern const uint32_t uocr_expf_fix_offsets[65537];
-}
 
 using namespace uocr_hip;
 
@@ -39,35 +34,6 @@ int hip_fail(hipError_t e, const char* what) {
         hipError_t _e = (expr);                     \
         if (_e != hipSuccess) return hip_fail(_e, what); \
     } while (0)
-
-struct FixTables {
-    uint32_t* offsets = nullptr;
-    uint32_t* entries = nullptr;
-};
-
-std::mutex g_fix_mu;
-std::map<int, FixTables> g_fix;
-
-// Device copy of the expf fix-up table, once per device.
-int fix_tables(FixTables* out) {
-    int dev = 0;
-    HIP_TRY(hipGetDevice(&dev), "hipGetDevice");
-    std::lock_guard<std::mutex> lk(g_fix_mu);
-    auto it = g_fix.find(dev);
-    if (it != g_fix.end()) {
-        *out = it->second;
-        return UOCR_HIP_OK;
-    }
-    FixTables t;
-    const size_t ob = sizeof(uint32_t) * 65537, eb = sizeof(uint32_t) * (uocr_expf_fix_count + 1);
-    HIP_TRY(hipMalloc(&t.offsets, ob), "hipMalloc(expf fix offsets)");
-    HIP_TRY(hipMalloc(&t.entries, eb), "hipMalloc(expf fix entries)");
-    HIP_TRY(hipMemcpy(t.offsets, uocr_expf_fix_offsets, ob, hipMemcpyHostToDevice), "copy fix offsets");
-    HIP_TRY(hipMemcpy(t.entries, uocr_expf_fix_entries, eb, hipMemcpyHostToDevice), "copy fix entries");
-    g_fix[dev] = t;
-    *out = t;
-    return UOCR_HIP_OK;
-}
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
@@ -147,6 +113,7 @@ struct uocr_hip_moe_layer {
     float scaling = 1.0f, rms_eps = 1e-6f;
     int device = 0;
     uint16_t* router_t = nullptr;
+    float* router_f32 = nullptr;  // [hidden/4][64][4] (decode router)
     float* rms_weight = nullptr;
     uint8_t* gate = nullptr;   // [Ev][inter x hidden] tile layout
     uint8_t* up = nullptr;
@@ -156,7 +123,6 @@ struct uocr_hip_moe_layer {
     uint16_t* down_s = nullptr;
     long long gu_wstride = 0, gu_sstride = 0, dn_wstride = 0, dn_sstride = 0;
     size_t device_bytes = 0;
-    FixTables fix;
     bool timing = false;
     hipEvent_t ev[6] = {};
     float stage_ms[5] = {};
@@ -168,7 +134,7 @@ namespace {
 
 void free_layer(uocr_hip_moe_layer* L) {
     if (!L) return;
-    void* ptrs[] = {L->router_t, L->rms_weight, L->gate, L->up, L->down, L->gate_s, L->up_s, L->down_s};
+    void* ptrs[] = {L->router_t, L->router_f32, L->rms_weight, L->gate, L->up, L->down, L->gate_s, L->up_s, L->down_s};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     for (auto& e : L->ev)
@@ -198,6 +164,9 @@ struct WsPlan {
 // tokens to fill its tiles; the decode kernels (16-slot tiles, weights streamed
 // once per tile) below that.
 constexpr int kPrefillMinSeq = 256;
+// one workgroup per token in the router up to this batch (the router matrix is
+// then read once per token from L2); larger batches share it through LDS
+constexpr int kRouterDecodeMaxSeq = 64;
 
 bool use_prefill(const uocr_hip_moe_layer* L, int seq) {
     (void)L;
@@ -252,7 +221,7 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
     const int H = d->hidden, I = d->inter, E = d->n_experts;
     if (H <= 0 || I <= 0 || H % kTileK || I % kTileK)
         return fail(UOCR_HIP_EINVAL, "hidden and inter must be positive multiples of 128");
-    if (router_smem_bytes(H) > 160 * 1024 || H > 1792 || I > 1792)
+    if (router_smem_bytes(H) > 150 * 1024 || H > 1792 || I > 1792)
         return fail(UOCR_HIP_EUNSUPPORTED, "hidden/inter above 1792 are not supported by this build");
     if (E <= 0 || E > 64) return fail(UOCR_HIP_EINVAL, "n_experts must be in [1, 64]");
     if (d->top_k <= 0 || d->top_k > kMaxTopK || d->top_k > E)
@@ -285,10 +254,6 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
     L->scoring_sigmoid = d->scoring_sigmoid;
     L->scaling = d->routed_scaling_factor;
     L->rms_eps = d->rms_eps;
-    if ((rc = fix_tables(&L->fix))) {
-        free_layer(L);
-        return rc;
-    }
     (void)hipGetDevice(&L->device);
 
     const int Ev = E + S;
@@ -340,6 +305,16 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
         for (int e = 0; e < E; ++e)
             for (int i = 0; i < 8; ++i) rt[((size_t)c8 * E + e) * 8 + i] = d->router_bf16[(size_t)e * H + c8 * 8 + i];
 
+    // and as f32 [H/4][64][4] for the decode router (experts padded to 64 with
+    // zeros, so a 64-column chunk is one contiguous 16 KiB block)
+    std::vector<float> rf((size_t)H * 64, 0.0f);
+    for (int c4 = 0; c4 < H / 4; ++c4)
+        for (int e = 0; e < E; ++e)
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t bits = (uint32_t)d->router_bf16[(size_t)e * H + c4 * 4 + i] << 16;
+                std::memcpy(&rf[((size_t)c4 * 64 + e) * 4 + i], &bits, 4);
+            }
+
     auto up_copy = [&](void** dst, const void* src, size_t bytes, const char* what) -> int {
         hipError_t e = hipMalloc(dst, bytes);
         if (e != hipSuccess) return fail(UOCR_HIP_ENOMEM, std::string("hipMalloc(") + what + "): " + hipGetErrorString(e));
@@ -349,6 +324,7 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
         return UOCR_HIP_OK;
     };
     if ((rc = up_copy((void**)&L->router_t, rt.data(), rt.size() * 2, "router")) ||
+        (rc = up_copy((void**)&L->router_f32, rf.data(), rf.size() * 4, "router f32")) ||
         (rc = up_copy((void**)&L->gate, hg.data(), hg.size(), "gate")) ||
         (rc = up_copy((void**)&L->up, hu.data(), hu.size(), "up")) ||
         (rc = up_copy((void**)&L->down, hd.data(), hd.size(), "down")) ||
@@ -406,6 +382,70 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     };
 
     mark(0);
+    if (!use_prefill(L, seq) && decode_shapes_ok(L->hidden, L->inter)) {
+        DecodeArgs da{};
+        da.x = x;
+        da.x_bf16 = x_dtype == UOCR_HIP_DTYPE_BF16;
+        da.seq = seq;
+        da.hidden = L->hidden;
+        da.inter = L->inter;
+        da.n_experts = L->n_experts;
+        da.top_k = L->top_k;
+        da.n_virtual = L->n_virtual;
+        da.group = L->group;
+        da.rms_weight = L->rms_weight;
+        da.rms_eps = L->rms_eps;
+        da.router_f32 = L->router_f32;
+        da.norm_topk_prob = L->norm_topk_prob;
+        da.scoring_sigmoid = L->scoring_sigmoid;
+        da.scaling = L->scaling;
+        da.x16 = x16;
+        da.ids = ids;
+        da.wts = wts;
+        da.gate = L->gate;
+        da.up = L->up;
+        da.down = L->down;
+        da.gate_s = L->gate_s;
+        da.up_s = L->up_s;
+        da.down_s = L->down_s;
+        da.gu_wstride = L->gu_wstride;
+        da.gu_sstride = L->gu_sstride;
+        da.dn_wstride = L->dn_wstride;
+        da.dn_sstride = L->dn_sstride;
+        da.act = (f16*)(ws + p.act);
+        da.y = (float*)(ws + p.y);
+        da.out = out;
+        if (seq <= kRouterDecodeMaxSeq) {
+            HIP_TRY(launch_router_decode(da, st), "router launch");
+        } else {
+            RouterArgs ra{};
+            ra.x = x;
+            ra.seq = seq;
+            ra.hidden = L->hidden;
+            ra.n_experts = L->n_experts;
+            ra.top_k = L->top_k;
+            ra.rms_weight = L->rms_weight;
+            ra.rms_eps = L->rms_eps;
+            ra.router_t = L->router_t;
+            ra.norm_topk_prob = L->norm_topk_prob;
+            ra.scoring_sigmoid = L->scoring_sigmoid;
+            ra.scaling = L->scaling;
+            ra.x16 = x16;
+            ra.ids = ids;
+            ra.weights = wts;
+            HIP_TRY(launch_router(ra, x_dtype == UOCR_HIP_DTYPE_BF16, st), "router launch");
+        }
+        mark(1);
+        mark(2);
+        HIP_TRY(launch_experts_decode2(da, true, st), "gate/up launch");
+        mark(3);
+        HIP_TRY(launch_experts_decode2(da, false, st), "down launch");
+        mark(4);
+        HIP_TRY(launch_combine_decode(da, st), "combine launch");
+        mark(5);
+        if (timing) Lm->pending = true;
+        return UOCR_HIP_OK;
+    }
     RouterArgs ra{};
     ra.x = x;
     ra.seq = seq;
@@ -418,8 +458,6 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     ra.norm_topk_prob = L->norm_topk_prob;
     ra.scoring_sigmoid = L->scoring_sigmoid;
     ra.scaling = L->scaling;
-    ra.fix_offsets = L->fix.offsets;
-    ra.fix_entries = L->fix.entries;
     ra.x16 = x16;
     ra.ids = ids;
     ra.weights = wts;
@@ -544,9 +582,6 @@ int uocr_hip_moe_router_topk(const float* logits, int seq, int n_experts, int to
     if (seq < 0 || n_experts < 0 || n_experts > kMaxExperts || top_k <= 0 || top_k > kMaxTopK || top_k > n_experts ||
         cap <= 0)
         return fail(UOCR_HIP_EINVAL, "bad shape (n_experts <= 128, 1 <= top_k <= min(8, n_experts), cap > 0)");
-    FixTables ft;
-    int rc;
-    if ((rc = fix_tables(&ft))) return rc;
     hipStream_t st = (hipStream_t)stream;
     RouterArgs ra{};
     ra.seq = seq;
@@ -555,8 +590,6 @@ int uocr_hip_moe_router_topk(const float* logits, int seq, int n_experts, int to
     ra.norm_topk_prob = norm_topk_prob;
     ra.scoring_sigmoid = scoring_sigmoid;
     ra.scaling = scaling;
-    ra.fix_offsets = ft.offsets;
-    ra.fix_entries = ft.entries;
     ra.ids = d_ids;
     ra.weights = d_weights;
     HIP_TRY(launch_router_from_logits(ra, logits, st), "router launch");

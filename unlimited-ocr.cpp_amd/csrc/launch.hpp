@@ -18,8 +18,6 @@ struct RouterArgs {
     const uint16_t* router_t; // router W as [hidden/8][n_experts][8] bf16
     int norm_topk_prob, scoring_sigmoid;
     float scaling;
-    const uint32_t* fix_offsets;
-    const uint32_t* fix_entries;
     f16* x16;                 // out [seq, hidden] f16 expert input
     int* ids;                 // out [seq, top_k]
     float* weights;           // out [seq, top_k]
@@ -81,6 +79,36 @@ struct CombineArgs {
     float* out;            // [seq, hidden]
     int seq, hidden, top_k, n_experts, n_virtual;
 };
+
+// Decode-sized layer (seq < 256): router_decode / expert passes / combine with
+// slots derived from the routing ids inside each workgroup.
+struct DecodeArgs {
+    const void* x;             // [seq, hidden] bf16 bits or f32 (f32 when rms_weight)
+    int x_bf16;
+    int seq, hidden, inter, n_experts, top_k, n_virtual, group;
+    const float* rms_weight;   // optional [hidden]; also selects out = x + moe
+    float rms_eps;
+    const float* router_f32;   // [hidden/4][64][4], experts padded to 64
+    int norm_topk_prob, scoring_sigmoid;
+    float scaling;
+    f16* x16;                  // [seq, hidden]
+    int* ids;                  // [seq, top_k]
+    float* wts;                // [seq, top_k]
+    const uint8_t* gate;       // [E + n_virtual] tile layout
+    const uint8_t* up;
+    const uint8_t* down;
+    const uint16_t* gate_s;
+    const uint16_t* up_s;
+    const uint16_t* down_s;
+    long long gu_wstride, gu_sstride, dn_wstride, dn_sstride;
+    f16* act;                  // [slots, inter]
+    float* y;                  // [slots, hidden]
+    float* out;                // [seq, hidden]
+};
+bool decode_shapes_ok(int hidden, int inter);
+hipError_t launch_router_decode(const DecodeArgs& a, hipStream_t st);
+hipError_t launch_experts_decode2(const DecodeArgs& a, bool gate_up, hipStream_t st);
+hipError_t launch_combine_decode(const DecodeArgs& a, hipStream_t st);
 
 hipError_t launch_router(const RouterArgs& a, bool x_is_bf16, hipStream_t st);
 size_t router_smem_bytes(int hidden);

@@ -5,8 +5,10 @@
 //   logits   src/kernels/cpu_ops.cpp:26-39 -- one sequential fmaf chain per
 //            (token, expert), k ascending (the -march=native build contracts
 //            `acc += x * w`); one lane per expert runs exactly that chain.
-//   rmsnorm  src/kernels/cpu_ops.cpp:58-67 -- sequential fmaf chain for the sum
-//            of squares, correctly rounded divide and sqrt, (x * inv) * w.
+//   rmsnorm  src/kernels/cpu_ops.cpp:58-67 -- as the reference's -O3
+//            -march=native build runs it: each x*x rounded, summed in column
+//            order (only a scalar tail of H % 4 terms would be fused),
+//            correctly rounded divide and sqrt, (x * inv) * w.
 //   softmax  src/kernels/cpu_ops.cpp:93-106 -- exp(l - max) with glibc's expf
 //            bits (correctly rounded exp + the generated fix-up table), sum in
 //            expert order, p = e * (1 / sum).
@@ -16,51 +18,9 @@
 //            ascending (token, j) order: a stable counting sort, built here from
 //            wave ballots (equal-expert masks) and per-wave LDS prefix counts.
 #include "launch.hpp"
+#include "routing.hpp"
 
 namespace uocr_hip {
-
-__device__ __forceinline__ float apply_expf_fix(float x, float y, const uint32_t* __restrict__ offs,
-                                                const uint32_t* __restrict__ ent) {
-    const uint32_t b = __float_as_uint(x);
-    uint32_t lo = offs[b >> 16], hi = offs[(b >> 16) + 1];
-    const uint32_t key = b & 0xffffu;
-    while (lo < hi) {  // entries of one bucket are sorted by their low 16 bits
-        const uint32_t mid = (lo + hi) >> 1;
-        const uint32_t v = ent[mid];
-        const uint32_t k = v & 0xffffu;
-        if (k == key) {
-            const uint32_t yb = __float_as_uint(y);
-            return __uint_as_float((v >> 16) ? yb + 1u : yb - 1u);
-        }
-        if (k < key) lo = mid + 1;
-        else hi = mid;
-    }
-    return y;
-}
-
-// glibc expf bits: correctly rounded exp, corrected from the fix-up table only
-// when the binary64 value sits within 1/256 ulp of a rounding midpoint.
-__device__ __forceinline__ float ref_expf(float x, const uint32_t* offs, const uint32_t* ent) {
-    if (x != x) return x;
-    if (x > 88.72283935546875f) return INFINITY;
-    if (x < -103.97208404541015625f) return 0.0f;
-    const double yd = uocr_uexp_d(x);
-    const float y = (float)yd;
-    return uocr_uexpf_near_tie_d(yd) ? apply_expf_fix(x, y, offs, ent) : y;
-}
-
-// Greedy top-k of the reference (strict '>' scan, first maximum wins,
-// moe_decoder.cpp:264-277) selects experts in order of (p descending, index
-// ascending); lane e's position in that order is the number of experts that
-// beat it. p[] holds the scores in LDS; returns the rank of `pe` (lane e).
-__device__ __forceinline__ int greedy_rank(const float* p, int E, int e, float pe) {
-    int rank = 0;
-    for (int j = 0; j < E; ++j) {
-        const float q = p[j];
-        rank += (q > pe || (q == pe && j < e)) ? 1 : 0;
-    }
-    return rank;
-}
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -395,6 +355,8 @@ __global__ __launch_bounds__(WAVES * 64) void router_kernel(RouterArgs a) {
     u32x4* wb = reinterpret_cast<u32x4*>(smem + (size_t)WAVES * H * 4);
     float* scr = reinterpret_cast<float*>(wb + 2 * kChunkC8 * 64) + wave * 64;
     float* topv = reinterpret_cast<float*>(wb + 2 * kChunkC8 * 64) + WAVES * 64 + wave * 16;
+    __shared__ uint64_t etab[32];
+    if (threadIdx.x < 32) etab[threadIdx.x] = uocr_exp2_tab[threadIdx.x];
     const int t = blockIdx.x * WAVES + wave;
     const bool live = t < a.seq;
     const XT* x = static_cast<const XT*>(a.x);
@@ -433,16 +395,15 @@ __global__ __launch_bounds__(WAVES * 64) void router_kernel(RouterArgs a) {
             float ss = 0.0f;
             for (int c = 0; c < H; c += 4) {
                 const f32x4 v = *reinterpret_cast<const f32x4*>(xs + c);
-                ss = fmaf(v[0], v[0], ss);
-                ss = fmaf(v[1], v[1], ss);
-                ss = fmaf(v[2], v[2], ss);
-                ss = fmaf(v[3], v[3], ss);
+                // the reference build rounds each x*x and sums in order (H % 4 == 0 here)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) ss = __fadd_rn(ss, __fmul_rn(v[i], v[i]));
             }
-            scr[0] = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)H) + a.rms_eps));
+            scr[0] = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)H), a.rms_eps)));
         }
         __syncthreads();
         const float inv = scr[0];
-        for (int c = lane; c < H; c += 64) xs[c] = xs[c] * inv * a.rms_weight[c];
+        for (int c = lane; c < H; c += 64) xs[c] = __fmul_rn(__fmul_rn(xs[c], inv), a.rms_weight[c]);
         __syncthreads();
     }
 
@@ -490,10 +451,10 @@ __global__ __launch_bounds__(WAVES * 64) void router_kernel(RouterArgs a) {
     // scoring (softmax over experts in index order, or sigmoid)
     float p;
     if (a.scoring_sigmoid) {
-        p = __fdiv_rn(1.0f, 1.0f + ref_expf(-acc, a.fix_offsets, a.fix_entries));
+        p = __fdiv_rn(1.0f, 1.0f + ref_expf(-acc, etab));
     } else {
         const float mx = wave_max(lane < E ? acc : -INFINITY);
-        const float ev = ref_expf(acc - mx, a.fix_offsets, a.fix_entries);
+        const float ev = ref_expf(acc - mx, etab);
         scr[lane] = ev;
         __syncthreads();
         float sum = 0.0f;
@@ -528,17 +489,20 @@ __global__ __launch_bounds__(256) void router_from_logits_kernel(RouterArgs a, c
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int E = a.n_experts, K = a.top_k;
     float* row = lds + (size_t)wave * E;
+    __shared__ uint64_t etab[32];
+    if (threadIdx.x < 32) etab[threadIdx.x] = uocr_exp2_tab[threadIdx.x];
+    __syncthreads();
     const int t = blockIdx.x * (blockDim.x >> 6) + wave;
     const bool live = t < a.seq;
     const float* src = logits + (size_t)(live ? t : 0) * E;
     if (a.scoring_sigmoid) {
         for (int e = lane; e < E; e += 64)
-            row[e] = __fdiv_rn(1.0f, 1.0f + ref_expf(-src[e], a.fix_offsets, a.fix_entries));
+            row[e] = __fdiv_rn(1.0f, 1.0f + ref_expf(-src[e], etab));
     } else {
         float mx = -INFINITY;
         for (int e = lane; e < E; e += 64) mx = fmaxf(mx, src[e]);
         mx = wave_max(mx);
-        for (int e = lane; e < E; e += 64) row[e] = ref_expf(src[e] - mx, a.fix_offsets, a.fix_entries);
+        for (int e = lane; e < E; e += 64) row[e] = ref_expf(src[e] - mx, etab);
         __syncthreads();
         float sum = 0.0f;
         for (int e = 0; e < E; ++e) sum += row[e];
@@ -589,7 +553,7 @@ template <typename XT, bool RMS, int WAVES>
 static hipError_t launch_router_t(const RouterArgs& a, hipStream_t st) {
     // > 64 KiB of dynamic LDS: raise the limit once per kernel
     static hipError_t attr = hipFuncSetAttribute((const void*)router_kernel<XT, RMS, WAVES>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
     if (attr != hipSuccess) return attr;
     const dim3 grid((a.seq + WAVES - 1) / WAVES);
     hipLaunchKernelGGL((router_kernel<XT, RMS, WAVES>), grid, dim3(WAVES * 64), router_lds_bytes(a.hidden, WAVES),
