@@ -60,17 +60,17 @@ __device__ __forceinline__ int greedy_rank(const float* p, int E, int e, float p
 // The same rank over exactly 64 scores in LDS (16-byte aligned): the reads are
 // independent 16-byte broadcasts, issued together.
 __device__ __forceinline__ int greedy_rank64(const float* p, int e, float pe) {
-    int rank = 0;
+    int part[4] = {0, 0, 0, 0};  // four independent counting chains
 #pragma unroll
     for (int j4 = 0; j4 < 16; ++j4) {
         const f32x4 q = reinterpret_cast<const f32x4*>(p)[j4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int j = 4 * j4 + i;
-            rank += (q[i] > pe || (q[i] == pe && j < e)) ? 1 : 0;
+            part[i] += (q[i] > pe || (q[i] == pe && j < e)) ? 1 : 0;
         }
     }
-    return rank;
+    return (part[0] + part[1]) + (part[2] + part[3]);
 }
 
 // sum of p[0..E) in index order (E <= 64; p 16-byte aligned, zero-padded to 64)
