@@ -117,6 +117,16 @@ def test_decode_group64_and_one_hot_expert(dev):
     assert (ids[:, 0] == 63).all()
 
 
+@pytest.mark.parametrize("seq", [10, 300])
+def test_other_shapes_prefill_kernels(dev, seq):
+    """Shapes outside the decode instantiations (inter 384 = 3 k-tiles) run on
+    the grouped prefill kernels at any batch; 16 experts, top-4, one shared."""
+    from uocr_hip import synth
+    L = synth.random_layer(900 + seq, hidden=512, inter=384, n_experts=16, top_k=4, n_shared=1, group=128)
+    x = synth.bf16_normal(np.random.default_rng(seq), (seq, 512), 1.0)
+    check_parity(L, x, dev, sample=32, label=f"shape512x384-t{seq}")
+
+
 def test_permutation_bit_exact(dev):
     """Grouped slot order equals the reference host grouping
     (gpu_decoder.cu:602-609): checked through the mirror router's

@@ -168,9 +168,11 @@ constexpr int kPrefillMinSeq = 256;
 // then read once per token from L2); larger batches share it through LDS
 constexpr int kRouterDecodeMaxSeq = 64;
 
+// Decode path (per-token router, grouping-free expert passes) below
+// kPrefillMinSeq tokens for the layer shapes it is instantiated for; the
+// prefill path (grouped LDS-tiled MFMA GEMM) otherwise.
 bool use_prefill(const uocr_hip_moe_layer* L, int seq) {
-    (void)L;
-    return seq >= kPrefillMinSeq;
+    return seq >= kPrefillMinSeq || !decode_shapes_ok(L->hidden, L->inter);
 }
 
 WsPlan plan(const uocr_hip_moe_layer* L, int seq) {
@@ -382,7 +384,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     };
 
     mark(0);
-    if (!use_prefill(L, seq) && decode_shapes_ok(L->hidden, L->inter)) {
+    if (!use_prefill(L, seq)) {
         DecodeArgs da{};
         da.x = x;
         da.x_bf16 = x_dtype == UOCR_HIP_DTYPE_BF16;
@@ -486,7 +488,6 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     HIP_TRY(launch_group(g, st), "group launch");
     mark(2);
 
-    const bool pre = use_prefill(L, seq);
     ExpertArgs gu{};
     gu.a = x16;
     gu.gather = 1;
@@ -507,7 +508,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     gu.tile_m0 = g.tile_m0;
     gu.n_tiles = g.n_tiles;
     gu.act_out = (f16*)(ws + p.act);
-    HIP_TRY(pre ? launch_experts_prefill(gu, true, p.max_tiles, st) : launch_experts_decode(gu, true, p.max_tiles, st),
+    HIP_TRY(launch_experts_prefill(gu, true, p.max_tiles, st),
             "gate/up launch");
     mark(3);
 
@@ -524,7 +525,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     dn.k = L->inter;
     dn.act_out = nullptr;
     dn.y_out = (float*)(ws + p.y);
-    HIP_TRY(pre ? launch_experts_prefill(dn, false, p.max_tiles, st) : launch_experts_decode(dn, false, p.max_tiles, st),
+    HIP_TRY(launch_experts_prefill(dn, false, p.max_tiles, st),
             "down launch");
     mark(4);
 

@@ -124,7 +124,6 @@ inline bool prefill_big_ok(int hidden, int inter) {
 hipError_t launch_router_from_logits(const RouterArgs& a, const float* logits, hipStream_t st);
 hipError_t launch_group(const GroupArgs& g, hipStream_t st);
 int group_chunks(int seq, int top_k);  // 1024-entry chunks of the multi-workgroup grouping
-hipError_t launch_experts_decode(const ExpertArgs& a, bool gate_up, int max_tiles, hipStream_t st);
 hipError_t launch_experts_prefill(const ExpertArgs& a, bool gate_up, int max_tiles, hipStream_t st);
 hipError_t launch_combine(const CombineArgs& c, hipStream_t st);
 
