@@ -7,9 +7,11 @@ on the next of R distinct weight replicas, so the ~128 MB layer is streamed
 from HBM rather than from the 256 MB Infinity Cache.
 
 Roofline: the dominant kernel is the fused gate/up expert pass. Its average
-duration comes from HIP events that libuocr_hip records around that launch on
-the layer's stream (uocr_hip_moe_layer_set_timing) over the same steps;
-achieved = algorithmic bytes per launch / that duration.
+duration comes from HIP events stamped on that kernel's own dispatch
+(hipExtLaunchKernelGGL start/stop events on the layer's stream, enabled by
+uocr_hip_moe_layer_set_timing) over a second pass of the same steps;
+achieved = algorithmic bytes per launch / that duration. traffic = HBM bytes per
+launch from the committed rocprofv3 --pmc summary under profiles/.
 
 Extra configs (0, 2, 3, 4) are reported under "configs" in the same line.
 cpu_baseline: the CPU oracle (a restatement of the reference's CPU path) on the
@@ -131,7 +133,7 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False):
             n += c
         for lay in layers:
             lay.set_timing(False)
-        stage = {k: v / max(n, 1) for k, v in tot.items()}
+        stage = {k: v / max(n, 1) for k, v in tot.items() if v > 0}
 
     torch.cuda.synchronize()
     counts = [np.bincount(t.cpu().numpy().ravel(), minlength=64) for t in ids]
@@ -181,6 +183,34 @@ def cpu_baseline(seconds=10.0):
             "sample": f"config 1 layer (16 tokens, all routed+shared experts) x{n} runs, {dt:.1f}s"}
 
 
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "expert_gate_up_decode_config1_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per gate/up launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel calibration it
+    records); None when the summary is absent."""
+    try:
+        for ln in open(TRAFFIC_SUMMARY):
+            if ln.startswith("traffic_bytes_per_launch:"):
+                return float(ln.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def copy_probe(nbytes, reps=5):
+    """A plain device copy of `nbytes` bytes, `reps` times: the calibration
+    kernel for the FETCH_SIZE / WRITE_SIZE counters (reads and writes nbytes)."""
+    import torch
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda:0").fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": nbytes, "reps": reps}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -189,7 +219,12 @@ def main():
     ap.add_argument("--replicas", type=int, default=6)
     ap.add_argument("--extra", default="0,2,3,4", help="extra configs to report ('' = none)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only run a plain copy of BYTES bytes (counter calibration)")
     args = ap.parse_args()
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the MoE path is benchmarked on a "
               "single MI355X; multi-GPU expert parallelism is design-only)", file=sys.stderr)
@@ -223,9 +258,9 @@ def main():
         "config": {"workload": "config1_decode_t16_g32", "tokens": 16, "hidden": 1280,
                    "experts": "64 routed top-6 + 2 shared", "inter": 896, "group": 32,
                    "weight_replicas": args.replicas},
-        "roofline": {"bound": "hbm", "kernel": "experts_decode_kernel (gate+up)",
+        "roofline": {"bound": "hbm", "kernel": "expert_decode_kernel<4, 10, true> (gate+up)",
                      "achieved": main_res["gate_up_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": main_res["gate_up_gbs"] / HBM_PEAK_GBS, "traffic": None,
+                     "frac": main_res["gate_up_gbs"] / HBM_PEAK_GBS, "traffic": measured_traffic(),
                      "avg_launch_ms": gu_ms, "algorithmic_bytes": main_res["gate_up_bytes"]},
         "layer_hbm_frac": main_res["layer_hbm_gbs"] / HBM_PEAK_GBS,
         "stage_ms": main_res["stage_ms"],

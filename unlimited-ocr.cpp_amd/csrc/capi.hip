@@ -16,6 +16,11 @@
 
 using namespace uocr_hip;
 
+uocr_hip::StageEvents& uocr_hip::stage_events() {
+    thread_local StageEvents e;
+    return e;
+}
+
 namespace {
 
 thread_local std::string g_err;
@@ -124,7 +129,8 @@ struct uocr_hip_moe_layer {
     long long gu_wstride = 0, gu_sstride = 0, dn_wstride = 0, dn_sstride = 0;
     size_t device_bytes = 0;
     bool timing = false;
-    hipEvent_t ev[6] = {};
+    hipEvent_t ev[10] = {};    // start/stop per stage
+    unsigned stage_mask = 0;   // stages the pending call recorded
     float stage_ms[5] = {};
     int timed_calls = 0;
     bool pending = false;
@@ -379,11 +385,18 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     f16* x16 = (f16*)(ws + p.x16);
     auto* Lm = const_cast<uocr_hip_moe_layer*>(L);
     const bool timing = L->timing;
-    auto mark = [&](int i) {
-        if (timing) (void)hipEventRecord(Lm->ev[i], st);
+    // stages: 0 router, 1 grouping, 2 gate/up, 3 down, 4 combine; stage(-1) ends timing
+    if (timing) Lm->stage_mask = 0;
+    auto stage = [&](int i) {
+        if (!timing) return;
+        stage_events() = i < 0 ? StageEvents{} : StageEvents{Lm->ev[2 * i], Lm->ev[2 * i + 1]};
+        if (i >= 0) Lm->stage_mask |= 1u << i;
     };
 
-    mark(0);
+    struct Disarm {  // an early error return must not leave later launches armed
+        ~Disarm() { stage_events() = StageEvents{}; }
+    } disarm_on_exit;
+    stage(0);
     if (!use_prefill(L, seq)) {
         DecodeArgs da{};
         da.x = x;
@@ -437,14 +450,13 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
             ra.weights = wts;
             HIP_TRY(launch_router(ra, x_dtype == UOCR_HIP_DTYPE_BF16, st), "router launch");
         }
-        mark(1);
-        mark(2);
+        stage(2);
         HIP_TRY(launch_experts_decode2(da, true, st), "gate/up launch");
-        mark(3);
+        stage(3);
         HIP_TRY(launch_experts_decode2(da, false, st), "down launch");
-        mark(4);
+        stage(4);
         HIP_TRY(launch_combine_decode(da, st), "combine launch");
-        mark(5);
+        stage(-1);
         if (timing) Lm->pending = true;
         return UOCR_HIP_OK;
     }
@@ -484,9 +496,9 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     g.chunk_count = (int*)(ws + p.chunk_count);
     g.chunk_base = (int*)(ws + p.chunk_base);
     HIP_TRY(launch_router(ra, x_dtype == UOCR_HIP_DTYPE_BF16, st), "router launch");
-    mark(1);
+    stage(1);
     HIP_TRY(launch_group(g, st), "group launch");
-    mark(2);
+    stage(2);
 
     ExpertArgs gu{};
     gu.a = x16;
@@ -510,7 +522,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     gu.act_out = (f16*)(ws + p.act);
     HIP_TRY(launch_experts_prefill(gu, true, p.max_tiles, st),
             "gate/up launch");
-    mark(3);
+    stage(3);
 
     ExpertArgs dn = gu;
     dn.a = gu.act_out;
@@ -527,7 +539,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     dn.y_out = (float*)(ws + p.y);
     HIP_TRY(launch_experts_prefill(dn, false, p.max_tiles, st),
             "down launch");
-    mark(4);
+    stage(4);
 
     CombineArgs c{};
     c.y = dn.y_out;
@@ -542,7 +554,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     c.n_experts = L->n_experts;
     c.n_virtual = L->n_virtual;
     HIP_TRY(launch_combine(c, st), "combine launch");
-    mark(5);
+    stage(-1);
     if (timing) Lm->pending = true;
     return UOCR_HIP_OK;
 }
@@ -550,7 +562,9 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
 int uocr_hip_moe_layer_set_timing(uocr_hip_moe_layer* L, int enable) {
     if (!L) return fail(UOCR_HIP_EINVAL, "null layer");
     if (enable && !L->ev[0])
-        for (auto& e : L->ev) HIP_TRY(hipEventCreate(&e), "hipEventCreate");
+        // no system-scope fence: a fenced event adds microseconds of cache
+        // maintenance to the interval it closes
+        for (auto& e : L->ev) HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableSystemFence), "hipEventCreate");
     L->timing = enable != 0;
     return UOCR_HIP_OK;
 }
@@ -558,10 +572,11 @@ int uocr_hip_moe_layer_set_timing(uocr_hip_moe_layer* L, int enable) {
 int uocr_hip_moe_layer_read_timing(uocr_hip_moe_layer* L, float* stage_ms, int n_stages, int* n_calls) {
     if (!L || !stage_ms) return fail(UOCR_HIP_EINVAL, "null argument");
     if (L->pending) {
-        HIP_TRY(hipEventSynchronize(L->ev[5]), "hipEventSynchronize");
         for (int i = 0; i < 5; ++i) {
+            if (!(L->stage_mask >> i & 1)) continue;
             float ms = 0.0f;
-            HIP_TRY(hipEventElapsedTime(&ms, L->ev[i], L->ev[i + 1]), "hipEventElapsedTime");
+            HIP_TRY(hipEventSynchronize(L->ev[2 * i + 1]), "hipEventSynchronize");
+            HIP_TRY(hipEventElapsedTime(&ms, L->ev[2 * i], L->ev[2 * i + 1]), "hipEventElapsedTime");
             L->stage_ms[i] += ms;
         }
         L->timed_calls++;

@@ -40,7 +40,7 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs c) {
 
 hipError_t launch_combine(const CombineArgs& c, hipStream_t st) {
     if (c.seq <= 0) return hipSuccess;
-    hipLaunchKernelGGL(combine_kernel, dim3(c.seq), dim3(256), 0, st, c);
+    launch_k(combine_kernel, dim3(c.seq), dim3(256), 0, st, c);
     return hipGetLastError();
 }
 

@@ -781,7 +781,7 @@ static void launch_expert(const DecodeArgs& a, int n_groups, int n_rows, hipStre
         return std::max(1, cus * std::max(1, per_cu));
     }();
     const int max_items = n_groups * ((n_rows / kTileRows + 3) / 4);
-    hipLaunchKernelGGL((expert_decode_kernel<GPT, KT, GU>), dim3(std::min(resident, max_items)), dim3(256), 0, st, a);
+    launch_k((expert_decode_kernel<GPT, KT, GU>), dim3(std::min(resident, max_items)), dim3(256), 0, st, a);
 }
 
 template <bool GU, int GPT>
@@ -825,7 +825,7 @@ static hipError_t launch_rd(const DecodeArgs& a, dim3 grid, size_t lds, hipStrea
     static hipError_t attr = hipFuncSetAttribute((const void*)router_decode_kernel<XT, RMS>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL((router_decode_kernel<XT, RMS>), grid, dim3(256), lds, st, a);
+    launch_k((router_decode_kernel<XT, RMS>), grid, dim3(256), lds, st, a);
     return hipGetLastError();
 }
 
@@ -849,7 +849,7 @@ hipError_t launch_experts_decode2(const DecodeArgs& a, bool gate_up, hipStream_t
 }
 
 hipError_t launch_combine_decode(const DecodeArgs& a, hipStream_t st) {
-    hipLaunchKernelGGL(combine_decode_kernel, dim3(a.seq), dim3(256), 0, st, a);
+    launch_k(combine_decode_kernel, dim3(a.seq), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

@@ -345,8 +345,8 @@ static bool launch_big(const ExpertArgs& a, int max_tiles, hipStream_t st) {
     if (n_ntiles * (GU ? kBigBN / 2 : kBigBN) != a.n_rows) return false;
     const dim3 grid(((max_tiles + 7) / 8) * 8 * n_ntiles);
     switch (a.k / kTileK) {
-        case 7: hipLaunchKernelGGL((experts_prefill_big_kernel<GPT, GU, 7>), grid, dim3(256), 0, st, a); return true;
-        case 10: hipLaunchKernelGGL((experts_prefill_big_kernel<GPT, GU, 10>), grid, dim3(256), 0, st, a); return true;
+        case 7: launch_k((experts_prefill_big_kernel<GPT, GU, 7>), grid, dim3(256), 0, st, a); return true;
+        case 10: launch_k((experts_prefill_big_kernel<GPT, GU, 10>), grid, dim3(256), 0, st, a); return true;
         default: return false;
     }
 }
@@ -367,9 +367,9 @@ static hipError_t launch_prefill_g(const ExpertArgs& a, int max_tiles, hipStream
     }
     if (a.bm != kPreBM) return hipErrorInvalidValue;
     switch (a.group) {
-        case 32: hipLaunchKernelGGL((experts_prefill_kernel<4, GU>), grid, dim3(256), 0, st, a); break;
-        case 64: hipLaunchKernelGGL((experts_prefill_kernel<2, GU>), grid, dim3(256), 0, st, a); break;
-        case 128: hipLaunchKernelGGL((experts_prefill_kernel<1, GU>), grid, dim3(256), 0, st, a); break;
+        case 32: launch_k((experts_prefill_kernel<4, GU>), grid, dim3(256), 0, st, a); break;
+        case 64: launch_k((experts_prefill_kernel<2, GU>), grid, dim3(256), 0, st, a); break;
+        case 128: launch_k((experts_prefill_kernel<1, GU>), grid, dim3(256), 0, st, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

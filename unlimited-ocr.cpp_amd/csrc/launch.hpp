@@ -1,11 +1,33 @@
 // Kernel argument blocks and host-side launchers (internal to libuocr_hip).
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 
 #include "common.hpp"
 
 namespace uocr_hip {
+
+// Per-stage kernel timing. While a stage is armed, every launch goes through
+// hipExtLaunchKernelGGL, which stamps the kernel's own dispatch: the start
+// event on the stage's first launch, the stop event on each launch (the last
+// one wins). These are the timestamps a kernel trace reports, without the
+// gaps that separate hipEventRecord markers add. Unarmed launches are plain.
+struct StageEvents {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+StageEvents& stage_events();  // thread-local
+
+template <typename F, typename... Args>
+inline void launch_k(F kernel, dim3 grid, dim3 block, uint32_t lds, hipStream_t st, Args... args) {
+    StageEvents& ev = stage_events();
+    if (ev.stop) {
+        hipExtLaunchKernelGGL(kernel, grid, block, lds, st, ev.start, ev.stop, 0, args...);
+        ev.start = nullptr;
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
+    }
+}
 
 constexpr int kMaxExperts = 128;  // routed + virtual (shared-expert) groups
 constexpr int kMaxTopK = 8;

@@ -556,7 +556,7 @@ static hipError_t launch_router_t(const RouterArgs& a, hipStream_t st) {
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
     if (attr != hipSuccess) return attr;
     const dim3 grid((a.seq + WAVES - 1) / WAVES);
-    hipLaunchKernelGGL((router_kernel<XT, RMS, WAVES>), grid, dim3(WAVES * 64), router_lds_bytes(a.hidden, WAVES),
+    launch_k((router_kernel<XT, RMS, WAVES>), grid, dim3(WAVES * 64), router_lds_bytes(a.hidden, WAVES),
                        st, a);
     return hipGetLastError();
 }
@@ -580,7 +580,7 @@ hipError_t launch_router_from_logits(const RouterArgs& a, const float* logits, h
     const int waves = 4;
     const dim3 grid((a.seq + waves - 1) / waves);
     const size_t lds = (size_t)waves * a.n_experts * sizeof(float);
-    hipLaunchKernelGGL(router_from_logits_kernel, grid, dim3(64 * waves), lds, st, a, logits);
+    launch_k(router_from_logits_kernel, grid, dim3(64 * waves), lds, st, a, logits);
     return hipGetLastError();
 }
 
@@ -589,19 +589,19 @@ int group_chunks(int seq, int top_k) { return (seq * top_k + kGroupThreads - 1) 
 hipError_t launch_group(const GroupArgs& g, hipStream_t st) {
     const int n_chunks = group_chunks(g.seq, g.top_k);
     if (n_chunks <= 1 || !g.lrank) {
-        hipLaunchKernelGGL(group_kernel, dim3(1), dim3(kGroupThreads), 0, st, g);
+        launch_k(group_kernel, dim3(1), dim3(kGroupThreads), 0, st, g);
         return hipGetLastError();
     }
     if (g.slot_tok && g.assign_token) return hipErrorInvalidValue;  // bases are slots or positions, not both
-    hipLaunchKernelGGL(group_rank_kernel, dim3(n_chunks), dim3(kGroupThreads), 0, st, g);
+    launch_k(group_rank_kernel, dim3(n_chunks), dim3(kGroupThreads), 0, st, g);
     const size_t lds = (size_t)n_chunks * g.n_experts * sizeof(int);
     if (lds > 96 * 1024) return hipErrorInvalidValue;
     static hipError_t attr = hipFuncSetAttribute((const void*)group_scan_kernel,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL(group_scan_kernel, dim3(1), dim3(kGroupThreads), lds, st, g, n_chunks);
+    launch_k(group_scan_kernel, dim3(1), dim3(kGroupThreads), lds, st, g, n_chunks);
     const int n = g.seq * g.top_k;
-    hipLaunchKernelGGL(group_place_kernel, dim3((n + 255) / 256), dim3(256), 0, st, g);
+    launch_k(group_place_kernel, dim3((n + 255) / 256), dim3(256), 0, st, g);
     return hipGetLastError();
 }
 
