@@ -6,8 +6,10 @@ tokens/s with inputs and weights resident in HBM. Each timed step runs the layer
 on the next of R distinct weight replicas, so the ~128 MB layer is streamed
 from HBM rather than from the 256 MB Infinity Cache.
 
-Roofline: the dominant kernel is the fused gate/up expert pass. Its average
-duration comes from HIP events stamped on that kernel's own dispatch
+Roofline: the dominant kernel is the single fused decode kernel (router,
+experts and combine in one launch; algorithmic bytes = the layer's: touched
+experts' weights + shared expert + router + activations), or, where that path
+does not apply, the gate/up expert pass. Its average duration comes from HIP events stamped on that kernel's own dispatch
 (hipExtLaunchKernelGGL start/stop events on the layer's stream, enabled by
 uocr_hip_moe_layer_set_timing) over a second pass of the same steps;
 achieved = algorithmic bytes per launch / that duration. traffic = HBM bytes per
@@ -151,12 +153,23 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False):
                    layer_hbm_gbs=avg["total"] / (ms * 1e-3) / 1e9,
                    layer_tflops=fl / (ms * 1e-3) / 1e12, stage_ms=stage,
                    gate_up_bytes=avg["gate_up"], gate_up_flops=fl_gu)
-        if stage:
+        if stage and "fused" in stage:
+            # one kernel for the whole layer: its algorithmic bytes are the
+            # layer's (touched experts only, although the dense gate/up pass
+            # reads every expert by design)
+            fu = stage["fused"] * 1e-3
+            res["dominant"] = {"kernel": "decode_fused_kernel<4, 10, 7> (router + experts + combine)",
+                               "ms": stage["fused"], "bytes": avg["total"],
+                               "gbs": avg["total"] / fu / 1e9, "traffic_file": "decode_fused_config1_traffic.md"}
+        elif stage:
             gu = stage["gate_up"] * 1e-3
             res["gate_up_gbs"] = avg["gate_up"] / gu / 1e9
             res["gate_up_tflops"] = fl_gu / gu / 1e12
             res["gate_up_hbm_frac"] = res["gate_up_gbs"] / HBM_PEAK_GBS
             res["gate_up_mfma_frac"] = res["gate_up_tflops"] / MFMA_PEAK_TFLOPS
+            res["dominant"] = {"kernel": "expert_decode_kernel<4, 10, true> (gate+up)", "ms": stage["gate_up"],
+                               "bytes": avg["gate_up"], "gbs": res["gate_up_gbs"],
+                               "traffic_file": "expert_gate_up_decode_config1_traffic.md"}
     for lay in layers:
         lay.close()
     return res
@@ -183,15 +196,12 @@ def cpu_baseline(seconds=10.0):
             "sample": f"config 1 layer (16 tokens, all routed+shared experts) x{n} runs, {dt:.1f}s"}
 
 
-TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "expert_gate_up_decode_config1_traffic.md")
-
-
-def measured_traffic():
-    """HBM bytes per gate/up launch from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel calibration it
-    records); None when the summary is absent."""
+def measured_traffic(name):
+    """HBM bytes per launch of the dominant kernel from its committed
+    rocprofv3 --pmc summary under profiles/ (FETCH_SIZE + WRITE_SIZE, each
+    scaled by the copy-kernel calibration it records); None when absent."""
     try:
-        for ln in open(TRAFFIC_SUMMARY):
+        for ln in open(os.path.join(ROOT, "profiles", name)):
             if ln.startswith("traffic_bytes_per_launch:"):
                 return float(ln.split(":", 1)[1])
     except OSError:
@@ -241,7 +251,7 @@ def main():
             extras[str(c)] = run_config(c, max(args.steps // (10 if c >= 2 else 1), 10),
                                         max(args.warmup // 4, 3), 3 if c >= 2 else args.replicas)
     cpu = None if args.no_cpu else cpu_baseline()
-    gu_ms = main_res["stage_ms"]["gate_up"]
+    dom = main_res["dominant"]
     line = {
         "metric": "INT4 MoE layer tokens/s (batch-16 decode, config 1)",
         "value": main_res["tokens_per_s"],
@@ -258,10 +268,10 @@ def main():
         "config": {"workload": "config1_decode_t16_g32", "tokens": 16, "hidden": 1280,
                    "experts": "64 routed top-6 + 2 shared", "inter": 896, "group": 32,
                    "weight_replicas": args.replicas},
-        "roofline": {"bound": "hbm", "kernel": "expert_decode_kernel<4, 10, true> (gate+up)",
-                     "achieved": main_res["gate_up_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": main_res["gate_up_gbs"] / HBM_PEAK_GBS, "traffic": measured_traffic(),
-                     "avg_launch_ms": gu_ms, "algorithmic_bytes": main_res["gate_up_bytes"]},
+        "roofline": {"bound": "hbm", "kernel": dom["kernel"],
+                     "achieved": dom["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": dom["gbs"] / HBM_PEAK_GBS, "traffic": measured_traffic(dom["traffic_file"]),
+                     "avg_launch_ms": dom["ms"], "algorithmic_bytes": dom["bytes"]},
         "layer_hbm_frac": main_res["layer_hbm_gbs"] / HBM_PEAK_GBS,
         "stage_ms": main_res["stage_ms"],
         "cpu_baseline": cpu,

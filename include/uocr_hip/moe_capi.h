@@ -117,7 +117,8 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* layer, const void* x, i
 /* Per-stage timing of uocr_hip_moe_layer_forward (benchmark support): when
  * enabled, forward records HIP events between its stages on its stream.
  * read_timing synchronizes on the last event and returns the accumulated
- * milliseconds per stage (router, group, gate_up, down, combine) and the
+ * milliseconds per stage (router, group, gate_up, down, combine, fused: the
+ * single-kernel decode path, seq <= 16 with bf16 input) and the
  * number of forwards accumulated; it then resets the totals. */
 int uocr_hip_moe_layer_set_timing(uocr_hip_moe_layer* layer, int enable);
 int uocr_hip_moe_layer_read_timing(uocr_hip_moe_layer* layer, float* stage_ms, int n_stages,

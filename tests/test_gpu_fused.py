@@ -1,0 +1,119 @@
+"""GPU parity of the single-kernel decode path (router + experts + combine in
+one persistent launch; seq <= 16, bf16 input, hidden 1280 / inter 896).
+
+The kernel's workgroups publish per-call progress words that must advance in
+step across calls, so the tests reuse one layer object across batch sizes and
+repeat calls, and replay it from a captured HIP graph. Routing ids / weights
+bit-exact, outputs within rel_l2 <= 5e-3 and max-abs <= 2e-2.
+"""
+import numpy as np
+import pytest
+
+from helpers import MAX_ABS_TOL, REL_L2_TOL, max_abs, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _forward(layer, x_np, dev, ws=None):
+    import torch
+    seq, H = x_np.shape
+    x = torch.from_numpy(x_np).to(dev).to(torch.bfloat16)
+    out = torch.empty(seq, H, dtype=torch.float32, device=dev)
+    ids = torch.empty(seq, layer.top_k, dtype=torch.int32, device=dev)
+    w = torch.empty(seq, layer.top_k, dtype=torch.float32, device=dev)
+    ws = layer.alloc_workspace(seq, dev) if ws is None else ws
+    layer.forward(x, out, ws, ids, w)
+    torch.cuda.synchronize()
+    return ids.cpu().numpy(), w.cpu().numpy(), out.cpu().numpy()
+
+
+def _check(L, x, got, label):
+    import oracle as O
+    ids, w, out = got
+    ids_o, w_o, out_o = O.moe_layer(L, x, threads=16)
+    assert np.array_equal(ids, ids_o), f"{label}: routing ids differ at {np.argwhere(ids != ids_o)[:5]}"
+    assert np.array_equal(w.view(np.uint32), w_o.view(np.uint32)), f"{label}: routing weights not bit-exact"
+    r, m = rel_l2(out, out_o), max_abs(out, out_o)
+    print(f"[fused] {label}: rel_l2={r:.3e} max_abs={m:.3e}", flush=True)
+    assert r <= REL_L2_TOL and m <= MAX_ABS_TOL, label
+
+
+@pytest.mark.parametrize("group", [32, 64, 128])
+def test_fused_batch_sizes_one_layer(dev, group):
+    """Sparse (seq < 12) and dense (seq >= 12) gate/up on one layer object, the
+    batch size changing between calls."""
+    from uocr_hip import MoELayerInt4, synth
+    L = synth.random_layer(4100 + group, group=group)
+    layer = MoELayerInt4(L)
+    for seq in (16, 1, 3, 11, 12, 16, 7):
+        x = synth.bf16_normal(np.random.default_rng(seq * 7 + group), (seq, L.hidden), 1.0)
+        print(f"[fused] group={group} seq={seq}", flush=True)
+        _check(L, x, _forward(layer, x, dev), f"g{group}-t{seq}")
+    layer.close()
+
+
+def test_fused_repeat_deterministic(dev):
+    """Ten calls in a row give bit-identical results (fixed reduction order,
+    progress words advancing every call)."""
+    from uocr_hip import MoELayerInt4, synth
+    L = synth.random_layer(4200)
+    layer = MoELayerInt4(L)
+    x = synth.bf16_normal(np.random.default_rng(5), (16, L.hidden), 1.0)
+    first = _forward(layer, x, dev)
+    _check(L, x, first, "repeat-0")
+    for i in range(9):
+        ids, w, out = _forward(layer, x, dev)
+        assert np.array_equal(ids, first[0]) and np.array_equal(w, first[1])
+        assert np.array_equal(out.view(np.uint32), first[2].view(np.uint32)), f"call {i + 1} differs"
+    layer.close()
+
+
+def test_fused_two_layers_interleaved(dev):
+    """Two layers (separate progress words) called alternately on one workspace."""
+    from uocr_hip import MoELayerInt4, synth
+    La, Lb = synth.random_layer(4300), synth.random_layer(4301)
+    la, lb = MoELayerInt4(La), MoELayerInt4(Lb)
+    x = synth.bf16_normal(np.random.default_rng(9), (14, La.hidden), 1.0)
+    ws = la.alloc_workspace(14, dev)
+    for rep in range(3):
+        _check(La, x, _forward(la, x, dev, ws), f"A{rep}")
+        _check(Lb, x, _forward(lb, x, dev, ws), f"B{rep}")
+    la.close()
+    lb.close()
+
+
+def test_fused_graph_replay(dev):
+    """Captured in a HIP graph and replayed: every replay equals the eager
+    result, with eager work and synchronisations between the replays."""
+    import torch
+    from uocr_hip import MoELayerInt4, synth
+    L = synth.random_layer(4400)
+    layer = MoELayerInt4(L)
+    seq = 16
+    x_np = synth.bf16_normal(np.random.default_rng(11), (seq, L.hidden), 1.0)
+    eager = _forward(layer, x_np, dev)
+    _check(L, x_np, eager, "graph-eager")
+    x = torch.from_numpy(x_np).to(dev).to(torch.bfloat16)
+    out = torch.empty(seq, L.hidden, dtype=torch.float32, device=dev)
+    ids = torch.empty(seq, layer.top_k, dtype=torch.int32, device=dev)
+    w = torch.empty(seq, layer.top_k, dtype=torch.float32, device=dev)
+    ws = layer.alloc_workspace(seq, dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        layer.forward(x, out, ws, ids, w)  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        layer.forward(x, out, ws, ids, w)
+    for rep in range(4):
+        out.fill_(float("nan"))
+        ids.fill_(-1)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(ids.cpu().numpy(), eager[0]), f"replay {rep}: ids"
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), eager[2].view(np.uint32)), f"replay {rep}: out"
+        _forward(layer, x_np, dev)  # eager call between replays
+    layer.close()

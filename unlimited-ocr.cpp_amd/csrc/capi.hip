@@ -3,6 +3,7 @@
 // src/engine/gpu_decoder.cu:537-657, in the reference).
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -112,6 +113,8 @@ int repack(const uocr_hip_qmatrix& q, int row0, int R, int col0, int K, uint8_t*
 
 }  // namespace
 
+constexpr int kStages = 6;  // router, group, gate_up, down, combine, fused
+
 struct uocr_hip_moe_layer {
     int hidden = 0, inter = 0, n_experts = 0, top_k = 0, n_virtual = 0, group = 0;
     int norm_topk_prob = 0, scoring_sigmoid = 0;
@@ -129,9 +132,10 @@ struct uocr_hip_moe_layer {
     long long gu_wstride = 0, gu_sstride = 0, dn_wstride = 0, dn_sstride = 0;
     size_t device_bytes = 0;
     bool timing = false;
-    hipEvent_t ev[10] = {};    // start/stop per stage
-    unsigned stage_mask = 0;   // stages the pending call recorded
-    float stage_ms[5] = {};
+    hipEvent_t ev[2 * kStages] = {};  // start/stop per stage
+    unsigned stage_mask = 0;          // stages the pending call recorded
+    float stage_ms[kStages] = {};
+    FusedSync* sync = nullptr;        // work queue of the fused decode kernel (zero between calls)
     int timed_calls = 0;
     bool pending = false;
 };
@@ -140,7 +144,8 @@ namespace {
 
 void free_layer(uocr_hip_moe_layer* L) {
     if (!L) return;
-    void* ptrs[] = {L->router_t, L->router_f32, L->rms_weight, L->gate, L->up, L->down, L->gate_s, L->up_s, L->down_s};
+    void* ptrs[] = {L->router_t, L->router_f32, L->rms_weight, L->gate,  L->up,
+                    L->down,     L->gate_s,     L->up_s,       L->down_s, L->sync};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     for (auto& e : L->ev)
@@ -181,6 +186,29 @@ bool use_prefill(const uocr_hip_moe_layer* L, int seq) {
     return seq >= kPrefillMinSeq || !decode_shapes_ok(L->hidden, L->inter);
 }
 
+// Fused decode kernel (router + experts + combine in one launch) up to
+// kFusedMaxSeq tokens, bf16 input without the fused RMSNorm; its gate/up pass
+// covers every group for all tokens (no wait for routing) from kDenseMinSeq
+// tokens, where most experts are live anyway (1 - (1 - 6/64)^12 = 69 % at
+// top-6 of 64). UOCR_FUSED=0 / UOCR_DENSE=0|1 override the choice (testing).
+constexpr int kDenseMinSeq = 12;
+
+int env_int(const char* name, int dflt) {
+    const char* e = std::getenv(name);
+    return e ? std::atoi(e) : dflt;
+}
+
+bool use_fused(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
+    static const int on = env_int("UOCR_FUSED", 1);
+    return on && L->sync && seq <= kFusedMaxSeq && x_dtype == UOCR_HIP_DTYPE_BF16 && !L->rms_weight &&
+           decode_fused_ok(L->hidden, L->inter, L->group) && L->n_experts + L->n_virtual <= kMaxExperts;
+}
+
+bool use_dense(int seq) {
+    static const int force = env_int("UOCR_DENSE", -1);
+    return force >= 0 ? force > 0 : seq >= kDenseMinSeq;
+}
+
 WsPlan plan(const uocr_hip_moe_layer* L, int seq) {
     WsPlan p{};
     const int Ev = L->n_experts + L->n_virtual;
@@ -205,7 +233,8 @@ WsPlan plan(const uocr_hip_moe_layer* L, int seq) {
     p.pos = take((size_t)seq * L->top_k * 4);
     p.tile_e = take((size_t)p.max_tiles * 4);
     p.tile_m0 = take((size_t)p.max_tiles * 4);
-    p.act = take((size_t)p.slots * L->inter * 2);
+    // act: one row per slot, or per (group, token) for the fused decode kernel
+    p.act = take((size_t)std::max(p.slots, Ev * seq) * L->inter * 2);
     p.y = take((size_t)p.slots * L->hidden * 4);
     const int chunks = group_chunks(seq, L->top_k);
     p.lrank = take((size_t)seq * L->top_k * 4);
@@ -343,6 +372,15 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
         free_layer(L);
         return rc;
     }
+    {
+        hipError_t e = hipMalloc((void**)&L->sync, sizeof(FusedSync));
+        if (e == hipSuccess) e = hipMemset(L->sync, 0, sizeof(FusedSync));
+        if (e != hipSuccess) {
+            free_layer(L);
+            return hip_fail(e, "fused work queue");
+        }
+        L->device_bytes += sizeof(FusedSync);
+    }
     *out = L;
     return UOCR_HIP_OK;
 }
@@ -385,12 +423,16 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     f16* x16 = (f16*)(ws + p.x16);
     auto* Lm = const_cast<uocr_hip_moe_layer*>(L);
     const bool timing = L->timing;
-    // stages: 0 router, 1 grouping, 2 gate/up, 3 down, 4 combine; stage(-1) ends timing
+    // stages: 0 router, 1 grouping, 2 gate/up, 3 down, 4 combine, 5 fused
+    // decode kernel; stage(-1) ends timing
     if (timing) Lm->stage_mask = 0;
+    // a stage counts once a launch has consumed its start event
+    int cur_stage = -1;
     auto stage = [&](int i) {
         if (!timing) return;
+        if (cur_stage >= 0 && !stage_events().start) Lm->stage_mask |= 1u << cur_stage;
         stage_events() = i < 0 ? StageEvents{} : StageEvents{Lm->ev[2 * i], Lm->ev[2 * i + 1]};
-        if (i >= 0) Lm->stage_mask |= 1u << i;
+        cur_stage = i;
     };
 
     struct Disarm {  // an early error return must not leave later launches armed
@@ -411,6 +453,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
         da.rms_weight = L->rms_weight;
         da.rms_eps = L->rms_eps;
         da.router_f32 = L->router_f32;
+        da.router_t = L->router_t;
         da.norm_topk_prob = L->norm_topk_prob;
         da.scoring_sigmoid = L->scoring_sigmoid;
         da.scaling = L->scaling;
@@ -430,6 +473,15 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
         da.act = (f16*)(ws + p.act);
         da.y = (float*)(ws + p.y);
         da.out = out;
+        if (use_fused(L, seq, x_dtype)) {
+            da.sync = L->sync;
+            da.dense = use_dense(seq);
+            stage(5);
+            HIP_TRY(launch_decode_fused(da, st), "fused decode launch");
+            stage(-1);
+            if (timing) Lm->pending = true;
+            return UOCR_HIP_OK;
+        }
         if (seq <= kRouterDecodeMaxSeq) {
             HIP_TRY(launch_router_decode(da, st), "router launch");
         } else {
@@ -572,7 +624,7 @@ int uocr_hip_moe_layer_set_timing(uocr_hip_moe_layer* L, int enable) {
 int uocr_hip_moe_layer_read_timing(uocr_hip_moe_layer* L, float* stage_ms, int n_stages, int* n_calls) {
     if (!L || !stage_ms) return fail(UOCR_HIP_EINVAL, "null argument");
     if (L->pending) {
-        for (int i = 0; i < 5; ++i) {
+        for (int i = 0; i < kStages; ++i) {
             if (!(L->stage_mask >> i & 1)) continue;
             float ms = 0.0f;
             HIP_TRY(hipEventSynchronize(L->ev[2 * i + 1]), "hipEventSynchronize");
@@ -582,7 +634,7 @@ int uocr_hip_moe_layer_read_timing(uocr_hip_moe_layer* L, float* stage_ms, int n
         L->timed_calls++;
         L->pending = false;
     }
-    for (int i = 0; i < n_stages && i < 5; ++i) stage_ms[i] = L->stage_ms[i];
+    for (int i = 0; i < n_stages && i < kStages; ++i) stage_ms[i] = L->stage_ms[i];
     if (n_calls) *n_calls = L->timed_calls;
     std::memset(L->stage_ms, 0, sizeof(L->stage_ms));
     L->timed_calls = 0;

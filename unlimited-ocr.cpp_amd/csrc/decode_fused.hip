@@ -1,0 +1,590 @@
+// Fused decode layer (seq <= 16, bf16 input, no fused RMSNorm): router, gate/up,
+// down and combine in ONE persistent kernel driven by an atomic work queue.
+//
+// The stand-alone decode path (decode_path.hip) runs four kernels in order. At
+// 16 tokens the router is latency-bound (the reference's sequential fmaf chain
+// per (token, expert), src/kernels/cpu_ops.cpp:26-39) and every kernel boundary
+// drains the chip. Here the queue hands out tickets in dependency order:
+//
+//   [0, T)                 router, one token per workgroup (router_token)
+//   [T, T + G*RBG)         gate/up items (group g, 64 rows): dense mode computes
+//                          every group for all T tokens, so these need no
+//                          routing and stream weights while the router runs;
+//                          sparse mode (few tokens) computes live groups only
+//   [.., + G*RBD)          down items (live group, 64 hidden rows): wait for the
+//                          routing and for the group's gate/up items
+//
+// The workgroup that finishes the last down item of a 64-column block of the
+// output runs the weighted combine of that block (src/engine/moe_decoder.cpp:
+// 88-97, 110-112). A workgroup only ever waits for tickets handed out before
+// its own, which are held by running workgroups, so the queue cannot deadlock
+// whatever the number of resident workgroups; every wait is also bounded
+// (kSpinLimit) and records a timeout in FusedSync::error instead of hanging.
+//
+// Cross-workgroup data (ids / weights, act rows, y rows) is written and read
+// with agent-coherent accesses around counter increments (see load_cg); the
+// counters live in a layer-owned FusedSync that the last workgroup to leave
+// returns to zero.
+//
+// act row of (group g, token t) is g * T + t; y is indexed by entry as in the
+// stand-alone path ((t, j) at t * top_k + j, shared group v at T * top_k + v*T + t).
+#include "decode_common.hpp"
+
+#include <algorithm>
+
+#if defined(UOCR_FTRACE)
+__device__ unsigned long long uocr_ftrace[4096 * 16];
+extern "C" hipError_t uocr_ftrace_read(void* host, size_t bytes) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(uocr_ftrace), bytes, 0, hipMemcpyDeviceToHost);
+}
+extern "C" hipError_t uocr_ftrace_clear() {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(uocr_ftrace));
+    return e != hipSuccess ? e : hipMemset(p, 0, sizeof(unsigned long long) * 4096 * 16);
+}
+#define FTR(i) \
+    if (threadIdx.x == 0) uocr_ftrace[blockIdx.x * 16 + (i)] = wall_clock64();
+#else
+#define FTR(i)
+#endif
+
+namespace uocr_hip {
+
+constexpr int kSpinLimit = 1 << 20;    // bounded waits (~1 s)
+constexpr int kFusedSteps = 1 << 12;   // progress advance per call (> steps of any workgroup)
+
+// Cross-workgroup data moves through agent-coherent accesses (sc1: written
+// through to, and read from, the coherence point shared by every XCD's L2), so
+// publishing needs no L2-wide writeback and reading no L2 invalidation -- both
+// serialise per XCD and cost far more than the few rows exchanged. Publish =
+// the stores, every wave's vmcnt(0) (__syncthreads), then a counter increment;
+// consume = spin on the counter, then the loads. The workgroup-scope fences
+// only keep the compiler from moving accesses across those points.
+__device__ __forceinline__ void fence_wg_release() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup"); }
+__device__ __forceinline__ void fence_wg_acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup"); }
+
+template <typename U>
+__device__ __forceinline__ U load_cg(const U* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename U>
+__device__ __forceinline__ void store_cg(U* p, U v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ f32x4 load4_cg(const float* p) {
+    return f32x4{load_cg(p), load_cg(p + 1), load_cg(p + 2), load_cg(p + 3)};
+}
+__device__ __forceinline__ void store_cg_f16(f16* p, f16 v) {
+    asm volatile("global_store_short %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+// 16-byte global -> LDS DMA, agent-coherent read
+__device__ __forceinline__ void load_lds16_cg(const void* src, void* lds_base) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)lds_base, 16, 0, 16 /* sc1 */);
+}
+
+// LDS of the expert phase (the router phase uses the same bytes for its ring)
+template <int GPT, int KTG, int KTD>
+struct FusedLds {
+    static constexpr int KTM = KTG > KTD ? KTG : KTD;
+    static constexpr int GS = kTileK / GPT;
+    static constexpr int NGG = scale_row_stride(KTG * kTileK, GS);
+    static constexpr int NGD = scale_row_stride(KTD * kTileK, GS);
+    static constexpr int SRM = kTileRows * (NGG > NGD ? NGG : NGD);
+    static constexpr size_t as_bytes = (size_t)KTM * 4 * 64 * 8 * 2;
+    static constexpr size_t ss_bytes = (size_t)4 * 2 * SRM * 2;
+    static constexpr int n_ints = kFusedMaxSeq * kMaxTopK + 2 * kMaxExperts + 4 * 16 + 4;
+    static constexpr size_t bytes = as_bytes + ss_bytes + (size_t)n_ints * 4;
+};
+
+// One wave's 16 rows x KT k-tiles against the staged A rows: four MFMA steps per
+// k-tile, LDS operands read one k-tile ahead (asm reads, explicit lgkmcnt waits).
+template <int GPT, int KT, bool GU>
+__device__ __forceinline__ void item_mma(const u32x4 (&bw0)[KT], const u32x4 (&bw1)[KT], uint32_t a_base,
+                                         uint32_t s_base0, uint32_t s_base1, f32x4& acc0, f32x4& acc1) {
+    TileRegs<GPT> tr[2];
+    lds_issue_tile<GPT>(a_base, s_base0, s_base1, tr[0]);
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+        f16 s0[4], s1[4];
+        if (kt + 1 < KT) {
+            lds_issue_tile<GPT>(a_base + (uint32_t)((kt + 1) * 4096), s_base0 + (uint32_t)((kt + 1) * GPT * 2),
+                                s_base1 + (uint32_t)((kt + 1) * GPT * 2), tr[(kt + 1) & 1]);
+            lds_wait_tile<GPT, 6>(tr[kt & 1], s0, s1);
+        } else {
+            lds_wait_tile<GPT, 0>(tr[kt & 1], s0, s1);
+        }
+        const f16x8* av = tr[kt & 1].av;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            acc0 = mfma16(av[s], dequant8(bw0[kt][s], scale2(s0[s])), acc0);
+            if constexpr (GU) acc1 = mfma16(av[s], dequant8(bw1[kt][s], scale2(s1[s])), acc1);
+        }
+    }
+}
+
+// bf16 token rows DMA'd into As by this lane -> f16 in place (the lane's own
+// 16 bytes of every k-tile; its DMA has landed once the caller has waited)
+template <int KT>
+__device__ __forceinline__ void convert_own_rows(f16* As, int wave, int lane) {
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+        const uint32_t ad = lds_addr(As + (size_t)(kt * 4 + wave) * 64 * 8 + (size_t)lane * 8);
+        u32x4 v;
+        asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(ad) : "memory");
+        f16x8 h;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            h[2 * i] = (f16)__uint_as_float(v[i] << 16);
+            h[2 * i + 1] = (f16)__uint_as_float(v[i] & 0xffff0000u);
+        }
+        asm volatile("ds_write_b128 %0, %1" ::"v"(ad), "v"(h) : "memory");
+    }
+}
+
+// Router of token t with the router matrix held in registers: wave w loads
+// columns [w*SEG, (w+1)*SEG) of lane e's row (bf16, [H/8][E][8]) in one burst
+// at kernel start, then the waves run the reference's sequential fmaf chain
+// (columns ascending, src/kernels/cpu_ops.cpp:26-39) one segment after the
+// other, handing the running sums on through LDS; the last wave scores and
+// selects. No LDS ring and no refills under the weight stream of the other
+// workgroups.
+template <int KT>
+__device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, float* hand, float* sc, float* topv,
+                                                  uint64_t* etab) {
+    constexpr int SEG = KT * 32;  // columns per wave (H = KT * 128)
+    constexpr int NL = SEG / 8;   // 16-byte weight loads per lane
+    constexpr int NX = SEG / 64;  // x blocks of 64 columns per wave
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int E = a.n_experts, H = KT * 128;
+    const int e = lane < E ? lane : 0;
+    const uint16_t* wbase = a.router_t + ((size_t)wave * NL * E + e) * 8;
+    u32x4 wr[NL];
+#pragma unroll
+    for (int i = 0; i < NL; ++i) wr[i] = *reinterpret_cast<const u32x4*>(wbase + (size_t)i * E * 8);
+    // this wave's columns of the token row: lane i of block j holds column
+    // wave*SEG + 64j + i (broadcast with readlane in the chain)
+    const uint16_t* x = static_cast<const uint16_t*>(a.x) + (size_t)t * H + wave * SEG;
+    float xr[NX];
+#pragma unroll
+    for (int j = 0; j < NX; ++j) xr[j] = __uint_as_float((uint32_t)x[64 * j + lane] << 16);
+    if (tid < 32) etab[tid] = uocr_exp2_tab[tid];
+    float acc = 0.0f;
+    for (int w = 0; w < 4; ++w) {
+        if (wave == w) {
+            if (w > 0) acc = hand[lane];
+#pragma unroll
+            for (int i = 0; i < NL; ++i) {
+                u32x4 q = wr[i];
+                asm volatile("" : "+v"(q));  // unpack at the point of use, not hoisted
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    const int col = i * 8 + c;
+                    const float xv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xr[col / 64]), col % 64));
+                    const uint32_t wbits = (c & 1) ? (q[c >> 1] & 0xffff0000u) : (q[c >> 1] << 16);
+                    acc = fmaf(xv, __uint_as_float(wbits), acc);
+                }
+            }
+            if (w < 3) hand[lane] = acc;
+        }
+        lds_barrier();
+    }
+    if (wave == 3) router_select<true>(a, t, acc, sc, topv, etab);
+}
+
+#ifndef UOCR_FUSED_WPE
+#define UOCR_FUSED_WPE 2
+#endif
+template <int GPT, int KTG, int KTD>
+__global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(DecodeArgs a) {
+    using Lay = FusedLds<GPT, KTG, KTD>;
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    f16* As = reinterpret_cast<f16*>(smem);
+    f16* Ss = reinterpret_cast<f16*>(smem + Lay::as_bytes);  // [4 waves][2][SRM]
+    int* ids_s = reinterpret_cast<int*>(smem + Lay::as_bytes + Lay::ss_bytes);
+    int* hist = ids_s + kFusedMaxSeq * kMaxTopK;
+    int* live = hist + kMaxExperts;
+    int* ent = live + kMaxExperts;  // [4 waves][16]
+    int* misc = ent + 4 * 16;       // routed live count
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 15;
+    const int T = a.seq, E = a.n_experts, V = a.n_virtual, G = E + V, K = a.top_k, N = T * K;
+    const int H = a.hidden, I = a.inter;
+    // gate/up items: 64 rows (one 16-row tile per wave); down items: 128 rows
+    // (two tiles per wave, one A staging)
+    const int RBG = (I / kTileRows + 3) / 4, RBD = (H / kTileRows + 7) / 8;
+    const int P = gridDim.x, b = blockIdx.x, PW = P - T;  // PW gate/up workers: T .. P-1
+    FusedSync* sy = a.sync;
+    int* prog = sy->progress;
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const uint16_t* xb = static_cast<const uint16_t*>(a.x);
+
+    // this call's base: every workgroup ended the previous call at the same value
+    const int S = load_cg(prog + b);
+    FTR(0)
+    int ftr = 2;
+    int k = 0;  // steps published by this workgroup
+    auto publish = [&]() {
+        __syncthreads();  // every wave's stores of the step are complete
+        ++k;
+        if (tid == 0) {
+            fence_wg_release();
+            store_cg(prog + b, S + k);
+        }
+    };
+    // wave 0: until, for every lane with want, prog[owner] >= S + step; then the
+    // whole workgroup proceeds
+    auto wait_steps = [&](auto&& pair_of, int n) {
+        if (wave == 0) {
+            for (int base = 0; base < n; base += 64) {
+                int owner = 0, step = 0;
+                const bool want = base + lane < n;
+                if (want) pair_of(base + lane, owner, step);
+                int it = 0;
+                while (__ballot(want && (int)(load_cg(prog + owner) - (S + step)) < 0)) {
+                    if (++it > kSpinLimit) {
+                        if (lane == 0) __hip_atomic_fetch_or(&sy->error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+            }
+        }
+        __syncthreads();
+        fence_wg_acquire();
+    };
+
+    // ---- schedule (identical arithmetic in every workgroup)
+    // gate/up item i -> worker T + i % PW, its step i / PW + 1; down item j ->
+    // workgroup j % P, its step n_router + n_gateup + j / P + 1
+    auto n_gu_of = [&](int w, int ngu_total) {
+        if (w < T) return 0;
+        const int q = w - T;
+        return ngu_total > q ? (ngu_total - 1 - q) / PW + 1 : 0;
+    };
+
+    bool have_summary = false;
+    bool have_x = false;  // As holds all T token rows as f16
+    int n_live_r = 0, n_live = 0;
+
+    // routing summary: counts per expert, live routed experts ascending, then
+    // the shared groups
+    auto need_summary = [&]() {
+        if (have_summary) return;
+        wait_steps([&](int t, int& owner, int& step) { owner = t; step = 1; }, T);
+        for (int e = tid; e < kMaxExperts; e += 256) hist[e] = 0;
+        for (int i = tid; i < N; i += 256) ids_s[i] = load_cg(a.ids + i);
+        __syncthreads();
+        for (int i = tid; i < N; i += 256) atomicAdd(&hist[ids_s[i]], 1);
+        __syncthreads();
+        if (wave == 0) {
+            int run = 0;
+            for (int e0 = 0; e0 < E; e0 += 64) {
+                const int e = e0 + lane;
+                const int c = e < E ? hist[e] : 0;
+                const uint64_t m = __ballot(c > 0);
+                if (c > 0) live[run + __popcll(m & below)] = e;
+                run += __popcll(m);
+            }
+            for (int v = lane; v < V; v += 64) live[run + v] = E + v;
+            if (lane == 0) misc[0] = run;
+        }
+        __syncthreads();
+        n_live_r = misc[0];
+        n_live = n_live_r + V;
+        have_summary = true;
+    };
+
+    // this wave's token list for group g (routed: entries t*K+j ascending;
+    // shared: tokens 0..T-1) -> ent[wave][]; returns the count
+    auto token_list = [&](int g) {
+        int* el = ent + wave * 16;
+        if (g < E) {
+            int run = 0;
+            for (int base = 0; base < N; base += 64) {
+                const int i = base + lane;
+                const bool hit = i < N && ids_s[i] == g;
+                const uint64_t m = __ballot(hit);
+                if (hit) el[run + __popcll(m & below)] = i;
+                run += __popcll(m);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            return run;
+        }
+        if (lane < T) el[lane] = lane;
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        return T;
+    };
+
+    // ---- gate/up item: group g, 64 rows rb*64.. (all_tokens: A = all T rows)
+    auto gate_up_item = [&](int g, int rb, bool all_tokens) {
+        constexpr int KT = KTG;
+        constexpr int NG = Lay::NGG;
+        constexpr int SROW = kTileRows * NG;
+        const int cnt = all_tokens ? T : token_list(g);
+        const int rbw = rb * 4 + wave;
+        const bool wave_live = rbw * kTileRows < I;
+        const int rbl = min(rbw, I / kTileRows - 1);
+        const bool stage = !(all_tokens && have_x);
+        if (stage && r < cnt) {
+            const int tok = all_tokens ? r : ent[wave * 16 + r] / K;
+            const uint16_t* src = xb + (size_t)tok * H + wave * 32 + 8 * (lane >> 4);
+#pragma unroll
+            for (int kt = 0; kt < KT; ++kt) load_lds16(src + kt * kTileK, As + (size_t)(kt * 4 + wave) * 64 * 8);
+        }
+        f16* ssw = Ss + (size_t)wave * 2 * Lay::SRM;
+        const size_t sb = (size_t)g * a.gu_sstride + (size_t)rbl * SROW;
+        for (int q = lane; q * 8 < SROW; q += 64) {
+            load_lds16(a.gate_s + sb + q * 8, ssw + (q & ~63) * 8);
+            load_lds16(a.up_s + sb + q * 8, ssw + Lay::SRM + (q & ~63) * 8);
+        }
+        u32x4 bw0[KT], bw1[KT];
+        const size_t toff = (size_t)g * a.gu_wstride + (size_t)rbl * KT * kTileBytes + (size_t)lane * 16;
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+            bw0[kt] = *reinterpret_cast<const u32x4*>(a.gate + toff + (size_t)kt * kTileBytes);
+            bw1[kt] = *reinterpret_cast<const u32x4*>(a.up + toff + (size_t)kt * kTileBytes);
+        }
+        wait_vm_n(2 * KT);  // A rows and scales (issued before the weights)
+        if (stage) convert_own_rows<KT>(As, wave, lane);
+        lds_barrier();
+        if (wave_live) {
+            f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+            item_mma<GPT, KT, true>(bw0, bw1, lds_addr(As + (size_t)lane * 8), lds_addr(ssw + r * NG),
+                                    lds_addr(ssw + Lay::SRM + r * NG), acc0, acc1);
+            const int col = rbw * kTileRows + r;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int m = 4 * (lane >> 4) + q;
+                if (m < cnt) {
+                    const int tok = all_tokens ? m : ent[wave * 16 + m] / K;
+                    store_cg_f16(a.act + (size_t)(g * T + tok) * I + col, (f16)silu_mul_f(acc0[q], acc1[q]));
+                }
+            }
+        }
+        have_x = all_tokens;
+    };
+
+    // ---- down item: group g, 128 hidden rows rb*128.. (tiles rb*8 + wave and
+    // rb*8 + 4 + wave of this wave)
+    auto down_item = [&](int g, int rb) {
+        constexpr int KT = KTD;
+        constexpr int NG = Lay::NGD;
+        constexpr int SROW = kTileRows * NG;
+        have_x = false;
+        const int cnt = token_list(g);
+        const int rbw0 = rb * 8 + wave, rbw1 = rbw0 + 4;
+        const int rbl0 = min(rbw0, H / kTileRows - 1), rbl1 = min(rbw1, H / kTileRows - 1);
+        if (r < cnt) {
+            const int tok = g < E ? ent[wave * 16 + r] / K : r;
+            const f16* src = a.act + (size_t)(g * T + tok) * I + wave * 32 + 8 * (lane >> 4);
+#pragma unroll
+            for (int kt = 0; kt < KT; ++kt) load_lds16_cg(src + kt * kTileK, As + (size_t)(kt * 4 + wave) * 64 * 8);
+        }
+        f16* ssw = Ss + (size_t)wave * 2 * Lay::SRM;
+        const size_t sb0 = (size_t)g * a.dn_sstride + (size_t)rbl0 * SROW;
+        const size_t sb1 = (size_t)g * a.dn_sstride + (size_t)rbl1 * SROW;
+        for (int q = lane; q * 8 < SROW; q += 64) {
+            load_lds16(a.down_s + sb0 + q * 8, ssw + (q & ~63) * 8);
+            load_lds16(a.down_s + sb1 + q * 8, ssw + Lay::SRM + (q & ~63) * 8);
+        }
+        u32x4 bw0[KT], bw1[KT];
+        const size_t toff0 = (size_t)g * a.dn_wstride + (size_t)rbl0 * KT * kTileBytes + (size_t)lane * 16;
+        const size_t toff1 = (size_t)g * a.dn_wstride + (size_t)rbl1 * KT * kTileBytes + (size_t)lane * 16;
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+            bw0[kt] = *reinterpret_cast<const u32x4*>(a.down + toff0 + (size_t)kt * kTileBytes);
+            bw1[kt] = *reinterpret_cast<const u32x4*>(a.down + toff1 + (size_t)kt * kTileBytes);
+        }
+        wait_vm_n(2 * KT);
+        lds_barrier();
+        if (rbw0 * kTileRows < H) {
+            // the two tiles share the A operand: the gate/up MMA shape
+            f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+            item_mma<GPT, KT, true>(bw0, bw1, lds_addr(As + (size_t)lane * 8), lds_addr(ssw + r * NG),
+                                    lds_addr(ssw + Lay::SRM + r * NG), acc0, acc1);
+            const bool live1 = rbw1 * kTileRows < H;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int m = 4 * (lane >> 4) + q;
+                if (m < cnt) {
+                    const int yrow = g < E ? ent[wave * 16 + m] : N + (g - E) * T + m;
+                    store_cg(a.y + (size_t)yrow * H + rbw0 * kTileRows + r, acc0[q]);
+                    if (live1) store_cg(a.y + (size_t)yrow * H + rbw1 * kTileRows + r, acc1[q]);
+                }
+            }
+        }
+    };
+
+    // ---- combine of output columns rb*128 .. rb*128+127 for every token
+    // (src/engine/moe_decoder.cpp:88-97, 110-112). One agent-scope acquire
+    // (an L2 invalidation) and then plain vector loads: cheaper here than a
+    // coherent load per element.
+    auto combine_block = [&](int rb) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        const int t = tid >> 4;
+        for (int c = rb * 128 + (tid & 15) * 4; c < min(rb * 128 + 128, H) && t < T; c += 64) {
+            float wt[kMaxTopK];
+            f32x4 yv[kMaxTopK];
+#pragma unroll
+            for (int j = 0; j < kMaxTopK; ++j) {
+                if (j < K) {
+                    wt[j] = a.wts[(size_t)t * K + j];
+                    yv[j] = *reinterpret_cast<const f32x4*>(a.y + ((size_t)t * K + j) * H + c);
+                }
+            }
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < kMaxTopK; ++j)
+                if (j < K)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[q] = fmaf(wt[j], yv[j][q], acc[q]);
+            if (V > 0) {
+                f32x4 sh = *reinterpret_cast<const f32x4*>(a.y + ((size_t)N + t) * H + c);
+                for (int v = 1; v < V; ++v) {
+                    const f32x4 y2 = *reinterpret_cast<const f32x4*>(a.y + ((size_t)N + (size_t)v * T + t) * H + c);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) sh[q] += y2[q];
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc[q] += sh[q];
+            }
+            *reinterpret_cast<f32x4*>(a.out + (size_t)t * H + c) = acc;
+        }
+    };
+
+    // ---- 1. router (workgroups 0 .. T-1)
+    if (b < T) {
+        float* hand = reinterpret_cast<float*>(smem);
+        float* sc = hand + 64;
+        float* topv = sc + 64;
+        uint64_t* etab = reinterpret_cast<uint64_t*>(topv + kMaxTopK);
+        router_token_regs<KTG>(a, b, hand, sc, topv, etab);
+        publish();
+        FTR(1)
+    }
+
+#if defined(UOCR_ROUTER_ONLY)
+    __syncthreads();
+    if (tid == 0) store_cg(prog + b, S + kFusedSteps);
+    FTR(15)
+    return;
+#endif
+    // ---- 2. gate/up (workers T .. P-1). Sparse: shared groups' items first
+    // (no routing needed), then the live routed experts'.
+    int ngu_total = a.dense ? G * RBG : -1;  // sparse: known with the summary
+    if (b >= T) {
+        for (int i = b - T;; i += PW) {
+            if (a.dense) {
+                if (i >= ngu_total) break;
+                gate_up_item(i / RBG, i % RBG, true);
+            } else if (i < V * RBG) {
+                gate_up_item(E + i / RBG, i % RBG, true);
+            } else {
+                need_summary();
+                const int j = i - V * RBG;
+                if (j >= n_live_r * RBG) break;
+                gate_up_item(live[j / RBG], j % RBG, false);
+            }
+            publish();
+            if (ftr < 6) { FTR(ftr) ++ftr; }
+        }
+    }
+
+    // ---- 3. down (every workgroup) and the combine of each column block by
+    // the owner of its last item
+    need_summary();
+    FTR(6)
+    ftr = 7;
+    if (!a.dense) ngu_total = (V + n_live_r) * RBG;
+    const int ndn_total = n_live * RBD;
+    // position of group g's gate/up item r in the gate/up numbering
+    auto gu_index = [&](int gpos, int r_) {
+        if (a.dense) return live[gpos] * RBG + r_;
+        return gpos < n_live_r ? V * RBG + gpos * RBG + r_ : (gpos - n_live_r) * RBG + r_;
+    };
+    // Down items go to "slots" ordered by the gate/up work of the workgroup
+    // behind them (router workgroups first, then workers with fewer gate/up
+    // items), so a second round of down items lands on the least loaded.
+    const int rem = ngu_total % PW;
+    auto slot_wg = [&](int sl) {
+        if (sl < T) return sl;
+        const int q = sl - T;
+        return q < PW - rem ? T + rem + q : T + (q - (PW - rem));
+    };
+    const int my_slot = b < T ? b : ((b - T) >= rem ? T + (b - T - rem) : T + (PW - rem) + (b - T));
+    auto dn_step = [&](int j, int& owner, int& step) {
+        owner = slot_wg(j % P);
+        step = (owner < T ? 1 : 0) + n_gu_of(owner, ngu_total) + j / P + 1;
+    };
+    for (int j = my_slot; j < ndn_total; j += P) {
+        const int gpos = j / RBD, rb = j % RBD;
+        wait_steps(
+            [&](int q, int& owner, int& step) {
+                const int i = gu_index(gpos, q);
+                owner = T + i % PW;
+                step = i / PW + 1;
+            },
+            RBG);
+        if (ftr < 13) { FTR(ftr) ++ftr; }
+        down_item(live[gpos], rb);
+        publish();
+        if (ftr < 13) { FTR(ftr) ++ftr; }
+    }
+    // combine of column block rb by slot (ndn_total + rb) % P, one with the
+    // fewest down items, after all of its own (a combine waits only for down
+    // items, which never wait for a combine)
+    for (int rb = 0; rb < RBD; ++rb) {
+        if ((ndn_total + rb) % P != my_slot) continue;
+        wait_steps([&](int q, int& owner, int& step) { dn_step(q * RBD + rb, owner, step); }, n_live);
+        FTR(13)
+        combine_block(rb);
+        FTR(14)
+    }
+
+    // ---- leave: every workgroup ends the call at S + kFusedSteps
+    __syncthreads();
+    if (tid == 0) store_cg(prog + b, S + kFusedSteps);
+    FTR(15)
+}
+
+template <int GPT, int KTG, int KTD>
+static hipError_t launch_fused(const DecodeArgs& a, hipStream_t st) {
+    using Lay = FusedLds<GPT, KTG, KTD>;
+    const size_t lds = std::max(Lay::bytes, (size_t)a.hidden * 4 + 1024);
+    static hipError_t attr = hipFuncSetAttribute((const void*)decode_fused_kernel<GPT, KTG, KTD>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 80 * 1024);
+    if (attr != hipSuccess) return attr;
+    if (lds > 80 * 1024) return hipErrorInvalidValue;
+    static int resident = [] {
+        int dev = 0, cus = 0, per_cu = 0;
+        (void)hipGetDevice(&dev);
+        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_fused_kernel<GPT, KTG, KTD>, 256,
+                                                           std::max(Lay::bytes, (size_t)kMaxHidden * 4 + 1024));
+        return std::max(1, cus * std::max(1, per_cu));
+    }();
+    // the grid is the same on every call (the progress words advance together)
+    // and fully resident (workgroups wait for one another)
+    const int grid = std::min(resident, kFusedMaxGrid);
+    if (grid <= a.seq) return hipErrorInvalidConfiguration;
+    launch_k((decode_fused_kernel<GPT, KTG, KTD>), dim3(grid), dim3(256), (uint32_t)lds, st, a);
+    return hipGetLastError();
+}
+
+bool decode_fused_ok(int hidden, int inter, int group) {
+    return hidden == 1280 && inter == 896 && (group == 32 || group == 64 || group == 128);
+}
+
+hipError_t launch_decode_fused(const DecodeArgs& a, hipStream_t st) {
+    if (a.seq < 1 || a.seq > kFusedMaxSeq || !a.x_bf16 || a.rms_weight || !a.sync) return hipErrorInvalidValue;
+    if (a.n_experts + a.n_virtual > kMaxExperts || a.n_experts > 64 || a.top_k > kMaxTopK) return hipErrorInvalidValue;
+    if (!decode_fused_ok(a.hidden, a.inter, a.group)) return hipErrorInvalidValue;
+    switch (a.group) {
+        case 32: return launch_fused<4, 10, 7>(a, st);
+        case 64: return launch_fused<2, 10, 7>(a, st);
+        default: return launch_fused<1, 10, 7>(a, st);
+    }
+}
+
+}  // namespace uocr_hip

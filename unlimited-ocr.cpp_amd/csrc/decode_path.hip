@@ -19,511 +19,19 @@
 //     T*top_k + v*T + t), so the combine needs no routing lookups.
 // act slot layout: shared-expert ("virtual") groups first, slot v*T + t, then
 // the routed groups in expert order, slot n_virtual*T + offset(e) + rank.
-#include "launch.hpp"
-#include "routing.hpp"
+#include "decode_common.hpp"
 
 #include <algorithm>
-#include <type_traits>
-
-#if defined(UOCR_DBG)
-__device__ unsigned long long uocr_dbg_ts[64 * 64];
-extern "C" hipError_t uocr_dbg_read(void* host, size_t bytes) {
-    return hipMemcpyFromSymbol(host, HIP_SYMBOL(uocr_dbg_ts), bytes, 0, hipMemcpyDeviceToHost);
-}
-#define RDBG(i) \
-    if (threadIdx.x == 0 && blockIdx.x < 64) uocr_dbg_ts[blockIdx.x * 64 + (i)] = wall_clock64();
-__device__ unsigned long long uocr_dbg_ex[2][80 * 20 * 8];
-extern "C" hipError_t uocr_dbg_read_ex(void* host, size_t bytes) {
-    return hipMemcpyFromSymbol(host, HIP_SYMBOL(uocr_dbg_ex), bytes, 0, hipMemcpyDeviceToHost);
-}
-#define EDBG(i) \
-    if (threadIdx.x == 0 && blockIdx.x < 80 && blockIdx.y < 20) uocr_dbg_ex[GU ? 0 : 1][(blockIdx.y * 80 + blockIdx.x) * 8 + (i)] = wall_clock64();
-#else
-#define RDBG(i)
-#define EDBG(i)
-#endif
 
 namespace uocr_hip {
 
-// ---------------------------------------------------------------------------
-// routing helpers shared with the router kernels
-// ---------------------------------------------------------------------------
-
-// ---------------------------------------------------------------------------
-// Router: one token per workgroup of one wave.
-// ---------------------------------------------------------------------------
-constexpr int kMaxHidden = 1792;
-
-template <typename XT>
-__device__ __forceinline__ void load8(const XT* p, float* out);
-template <>
-__device__ __forceinline__ void load8<uint16_t>(const uint16_t* p, float* out) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(p);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        out[2 * i] = __uint_as_float(v[i] << 16);
-        out[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
-    }
-}
-template <>
-__device__ __forceinline__ void load8<float>(const float* p, float* out) {
-    const f32x4 a = *reinterpret_cast<const f32x4*>(p);
-    const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        out[i] = a[i];
-        out[4 + i] = b[i];
-    }
-}
-
-// The router matrix streams through an LDS ring of 16 KiB chunks (64 columns x
-// 64 experts x f32, [H/4][64][4] in HBM) filled by direct global->LDS loads
-// from all four waves; wave 0 runs the 64 FMA chains out of LDS. Eight chunks
-// (512 columns) are in flight at a time.
-constexpr int kRChunkCols = 128;
-constexpr int kRChunkBytes = kRChunkCols * 64 * 4;  // 32 KiB
+// Ring of four 32 KiB chunks for the stand-alone router kernel
 constexpr int kRRing = 4;
-constexpr int kRChunkLoads = kRChunkBytes / 1024;   // 1 KiB per wave load
-// DMA loads per chunk issued by producer wave w (1..3): units w-1, w+2, ...
-__host__ __device__ constexpr int router_loads_of(int wave) { return (kRChunkLoads - (wave - 1) + 2) / 3; }
-
-// s_waitcnt vmcnt(n) (n <= 63), leaving expcnt / lgkmcnt unconstrained
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-// s_waitcnt vmcnt(n) for a wave-uniform runtime n (values above 31 wait for 0)
-__device__ __forceinline__ void wait_vm_n(int n) {
-    switch (n) {
-#define UOCR_VM(k) case k: wait_vm<k>(); break;
-        UOCR_VM(1) UOCR_VM(2) UOCR_VM(3) UOCR_VM(4) UOCR_VM(5) UOCR_VM(6) UOCR_VM(7) UOCR_VM(8)
-        UOCR_VM(9) UOCR_VM(10) UOCR_VM(11) UOCR_VM(12) UOCR_VM(13) UOCR_VM(14) UOCR_VM(15) UOCR_VM(16)
-        UOCR_VM(17) UOCR_VM(18) UOCR_VM(19) UOCR_VM(20) UOCR_VM(21) UOCR_VM(22) UOCR_VM(23) UOCR_VM(24)
-        UOCR_VM(25) UOCR_VM(26) UOCR_VM(27) UOCR_VM(28) UOCR_VM(29) UOCR_VM(30) UOCR_VM(31)
-#undef UOCR_VM
-        default: wait_vm<0>(); break;
-    }
-}
-
-__device__ __forceinline__ void router_issue_chunk(const float* w, int chunk, unsigned char* ring, int wave, int lane) {
-    const unsigned char* src = reinterpret_cast<const unsigned char*>(w) + (size_t)chunk * kRChunkBytes;
-    unsigned char* dst = ring + (size_t)(chunk % kRRing) * kRChunkBytes;
-    for (int unit = wave - 1; unit < kRChunkLoads; unit += 3)  // 1 KiB per wave instruction
-        load_lds16(src + ((size_t)unit * 64 + lane) * 16, dst + (size_t)unit * 1024);
-}
-
-// LDS byte address of a __shared__ object
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-
-// LDS operands of one k-tile: four A fragments (1 KiB apart) and the scale
-// words of one or two scale rows (the GPT groups of the k-tile; MFMA step s
-// uses group (s * GPT) / 4). lds_issue_tile only issues the six reads (the
-// registers must not be used before lds_wait_tile); reading through asm keeps
-// the compiler's LDS-DMA tracking from turning the first read into a wait for
-// every outstanding global load.
-template <int GPT>
-struct TileRegs {
-    f16x8 av[4];
-    // GPT 4: four scales in 64 bits; GPT 2 / 1: two / one in 32 bits
-    typename std::conditional<GPT == 4, uint64_t, uint32_t>::type w0, w1;
-};
-
-template <int GPT>
-__device__ __forceinline__ void lds_issue_tile(uint32_t a_addr, uint32_t s0_addr, uint32_t s1_addr, TileRegs<GPT>& t) {
-#define UOCR_TILE_READS(SREAD)                                                                        \
-    asm volatile("ds_read_b128 %0, %6\n"                                                             \
-                 "ds_read_b128 %1, %6 offset:1024\n"                                                 \
-                 "ds_read_b128 %2, %6 offset:2048\n"                                                 \
-                 "ds_read_b128 %3, %6 offset:3072\n" SREAD " %4, %7\n" SREAD " %5, %8\n"             \
-                 : "=&v"(t.av[0]), "=&v"(t.av[1]), "=&v"(t.av[2]), "=&v"(t.av[3]), "=&v"(t.w0), "=&v"(t.w1) \
-                 : "v"(a_addr), "v"(s0_addr), "v"(s1_addr)                                          \
-                 : "memory")
-    if constexpr (GPT == 4) {
-        UOCR_TILE_READS("ds_read_b64");
-    } else if constexpr (GPT == 2) {
-        UOCR_TILE_READS("ds_read_b32");
-    } else {
-        UOCR_TILE_READS("ds_read_u16");
-    }
-#undef UOCR_TILE_READS
-}
-
-// Wait until at most `later` LDS reads (issued after this tile's) are
-// outstanding, then unpack the scales.
-template <int GPT, int LATER>
-__device__ __forceinline__ void lds_wait_tile(TileRegs<GPT>& t, f16* s0, f16* s1) {
-    asm volatile("s_waitcnt lgkmcnt(%6)"
-                 : "+v"(t.av[0]), "+v"(t.av[1]), "+v"(t.av[2]), "+v"(t.av[3]), "+v"(t.w0), "+v"(t.w1)
-                 : "n"(LATER));
-    const uint64_t x0 = t.w0, x1 = t.w1;
-    const uint32_t w0[2] = {(uint32_t)x0, (uint32_t)(x0 >> 32)};
-    const uint32_t w1[2] = {(uint32_t)x1, (uint32_t)(x1 >> 32)};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        const int gi = (s * GPT) >> 2;  // group within the k-tile
-        s0[s] = __builtin_bit_cast(f16, (uint16_t)((w0[gi >> 1] >> (16 * (gi & 1))) & 0xffffu));
-        s1[s] = __builtin_bit_cast(f16, (uint16_t)((w1[gi >> 1] >> (16 * (gi & 1))) & 0xffffu));
-    }
-}
-
-// Workgroup barrier that orders LDS only: __syncthreads() would also wait for
-// every outstanding global load (vmcnt(0)), draining the ring.
-__device__ __forceinline__ void lds_barrier() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt unconstrained
-    __builtin_amdgcn_s_barrier();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
 
 template <typename XT, bool RMS>
 __global__ __launch_bounds__(256) void router_decode_kernel(DecodeArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char rsmem[];
-    unsigned char* ring = rsmem;
-    float* xs = reinterpret_cast<float*>(rsmem + kRRing * kRChunkBytes);
-    __shared__ __attribute__((aligned(16))) float sc[64];
-    __shared__ float topv[kMaxTopK];
-    __shared__ uint64_t etab[32];
-    const int t = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int H = a.hidden, E = a.n_experts, K = a.top_k;
-    if (tid < 32) etab[tid] = uocr_exp2_tab[tid];
-    const int NCH = H / kRChunkCols;
-    const XT* x = static_cast<const XT*>(a.x) + (size_t)t * H;
-    RDBG(0)
-
-    // waves 1..3 start the router-matrix ring; wave 0 loads the token row -> xs (f32)
-    if (wave != 0) {
-        for (int ch = 0; ch < kRRing && ch < NCH; ++ch) router_issue_chunk(a.router_f32, ch, ring, wave, lane);
-    } else {
-        for (int c = lane * 8; c < H; c += 64 * 8) {
-            float v[8];
-            load8<XT>(x + c, v);
-            *reinterpret_cast<f32x4*>(xs + c) = f32x4{v[0], v[1], v[2], v[3]};
-            *reinterpret_cast<f32x4*>(xs + c + 4) = f32x4{v[4], v[5], v[6], v[7]};
-        }
-    }
-    lds_barrier();  // xs
-    RDBG(1)
-
-    if constexpr (RMS) {
-        // src/kernels/cpu_ops.cpp:58-67 as the reference build computes it: the
-        // products x*x rounded, summed in column order; the last H % 4 terms fused
-        if (tid == 0) {
-            float ss = 0.0f;
-            const int h4 = H & ~3;
-            for (int c = 0; c < h4; c += 4) {
-                const f32x4 v = *reinterpret_cast<const f32x4*>(xs + c);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) ss = __fadd_rn(ss, __fmul_rn(v[i], v[i]));
-            }
-            for (int c = h4; c < H; ++c) ss = fmaf(xs[c], xs[c], ss);
-            sc[0] = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)H), a.rms_eps)));
-        }
-        __syncthreads();
-        const float inv = sc[0];
-        for (int c = tid; c < H; c += 256) xs[c] = __fmul_rn(__fmul_rn(xs[c], inv), a.rms_weight[c]);
-        __syncthreads();
-    }
-
-    // f16 expert input (waves 1..3; wave 0 starts its chains)
-    if (wave > 0)
-        for (int c = (tid - 64) * 8; c < H; c += 192 * 8) {
-            const f32x4 p = *reinterpret_cast<const f32x4*>(xs + c);
-            const f32x4 q = *reinterpret_cast<const f32x4*>(xs + c + 4);
-            const f16x8 h = {(f16)p[0], (f16)p[1], (f16)p[2], (f16)p[3], (f16)q[0], (f16)q[1], (f16)q[2], (f16)q[3]};
-            *reinterpret_cast<f16x8*>(a.x16 + (size_t)t * H + c) = h;
-        }
-
-    // logits: lane e of wave 0 runs the reference's sequential fmaf chain,
-    // columns ascending (src/kernels/cpu_ops.cpp:26-39, contracted by the
-    // -march=native build). Waves 1..3 keep the ring filled; wave 0 only
-    // computes.
-    float acc = 0.0f;
-    const int my_loads = wave == 0 ? 0 : router_loads_of(wave);
-    for (int ch = 0; ch < NCH; ++ch) {
-        // chunks this wave has issued so far: 0 .. last
-        const int last = min(NCH - 1, max(kRRing - 1, ch - 2 + kRRing));
-        if (wave != 0) wait_vm_n(my_loads * (last - ch));
-        lds_barrier();
-        if (wave != 0 && ch >= 1 && ch - 1 + kRRing < NCH)
-            router_issue_chunk(a.router_f32, ch - 1 + kRRing, ring, wave, lane);
-        if (wave == 0) {
-            // 32 steps of 4 columns: the LDS reads run 6 steps (12 reads) ahead
-            // of the FMA chain, with explicit lgkmcnt waits (the compiler's own
-            // schedule waits for every read pair)
-            const uint32_t w_addr = lds_addr(ring + (size_t)(ch % kRRing) * kRChunkBytes) + lane * 16;
-            const uint32_t x_addr = lds_addr(xs + ch * kRChunkCols);
-            asm volatile(
-                "s_waitcnt lgkmcnt(0)\n"
-                "ds_read_b128 v[64:67], %[w] offset:0\n"
-                "ds_read_b128 v[68:71], %[x] offset:0\n"
-                "ds_read_b128 v[72:75], %[w] offset:1024\n"
-                "ds_read_b128 v[76:79], %[x] offset:16\n"
-                "ds_read_b128 v[80:83], %[w] offset:2048\n"
-                "ds_read_b128 v[84:87], %[x] offset:32\n"
-                "ds_read_b128 v[88:91], %[w] offset:3072\n"
-                "ds_read_b128 v[92:95], %[x] offset:48\n"
-                "ds_read_b128 v[96:99], %[w] offset:4096\n"
-                "ds_read_b128 v[100:103], %[x] offset:64\n"
-                "ds_read_b128 v[104:107], %[w] offset:5120\n"
-                "ds_read_b128 v[108:111], %[x] offset:80\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v68, v64\n"
-                "v_fmac_f32 %[acc], v69, v65\n"
-                "v_fmac_f32 %[acc], v70, v66\n"
-                "v_fmac_f32 %[acc], v71, v67\n"
-                "ds_read_b128 v[64:67], %[w] offset:6144\n"
-                "ds_read_b128 v[68:71], %[x] offset:96\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v76, v72\n"
-                "v_fmac_f32 %[acc], v77, v73\n"
-                "v_fmac_f32 %[acc], v78, v74\n"
-                "v_fmac_f32 %[acc], v79, v75\n"
-                "ds_read_b128 v[72:75], %[w] offset:7168\n"
-                "ds_read_b128 v[76:79], %[x] offset:112\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v84, v80\n"
-                "v_fmac_f32 %[acc], v85, v81\n"
-                "v_fmac_f32 %[acc], v86, v82\n"
-                "v_fmac_f32 %[acc], v87, v83\n"
-                "ds_read_b128 v[80:83], %[w] offset:8192\n"
-                "ds_read_b128 v[84:87], %[x] offset:128\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v92, v88\n"
-                "v_fmac_f32 %[acc], v93, v89\n"
-                "v_fmac_f32 %[acc], v94, v90\n"
-                "v_fmac_f32 %[acc], v95, v91\n"
-                "ds_read_b128 v[88:91], %[w] offset:9216\n"
-                "ds_read_b128 v[92:95], %[x] offset:144\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v100, v96\n"
-                "v_fmac_f32 %[acc], v101, v97\n"
-                "v_fmac_f32 %[acc], v102, v98\n"
-                "v_fmac_f32 %[acc], v103, v99\n"
-                "ds_read_b128 v[96:99], %[w] offset:10240\n"
-                "ds_read_b128 v[100:103], %[x] offset:160\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v108, v104\n"
-                "v_fmac_f32 %[acc], v109, v105\n"
-                "v_fmac_f32 %[acc], v110, v106\n"
-                "v_fmac_f32 %[acc], v111, v107\n"
-                "ds_read_b128 v[104:107], %[w] offset:11264\n"
-                "ds_read_b128 v[108:111], %[x] offset:176\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v68, v64\n"
-                "v_fmac_f32 %[acc], v69, v65\n"
-                "v_fmac_f32 %[acc], v70, v66\n"
-                "v_fmac_f32 %[acc], v71, v67\n"
-                "ds_read_b128 v[64:67], %[w] offset:12288\n"
-                "ds_read_b128 v[68:71], %[x] offset:192\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v76, v72\n"
-                "v_fmac_f32 %[acc], v77, v73\n"
-                "v_fmac_f32 %[acc], v78, v74\n"
-                "v_fmac_f32 %[acc], v79, v75\n"
-                "ds_read_b128 v[72:75], %[w] offset:13312\n"
-                "ds_read_b128 v[76:79], %[x] offset:208\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v84, v80\n"
-                "v_fmac_f32 %[acc], v85, v81\n"
-                "v_fmac_f32 %[acc], v86, v82\n"
-                "v_fmac_f32 %[acc], v87, v83\n"
-                "ds_read_b128 v[80:83], %[w] offset:14336\n"
-                "ds_read_b128 v[84:87], %[x] offset:224\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v92, v88\n"
-                "v_fmac_f32 %[acc], v93, v89\n"
-                "v_fmac_f32 %[acc], v94, v90\n"
-                "v_fmac_f32 %[acc], v95, v91\n"
-                "ds_read_b128 v[88:91], %[w] offset:15360\n"
-                "ds_read_b128 v[92:95], %[x] offset:240\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v100, v96\n"
-                "v_fmac_f32 %[acc], v101, v97\n"
-                "v_fmac_f32 %[acc], v102, v98\n"
-                "v_fmac_f32 %[acc], v103, v99\n"
-                "ds_read_b128 v[96:99], %[w] offset:16384\n"
-                "ds_read_b128 v[100:103], %[x] offset:256\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v108, v104\n"
-                "v_fmac_f32 %[acc], v109, v105\n"
-                "v_fmac_f32 %[acc], v110, v106\n"
-                "v_fmac_f32 %[acc], v111, v107\n"
-                "ds_read_b128 v[104:107], %[w] offset:17408\n"
-                "ds_read_b128 v[108:111], %[x] offset:272\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v68, v64\n"
-                "v_fmac_f32 %[acc], v69, v65\n"
-                "v_fmac_f32 %[acc], v70, v66\n"
-                "v_fmac_f32 %[acc], v71, v67\n"
-                "ds_read_b128 v[64:67], %[w] offset:18432\n"
-                "ds_read_b128 v[68:71], %[x] offset:288\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v76, v72\n"
-                "v_fmac_f32 %[acc], v77, v73\n"
-                "v_fmac_f32 %[acc], v78, v74\n"
-                "v_fmac_f32 %[acc], v79, v75\n"
-                "ds_read_b128 v[72:75], %[w] offset:19456\n"
-                "ds_read_b128 v[76:79], %[x] offset:304\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v84, v80\n"
-                "v_fmac_f32 %[acc], v85, v81\n"
-                "v_fmac_f32 %[acc], v86, v82\n"
-                "v_fmac_f32 %[acc], v87, v83\n"
-                "ds_read_b128 v[80:83], %[w] offset:20480\n"
-                "ds_read_b128 v[84:87], %[x] offset:320\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v92, v88\n"
-                "v_fmac_f32 %[acc], v93, v89\n"
-                "v_fmac_f32 %[acc], v94, v90\n"
-                "v_fmac_f32 %[acc], v95, v91\n"
-                "ds_read_b128 v[88:91], %[w] offset:21504\n"
-                "ds_read_b128 v[92:95], %[x] offset:336\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v100, v96\n"
-                "v_fmac_f32 %[acc], v101, v97\n"
-                "v_fmac_f32 %[acc], v102, v98\n"
-                "v_fmac_f32 %[acc], v103, v99\n"
-                "ds_read_b128 v[96:99], %[w] offset:22528\n"
-                "ds_read_b128 v[100:103], %[x] offset:352\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v108, v104\n"
-                "v_fmac_f32 %[acc], v109, v105\n"
-                "v_fmac_f32 %[acc], v110, v106\n"
-                "v_fmac_f32 %[acc], v111, v107\n"
-                "ds_read_b128 v[104:107], %[w] offset:23552\n"
-                "ds_read_b128 v[108:111], %[x] offset:368\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v68, v64\n"
-                "v_fmac_f32 %[acc], v69, v65\n"
-                "v_fmac_f32 %[acc], v70, v66\n"
-                "v_fmac_f32 %[acc], v71, v67\n"
-                "ds_read_b128 v[64:67], %[w] offset:24576\n"
-                "ds_read_b128 v[68:71], %[x] offset:384\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v76, v72\n"
-                "v_fmac_f32 %[acc], v77, v73\n"
-                "v_fmac_f32 %[acc], v78, v74\n"
-                "v_fmac_f32 %[acc], v79, v75\n"
-                "ds_read_b128 v[72:75], %[w] offset:25600\n"
-                "ds_read_b128 v[76:79], %[x] offset:400\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v84, v80\n"
-                "v_fmac_f32 %[acc], v85, v81\n"
-                "v_fmac_f32 %[acc], v86, v82\n"
-                "v_fmac_f32 %[acc], v87, v83\n"
-                "ds_read_b128 v[80:83], %[w] offset:26624\n"
-                "ds_read_b128 v[84:87], %[x] offset:416\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v92, v88\n"
-                "v_fmac_f32 %[acc], v93, v89\n"
-                "v_fmac_f32 %[acc], v94, v90\n"
-                "v_fmac_f32 %[acc], v95, v91\n"
-                "ds_read_b128 v[88:91], %[w] offset:27648\n"
-                "ds_read_b128 v[92:95], %[x] offset:432\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v100, v96\n"
-                "v_fmac_f32 %[acc], v101, v97\n"
-                "v_fmac_f32 %[acc], v102, v98\n"
-                "v_fmac_f32 %[acc], v103, v99\n"
-                "ds_read_b128 v[96:99], %[w] offset:28672\n"
-                "ds_read_b128 v[100:103], %[x] offset:448\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v108, v104\n"
-                "v_fmac_f32 %[acc], v109, v105\n"
-                "v_fmac_f32 %[acc], v110, v106\n"
-                "v_fmac_f32 %[acc], v111, v107\n"
-                "ds_read_b128 v[104:107], %[w] offset:29696\n"
-                "ds_read_b128 v[108:111], %[x] offset:464\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v68, v64\n"
-                "v_fmac_f32 %[acc], v69, v65\n"
-                "v_fmac_f32 %[acc], v70, v66\n"
-                "v_fmac_f32 %[acc], v71, v67\n"
-                "ds_read_b128 v[64:67], %[w] offset:30720\n"
-                "ds_read_b128 v[68:71], %[x] offset:480\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v76, v72\n"
-                "v_fmac_f32 %[acc], v77, v73\n"
-                "v_fmac_f32 %[acc], v78, v74\n"
-                "v_fmac_f32 %[acc], v79, v75\n"
-                "ds_read_b128 v[72:75], %[w] offset:31744\n"
-                "ds_read_b128 v[76:79], %[x] offset:496\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v84, v80\n"
-                "v_fmac_f32 %[acc], v85, v81\n"
-                "v_fmac_f32 %[acc], v86, v82\n"
-                "v_fmac_f32 %[acc], v87, v83\n"
-                "s_waitcnt lgkmcnt(8)\n"
-                "v_fmac_f32 %[acc], v92, v88\n"
-                "v_fmac_f32 %[acc], v93, v89\n"
-                "v_fmac_f32 %[acc], v94, v90\n"
-                "v_fmac_f32 %[acc], v95, v91\n"
-                "s_waitcnt lgkmcnt(6)\n"
-                "v_fmac_f32 %[acc], v100, v96\n"
-                "v_fmac_f32 %[acc], v101, v97\n"
-                "v_fmac_f32 %[acc], v102, v98\n"
-                "v_fmac_f32 %[acc], v103, v99\n"
-                "s_waitcnt lgkmcnt(4)\n"
-                "v_fmac_f32 %[acc], v108, v104\n"
-                "v_fmac_f32 %[acc], v109, v105\n"
-                "v_fmac_f32 %[acc], v110, v106\n"
-                "v_fmac_f32 %[acc], v111, v107\n"
-                "s_waitcnt lgkmcnt(2)\n"
-                "v_fmac_f32 %[acc], v68, v64\n"
-                "v_fmac_f32 %[acc], v69, v65\n"
-                "v_fmac_f32 %[acc], v70, v66\n"
-                "v_fmac_f32 %[acc], v71, v67\n"
-                "s_waitcnt lgkmcnt(0)\n"
-                "v_fmac_f32 %[acc], v76, v72\n"
-                "v_fmac_f32 %[acc], v77, v73\n"
-                "v_fmac_f32 %[acc], v78, v74\n"
-                "v_fmac_f32 %[acc], v79, v75\n"
-                : [acc] "+v"(acc)
-                : [w] "v"(w_addr), [x] "v"(x_addr)
-                : "v64", "v65", "v66", "v67", "v68", "v69", "v70", "v71", "v72", "v73", "v74", "v75", "v76", "v77", "v78", "v79", "v80", "v81", "v82", "v83", "v84", "v85", "v86", "v87", "v88", "v89", "v90", "v91", "v92", "v93", "v94", "v95", "v96", "v97", "v98", "v99", "v100", "v101", "v102", "v103", "v104", "v105", "v106", "v107", "v108", "v109", "v110", "v111", "memory");
-        }
-    }
-    RDBG(40)
-    // scoring (src/kernels/cpu_ops.cpp:93-106 softmax, or sigmoid) and greedy
-    // top-k (src/engine/moe_decoder.cpp:264-287) by wave 0 alone: its LDS
-    // accesses are ordered within the wave, so no workgroup barrier is needed
-    if (wave != 0) return;
-    float p;
-    if (a.scoring_sigmoid) {
-        p = __fdiv_rn(1.0f, 1.0f + ref_expf(-acc, etab));
-    } else {
-        float mx = lane < E ? acc : -INFINITY;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
-        const float ev = lane < E ? ref_expf(acc - mx, etab) : 0.0f;
-        sc[lane] = ev;
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        const float sum = ordered_sum64(sc, E);  // expert order
-        p = ev * __fdiv_rn(1.0f, sum);
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    }
-    RDBG(42)
-    sc[lane] = lane < E ? p : -1.0f;
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    const int rank = lane < E ? greedy_rank64(sc, lane, p) : 64;  // sc[E..64) holds -1 (below every score)
-    if (rank < K) topv[rank] = p;
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    RDBG(43)
-    if (lane < K) {
-        float wj = topv[lane];
-        if (K > 1 && a.norm_topk_prob) {  // moe_decoder.cpp:280-284
-            float s = 0.0f;
-            for (int j = 0; j < K; ++j) s += topv[j];
-            wj = __fdiv_rn(wj, s + 1e-20f) * a.scaling;
-        } else {
-            wj *= a.scaling;
-        }
-        a.wts[(size_t)t * K + lane] = wj;
-    }
-    if (rank < K) a.ids[(size_t)t * K + rank] = lane;
-    RDBG(41)
+    router_token<XT, RMS, kRRing>(a, blockIdx.x, rsmem);
 }
 
 // ---------------------------------------------------------------------------
@@ -640,13 +148,8 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(DecodeArgs a) {
             const size_t toff = (size_t)g * wstr + (size_t)rbl * KT * kTileBytes + (size_t)lane * 16;
 #pragma unroll
             for (int kt = 0; kt < KT; ++kt) {
-#if defined(UOCR_NOLOAD)
-                bw0[kt] = u32x4{(uint32_t)(toff + kt), 1u, 2u, 3u};
-                if constexpr (GU) bw1[kt] = u32x4{(uint32_t)(toff * 3 + kt), 1u, 2u, 3u};
-#else
                 bw0[kt] = *reinterpret_cast<const u32x4*>(wsrc0 + toff + (size_t)kt * kTileBytes);
                 if constexpr (GU) bw1[kt] = *reinterpret_cast<const u32x4*>(a.up + toff + (size_t)kt * kTileBytes);
-#endif
             }
         }
 
@@ -682,16 +185,11 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(DecodeArgs a) {
                     lds_wait_tile<GPT, 0>(tr[kt & 1], s0, s1);
                 }
                 const f16x8* av = tr[kt & 1].av;
-#if defined(UOCR_NOCOMPUTE)
-                acc0[0] += __uint_as_float(bw0[kt][0] ^ bw0[kt][1] ^ bw0[kt][2] ^ bw0[kt][3]) + (float)av[0][0] + (float)s0[0];
-                if constexpr (GU) acc1[0] += __uint_as_float(bw1[kt][0] ^ bw1[kt][1] ^ bw1[kt][2] ^ bw1[kt][3]) + (float)s1[0];
-#else
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
                     acc0 = mfma16(av[s], dequant8(bw0[kt][s], scale2(s0[s])), acc0);
                     if constexpr (GU) acc1 = mfma16(av[s], dequant8(bw1[kt][s], scale2(s1[s])), acc1);
                 }
-#endif
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {

@@ -102,6 +102,16 @@ struct CombineArgs {
     int seq, hidden, top_k, n_experts, n_virtual;
 };
 
+// Progress words of the fused decode kernel (layer-owned device memory, zero
+// at creation): workgroup b publishes the number of steps it has finished this
+// call as base + steps, and leaves every call at base + kFusedSteps.
+constexpr int kFusedMaxSeq = 16;
+constexpr int kFusedMaxGrid = 4096;
+struct FusedSync {
+    int progress[kFusedMaxGrid];
+    int error;  // a bounded wait timed out (sticky)
+};
+
 // Decode-sized layer (seq < 256): router_decode / expert passes / combine with
 // slots derived from the routing ids inside each workgroup.
 struct DecodeArgs {
@@ -111,6 +121,7 @@ struct DecodeArgs {
     const float* rms_weight;   // optional [hidden]; also selects out = x + moe
     float rms_eps;
     const float* router_f32;   // [hidden/4][64][4], experts padded to 64
+    const uint16_t* router_t;  // [hidden/8][n_experts][8] bf16 (fused decode kernel)
     int norm_topk_prob, scoring_sigmoid;
     float scaling;
     f16* x16;                  // [seq, hidden]
@@ -123,7 +134,9 @@ struct DecodeArgs {
     const uint16_t* up_s;
     const uint16_t* down_s;
     long long gu_wstride, gu_sstride, dn_wstride, dn_sstride;
-    f16* act;                  // [slots, inter]
+    FusedSync* sync;           // fused kernel only
+    int dense;                 // fused kernel: gate/up over every group and token
+    f16* act;                  // [slots, inter]; fused: [(E + n_virtual) * seq, inter]
     float* y;                  // [slots, hidden]
     float* out;                // [seq, hidden]
 };
@@ -131,6 +144,8 @@ bool decode_shapes_ok(int hidden, int inter);
 hipError_t launch_router_decode(const DecodeArgs& a, hipStream_t st);
 hipError_t launch_experts_decode2(const DecodeArgs& a, bool gate_up, hipStream_t st);
 hipError_t launch_combine_decode(const DecodeArgs& a, hipStream_t st);
+bool decode_fused_ok(int hidden, int inter, int group);
+hipError_t launch_decode_fused(const DecodeArgs& a, hipStream_t st);
 
 hipError_t launch_router(const RouterArgs& a, bool x_is_bf16, hipStream_t st);
 size_t router_smem_bytes(int hidden);

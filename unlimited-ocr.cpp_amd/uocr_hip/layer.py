@@ -6,7 +6,7 @@ import numpy as np
 from . import _lib
 from ._lib import DTYPE_BF16, DTYPE_F32, LayerDescC, QMatrixC, check, load
 
-STAGES = ("router", "group", "gate_up", "down", "combine")
+STAGES = ("router", "group", "gate_up", "down", "combine", "fused")
 
 
 class QMatrix:
@@ -105,7 +105,7 @@ class MoELayerInt4:
         check(self.lib.uocr_hip_moe_layer_set_timing(self.handle, 1 if enable else 0))
 
     def read_timing(self):
-        ms = (C.c_float * 5)()
+        ms = (C.c_float * len(STAGES))()
         n = C.c_int()
-        check(self.lib.uocr_hip_moe_layer_read_timing(self.handle, ms, 5, C.byref(n)))
+        check(self.lib.uocr_hip_moe_layer_read_timing(self.handle, ms, len(STAGES), C.byref(n)))
         return dict(zip(STAGES, list(ms))), n.value
