@@ -235,7 +235,8 @@ WsPlan plan(const uocr_hip_moe_layer* L, int seq) {
     p.tile_m0 = take((size_t)p.max_tiles * 4);
     // act: one row per slot, or per (group, token) for the fused decode kernel
     p.act = take((size_t)std::max(p.slots, Ev * seq) * L->inter * 2);
-    p.y = take((size_t)p.slots * L->hidden * 4);
+    // y: one row per entry, or per (group, token) for the fused decode kernel
+    p.y = take((size_t)std::max(p.slots, Ev * seq) * L->hidden * 4);
     const int chunks = group_chunks(seq, L->top_k);
     p.lrank = take((size_t)seq * L->top_k * 4);
     p.chunk_count = take((size_t)chunks * L->n_experts * 4);
@@ -476,6 +477,8 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
         if (use_fused(L, seq, x_dtype)) {
             da.sync = L->sync;
             da.dense = use_dense(seq);
+            static const int dense_dn = env_int("UOCR_DENSE_DN", 0);
+            da.dense_dn = da.dense && dense_dn > 0;
             stage(5);
             HIP_TRY(launch_decode_fused(da, st), "fused decode launch");
             stage(-1);

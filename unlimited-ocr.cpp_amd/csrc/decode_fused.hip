@@ -372,11 +372,11 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
         constexpr int NG = Lay::NGD;
         constexpr int SROW = kTileRows * NG;
         have_x = false;
-        const int cnt = token_list(g);
+        const int cnt = a.dense_dn ? T : token_list(g);
         const int rbw0 = rb * 8 + wave, rbw1 = rbw0 + 4;
         const int rbl0 = min(rbw0, H / kTileRows - 1), rbl1 = min(rbw1, H / kTileRows - 1);
         if (r < cnt) {
-            const int tok = g < E ? ent[wave * 16 + r] / K : r;
+            const int tok = (g < E && !a.dense_dn) ? ent[wave * 16 + r] / K : r;
             const f16* src = a.act + (size_t)(g * T + tok) * I + wave * 32 + 8 * (lane >> 4);
 #pragma unroll
             for (int kt = 0; kt < KT; ++kt) load_lds16_cg(src + kt * kTileK, As + (size_t)(kt * 4 + wave) * 64 * 8);
@@ -408,7 +408,8 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
             for (int q = 0; q < 4; ++q) {
                 const int m = 4 * (lane >> 4) + q;
                 if (m < cnt) {
-                    const int yrow = g < E ? ent[wave * 16 + m] : N + (g - E) * T + m;
+                    // dense: y row of (group g, token m) is g*T + m
+                    const int yrow = a.dense_dn ? g * T + m : g < E ? ent[wave * 16 + m] : N + (g - E) * T + m;
                     store_cg(a.y + (size_t)yrow * H + rbw0 * kTileRows + r, acc0[q]);
                     if (live1) store_cg(a.y + (size_t)yrow * H + rbw1 * kTileRows + r, acc1[q]);
                 }
@@ -430,7 +431,8 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
             for (int j = 0; j < kMaxTopK; ++j) {
                 if (j < K) {
                     wt[j] = a.wts[(size_t)t * K + j];
-                    yv[j] = *reinterpret_cast<const f32x4*>(a.y + ((size_t)t * K + j) * H + c);
+                    const size_t yrow = a.dense_dn ? (size_t)a.ids[(size_t)t * K + j] * T + t : (size_t)t * K + j;
+                    yv[j] = *reinterpret_cast<const f32x4*>(a.y + yrow * H + c);
                 }
             }
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -440,9 +442,10 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
 #pragma unroll
                     for (int q = 0; q < 4; ++q) acc[q] = fmaf(wt[j], yv[j][q], acc[q]);
             if (V > 0) {
-                f32x4 sh = *reinterpret_cast<const f32x4*>(a.y + ((size_t)N + t) * H + c);
+                const size_t sh0 = a.dense_dn ? (size_t)E * T : (size_t)N;  // first shared row
+                f32x4 sh = *reinterpret_cast<const f32x4*>(a.y + (sh0 + t) * H + c);
                 for (int v = 1; v < V; ++v) {
-                    const f32x4 y2 = *reinterpret_cast<const f32x4*>(a.y + ((size_t)N + (size_t)v * T + t) * H + c);
+                    const f32x4 y2 = *reinterpret_cast<const f32x4*>(a.y + (sh0 + (size_t)v * T + t) * H + c);
 #pragma unroll
                     for (int q = 0; q < 4; ++q) sh[q] += y2[q];
                 }
@@ -491,15 +494,20 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
         }
     }
 
-    // ---- 3. down (every workgroup) and the combine of each column block by
-    // the owner of its last item
-    need_summary();
+    // ---- 3. down (every workgroup) and the combine of each column block.
+    // Dense: every group for all T tokens, item j = (group j / RBD, block
+    // j % RBD); it waits only for its group's gate/up items, so the weight
+    // stream runs on from gate/up into down while the router finishes. Sparse:
+    // the live groups only (the routing summary first).
+    if (!a.dense_dn) need_summary();
+    if (!a.dense) ngu_total = (V + n_live_r) * RBG;
     FTR(6)
     ftr = 7;
-    if (!a.dense) ngu_total = (V + n_live_r) * RBG;
-    const int ndn_total = n_live * RBD;
-    // position of group g's gate/up item r in the gate/up numbering
+    const int n_dn_groups = a.dense_dn ? G : n_live;
+    const int ndn_total = n_dn_groups * RBD;
+    // position of gate/up item r of the group at down position gpos
     auto gu_index = [&](int gpos, int r_) {
+        if (a.dense_dn) return gpos * RBG + r_;
         if (a.dense) return live[gpos] * RBG + r_;
         return gpos < n_live_r ? V * RBG + gpos * RBG + r_ : (gpos - n_live_r) * RBG + r_;
     };
@@ -527,16 +535,23 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
             },
             RBG);
         if (ftr < 13) { FTR(ftr) ++ftr; }
-        down_item(live[gpos], rb);
+        down_item(a.dense_dn ? gpos : live[gpos], rb);
         publish();
         if (ftr < 13) { FTR(ftr) ++ftr; }
     }
     // combine of column block rb by slot (ndn_total + rb) % P, one with the
     // fewest down items, after all of its own (a combine waits only for down
-    // items, which never wait for a combine)
+    // items and the router, which never wait for a combine)
     for (int rb = 0; rb < RBD; ++rb) {
         if ((ndn_total + rb) % P != my_slot) continue;
-        wait_steps([&](int q, int& owner, int& step) { dn_step(q * RBD + rb, owner, step); }, n_live);
+        wait_steps([&](int q, int& owner, int& step) {
+            if (q < T) {  // the router of token q
+                owner = q;
+                step = 1;
+            } else {
+                dn_step((q - T) * RBD + rb, owner, step);
+            }
+        }, T + n_dn_groups);
         FTR(13)
         combine_block(rb);
         FTR(14)
