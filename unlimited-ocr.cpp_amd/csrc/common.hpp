@@ -48,27 +48,28 @@ constexpr int kTileBytes = 1024;
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
-__device__ __forceinline__ f16x2 nib_pair(uint32_t w) {
-    // (w & 0x000F000F) | 0x64006400 holds two f16 values 1024 + q; one
-    // v_bfi_b32 (the high nibbles of 0x64006400 are zero where the mask is set)
-    uint32_t v;
-    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(v) : "v"(0x000F000Fu), "v"(w), "v"(0x64006400u));
+__device__ __forceinline__ f16x2 as_h2(uint32_t v) {
     f16x2 h;
     __builtin_memcpy(&h, &v, 4);
     return h;
 }
 
-// Eight nibbles of one packed word -> f16x8 of (q - 8) * scale. Exact whenever
-// the scale is a normal f16: (q - 8) has <= 3 significant bits and a bf16 scale
-// 8, so the product fits the 11-bit f16 significand.
-// (Scalar words on purpose: a __builtin_bit_cast of an ext_vector element was
-// miscompiled by this toolchain into a copy of element 0.)
+// Eight nibbles of one packed word -> f16x8 of (q - 8) * scale, in the order of
+// the tile layout (nibble i of the word at bit (i & 1) * 16 + (i >> 1) * 4).
+// One AND-OR per nibble pair builds two f16 values directly: a nibble in bits
+// [3:0] under the exponent of 1024 (0x6400, unit ulp) is 1024 + q, a nibble in
+// bits [7:4] under the exponent of 64 (0x5400, ulp 1/16) is 64 + q -- so one
+// shift by 8 serves all four pairs. Subtracting 1032 / 72 gives q - 8 exactly,
+// and the product with a bf16-valued scale is exact in f16: (q - 8) has <= 3
+// significant bits and the scale 8, within the 11-bit significand.
 __device__ __forceinline__ f16x8 dequant8(uint32_t w, f16x2 s2) {
-    const f16x2 off = {(f16)-1032.0f, (f16)-1032.0f};
-    const f16x2 h0 = (nib_pair(w) + off) * s2;
-    const f16x2 h1 = (nib_pair(w >> 4) + off) * s2;
-    const f16x2 h2 = (nib_pair(w >> 8) + off) * s2;
-    const f16x2 h3 = (nib_pair(w >> 12) + off) * s2;
+    const f16x2 off0 = {(f16)-1032.0f, (f16)-1032.0f}, off1 = {(f16)-72.0f, (f16)-72.0f};
+    // (w & mask) | magic as one v_bitop3_b32 (truth table 0xEA = (a & b) | c)
+    const uint32_t w8 = w >> 8;
+    const f16x2 h0 = (as_h2(__builtin_amdgcn_bitop3_b32(w, 0x000F000Fu, 0x64006400u, 0xEA)) + off0) * s2;
+    const f16x2 h1 = (as_h2(__builtin_amdgcn_bitop3_b32(w, 0x00F000F0u, 0x54005400u, 0xEA)) + off1) * s2;
+    const f16x2 h2 = (as_h2(__builtin_amdgcn_bitop3_b32(w8, 0x000F000Fu, 0x64006400u, 0xEA)) + off0) * s2;
+    const f16x2 h3 = (as_h2(__builtin_amdgcn_bitop3_b32(w8, 0x00F000F0u, 0x54005400u, 0xEA)) + off1) * s2;
     f16x8 r;
     r[0] = h0[0]; r[1] = h0[1]; r[2] = h1[0]; r[3] = h1[1];
     r[4] = h2[0]; r[5] = h2[1]; r[6] = h3[0]; r[7] = h3[1];
