@@ -28,10 +28,7 @@
 //
 // act row of (group g, token t) is g * T + t; y is indexed by entry as in the
 // stand-alone path ((t, j) at t * top_k + j, shared group v at T * top_k + v*T + t).
-#include "decode_common.hpp"
-
-#include <algorithm>
-
+#include <hip/hip_runtime.h>
 #if defined(UOCR_FTRACE)
 __device__ unsigned long long uocr_ftrace[4096 * 16];
 extern "C" hipError_t uocr_ftrace_read(void* host, size_t bytes) {
@@ -44,9 +41,21 @@ extern "C" hipError_t uocr_ftrace_clear() {
 }
 #define FTR(i) \
     if (threadIdx.x == 0) uocr_ftrace[blockIdx.x * 16 + (i)] = wall_clock64();
+__device__ unsigned long long uocr_rtrace[64 * 16];
+extern "C" hipError_t uocr_rtrace_read(void* host, size_t bytes) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(uocr_rtrace), bytes, 0, hipMemcpyDeviceToHost);
+}
+#define RTR(i) \
+    if ((threadIdx.x & 63) == 0) uocr_rtrace[blockIdx.x * 16 + (i)] = wall_clock64();
 #else
 #define FTR(i)
+#define RTR(i)
 #endif
+#include "decode_common.hpp"
+
+#include <algorithm>
+
+
 
 namespace uocr_hip {
 
@@ -147,49 +156,82 @@ __device__ __forceinline__ void convert_own_rows(f16* As, int wave, int lane) {
 // at kernel start, then the waves run the reference's sequential fmaf chain
 // (columns ascending, src/kernels/cpu_ops.cpp:26-39) one segment after the
 // other, handing the running sums on through LDS; the last wave scores and
-// selects. No LDS ring and no refills under the weight stream of the other
-// workgroups.
+// selects. The token row sits in LDS as f32 and reaches the chain as broadcast
+// 16-byte reads one 8-column block ahead, so a column costs the weight's
+// widening and the fmac. The router waves run at raised issue priority (the
+// other workgroup on the CU dequantises expert weights meanwhile).
 template <int KT>
 __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, float* hand, float* sc, float* topv,
-                                                  uint64_t* etab) {
+                                                  uint64_t* etab, float* xs) {
     constexpr int SEG = KT * 32;  // columns per wave (H = KT * 128)
     constexpr int NL = SEG / 8;   // 16-byte weight loads per lane
-    constexpr int NX = SEG / 64;  // x blocks of 64 columns per wave
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int E = a.n_experts, H = KT * 128;
     const int e = lane < E ? lane : 0;
+    // token row first (the weight burst behind it is waited for only by the chain)
+    static_assert(H % 256 == 0, "token row: whole 256-column passes");
+    constexpr int NXT = H / 256;
+    __builtin_amdgcn_s_setprio(3);
+    const uint16_t* x = static_cast<const uint16_t*>(a.x) + (size_t)t * H;
+    uint32_t xb[NXT];
+#pragma unroll
+    for (int i = 0; i < NXT; ++i) xb[i] = x[tid + 256 * i];
     const uint16_t* wbase = a.router_t + ((size_t)wave * NL * E + e) * 8;
     u32x4 wr[NL];
 #pragma unroll
     for (int i = 0; i < NL; ++i) wr[i] = *reinterpret_cast<const u32x4*>(wbase + (size_t)i * E * 8);
-    // this wave's columns of the token row: lane i of block j holds column
-    // wave*SEG + 64j + i (broadcast with readlane in the chain)
-    const uint16_t* x = static_cast<const uint16_t*>(a.x) + (size_t)t * H + wave * SEG;
-    float xr[NX];
+    asm volatile("" ::: "memory");  // the whole burst is issued before the row is waited for
 #pragma unroll
-    for (int j = 0; j < NX; ++j) xr[j] = __uint_as_float((uint32_t)x[64 * j + lane] << 16);
-    if (tid < 32) etab[tid] = uocr_exp2_tab[tid];
+    for (int i = 0; i < NXT; ++i) {
+        asm volatile("" : "+v"(xb[i]));
+        xs[tid + 256 * i] = __uint_as_float(xb[i] << 16);
+    }
+    lds_barrier();
+    RTR(0)
+    const uint32_t xa = lds_addr(xs + wave * SEG);
     float acc = 0.0f;
     for (int w = 0; w < 4; ++w) {
         if (wave == w) {
             if (w > 0) acc = hand[lane];
+            RTR(1 + w)
+            f32x4 c0, c1, n0, n1;
+            asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:16\n\ts_waitcnt lgkmcnt(0)"
+                         : "=&v"(c0), "=&v"(c1) : "v"(xa) : "memory");
 #pragma unroll
             for (int i = 0; i < NL; ++i) {
-                u32x4 q = wr[i];
-                asm volatile("" : "+v"(q));  // unpack at the point of use, not hoisted
+                if (i + 1 < NL)
+                    asm volatile("ds_read_b128 %0, %2 offset:%3\n\tds_read_b128 %1, %2 offset:%4"
+                                 : "=&v"(n0), "=&v"(n1) : "v"(xa), "i"((i + 1) * 32), "i"((i + 1) * 32 + 16));
+                // widen at the point of use (volatile: not hoisted into a spill)
+                f32x4 w0, w1;
+                asm volatile(
+                    "v_lshlrev_b32 %0, 16, %8\n\tv_and_b32 %1, 0xffff0000, %8\n\t"
+                    "v_lshlrev_b32 %2, 16, %9\n\tv_and_b32 %3, 0xffff0000, %9\n\t"
+                    "v_lshlrev_b32 %4, 16, %10\n\tv_and_b32 %5, 0xffff0000, %10\n\t"
+                    "v_lshlrev_b32 %6, 16, %11\n\tv_and_b32 %7, 0xffff0000, %11"
+                    : "=&v"(w0[0]), "=&v"(w0[1]), "=&v"(w0[2]), "=&v"(w0[3]), "=&v"(w1[0]), "=&v"(w1[1]),
+                      "=&v"(w1[2]), "=&v"(w1[3])
+                    : "v"(wr[i][0]), "v"(wr[i][1]), "v"(wr[i][2]), "v"(wr[i][3]));
 #pragma unroll
-                for (int c = 0; c < 8; ++c) {
-                    const int col = i * 8 + c;
-                    const float xv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xr[col / 64]), col % 64));
-                    const uint32_t wbits = (c & 1) ? (q[c >> 1] & 0xffff0000u) : (q[c >> 1] << 16);
-                    acc = fmaf(xv, __uint_as_float(wbits), acc);
+                for (int c = 0; c < 4; ++c) acc = fmaf(c0[c], w0[c], acc);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc = fmaf(c1[c], w1[c], acc);
+                if (i + 1 < NL) {
+                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(n0), "+v"(n1), "+v"(acc));
+                    c0 = n0;
+                    c1 = n1;
                 }
             }
+            RTR(5 + w)
             if (w < 3) hand[lane] = acc;
+            // the expf table for the selection (wave 0's weight burst is drained)
+            if (w == 0 && lane < 32) etab[lane] = uocr_exp2_tab[lane];
         }
         lds_barrier();
     }
     if (wave == 3) router_select<true>(a, t, acc, sc, topv, etab);
+    __builtin_amdgcn_s_setprio(0);
+    RTR(9)
 }
 
 #ifndef UOCR_FUSED_WPE
@@ -462,7 +504,7 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
         float* sc = hand + 64;
         float* topv = sc + 64;
         uint64_t* etab = reinterpret_cast<uint64_t*>(topv + kMaxTopK);
-        router_token_regs<KTG>(a, b, hand, sc, topv, etab);
+        router_token_regs<KTG>(a, b, hand, sc, topv, etab, hand + 256);
         publish();
         FTR(1)
     }
@@ -476,6 +518,9 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
     // ---- 2. gate/up (workers T .. P-1). Sparse: shared groups' items first
     // (no routing needed), then the live routed experts'.
     int ngu_total = a.dense ? G * RBG : -1;  // sparse: known with the summary
+#if defined(UOCR_GU_DELAY)
+    if (b >= T) for (int i = 0; i < UOCR_GU_DELAY; ++i) __builtin_amdgcn_s_sleep(32);
+#endif
     if (b >= T) {
         for (int i = b - T;; i += PW) {
             if (a.dense) {
