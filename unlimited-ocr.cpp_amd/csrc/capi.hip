@@ -135,7 +135,7 @@ struct uocr_hip_moe_layer {
     hipEvent_t ev[2 * kStages] = {};  // start/stop per stage
     unsigned stage_mask = 0;          // stages the pending call recorded
     float stage_ms[kStages] = {};
-    FusedSync* sync = nullptr;        // work queue of the fused decode kernel (zero between calls)
+    FusedSync* sync = nullptr;        // progress words and tagged routing of the fused decode kernel
     int timed_calls = 0;
     bool pending = false;
 };

@@ -76,6 +76,24 @@ __device__ __forceinline__ f16x8 dequant8(uint32_t w, f16x2 s2) {
     return r;
 }
 
+// The same eight nibbles as biased f16 values without the zero point and the
+// scale: positions 0, 1, 4, 5 hold 1024 + q, positions 2, 3, 6, 7 hold 64 + q
+// (the magic exponents of dequant8). A caller that seeds the MFMA accumulator
+// with -(1032 * sum of its A values at the first positions + 72 * sum at the
+// others) over a scale group, then scales the group's result, gets the same
+// product as with dequant8 at four operations per word instead of twelve.
+__device__ __forceinline__ f16x8 dequant8_biased(uint32_t w) {
+    const uint32_t w8 = w >> 8;
+    u32x4 p;
+    p[0] = __builtin_amdgcn_bitop3_b32(w, 0x000F000Fu, 0x64006400u, 0xEA);
+    p[1] = __builtin_amdgcn_bitop3_b32(w, 0x00F000F0u, 0x54005400u, 0xEA);
+    p[2] = __builtin_amdgcn_bitop3_b32(w8, 0x000F000Fu, 0x64006400u, 0xEA);
+    p[3] = __builtin_amdgcn_bitop3_b32(w8, 0x00F000F0u, 0x54005400u, 0xEA);
+    f16x8 r;
+    __builtin_memcpy(&r, &p, 16);
+    return r;
+}
+
 __device__ __forceinline__ f16x2 scale2(f16 s) { return f16x2{s, s}; }
 
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {

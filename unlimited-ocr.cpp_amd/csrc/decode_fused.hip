@@ -101,34 +101,118 @@ struct FusedLds {
     static constexpr int NGD = scale_row_stride(KTD * kTileK, GS);
     static constexpr int SRM = kTileRows * (NGG > NGD ? NGG : NGD);
     static constexpr size_t as_bytes = (size_t)KTM * 4 * 64 * 8 * 2;
-    static constexpr size_t ss_bytes = (size_t)4 * 2 * SRM * 2;
+    static constexpr size_t ss_bytes = ((size_t)4 * 2 * SRM * 2 + 15) / 16 * 16;
+    static constexpr size_t cs_bytes = (size_t)KTM * GPT * 16 * 4;  // bias seeds [group][16 tokens] f32
     static constexpr int n_ints = kFusedMaxSeq * kMaxTopK + 2 * kMaxExperts + 4 * 16 + 4;
-    static constexpr size_t bytes = as_bytes + ss_bytes + (size_t)n_ints * 4;
+    static constexpr size_t bytes = as_bytes + ss_bytes + cs_bytes + (size_t)n_ints * 4;
 };
 
-// One wave's 16 rows x KT k-tiles against the staged A rows: four MFMA steps per
-// k-tile, LDS operands read one k-tile ahead (asm reads, explicit lgkmcnt waits).
-template <int GPT, int KT, bool GU>
+// Bias seeds of the staged A rows (As, the MFMA fragment layout: region
+// kt*4 + s holds k = kt*128 + s*32 .. +32, lane t + 16c the eight k from 8c of
+// token t): for scale group g of the item and token t, Cs[g][t] =
+// -(1032 * sum of A at the positions that dequant8_biased biases by 1024 +
+// 72 * sum at the positions biased by 64), summed with v_dot2_f32_f16.
+template <int KT, int GPT>
+__device__ __forceinline__ void bias_seeds(const f16* As, float* Cs, int tid) {
+    constexpr int NGI = KT * GPT;
+    const f16x2 one = {(f16)1.0f, (f16)1.0f};
+    for (int p = tid; p < NGI * 16; p += 256) {
+        const int g = p >> 4, t = p & 15, kt = g / GPT, gi = g % GPT;
+        float xe = 0.0f, xo = 0.0f;
+#pragma unroll
+        for (int s = gi * 4 / GPT; s < (gi + 1) * 4 / GPT; ++s)
+            {
+                // asm reads: a plain LDS read after the DMA staging would wait
+                // for every outstanding global load (the weights in flight)
+                u32x4 v[4];
+                asm volatile("ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:256\n\t"
+                             "ds_read_b128 %2, %4 offset:512\n\tds_read_b128 %3, %4 offset:768\n\t"
+                             "s_waitcnt lgkmcnt(0)"
+                             : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+                             : "v"(lds_addr(As + ((size_t)(kt * 4 + s) * 64 + t) * 8))
+                             : "memory");
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    xe = __builtin_amdgcn_fdot2(as_h2(v[c][0]), one, xe, false);
+                    xo = __builtin_amdgcn_fdot2(as_h2(v[c][1]), one, xo, false);
+                    xe = __builtin_amdgcn_fdot2(as_h2(v[c][2]), one, xe, false);
+                    xo = __builtin_amdgcn_fdot2(as_h2(v[c][3]), one, xo, false);
+                }
+            }
+        Cs[p] = -(1032.0f * xe + 72.0f * xo);
+    }
+}
+
+// The seeds of the GPT groups of one k-tile for this lane's four tokens
+template <int GPT>
+__device__ __forceinline__ void lds_issue_seeds(uint32_t c_addr, f32x4 (&c)[GPT]) {
+    if constexpr (GPT == 4) {
+        asm volatile("ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:64\n\t"
+                     "ds_read_b128 %2, %4 offset:128\n\tds_read_b128 %3, %4 offset:192"
+                     : "=&v"(c[0]), "=&v"(c[1]), "=&v"(c[2]), "=&v"(c[3]) : "v"(c_addr) : "memory");
+    } else if constexpr (GPT == 2) {
+        asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:64"
+                     : "=&v"(c[0]), "=&v"(c[1]) : "v"(c_addr) : "memory");
+    } else {
+        asm volatile("ds_read_b128 %0, %1" : "=&v"(c[0]) : "v"(c_addr) : "memory");
+    }
+}
+
+// One wave's 16 rows x KT k-tiles (two weight tiles sharing the A rows)
+// against the staged A rows. Per scale group the MFMAs run on the biased
+// nibbles from the group's bias seed, then the group result is scaled into
+// the accumulator (f16 scale x f32, one fma per element). LDS operands are read
+// one k-tile ahead (asm reads, explicit lgkmcnt waits).
+template <int GPT, int KT>
 __device__ __forceinline__ void item_mma(const u32x4 (&bw0)[KT], const u32x4 (&bw1)[KT], uint32_t a_base,
-                                         uint32_t s_base0, uint32_t s_base1, f32x4& acc0, f32x4& acc1) {
+                                         uint32_t s_base0, uint32_t s_base1, uint32_t c_base, f32x4& acc0,
+                                         f32x4& acc1) {
     TileRegs<GPT> tr[2];
+    f32x4 cr[2][GPT];
     lds_issue_tile<GPT>(a_base, s_base0, s_base1, tr[0]);
+    lds_issue_seeds<GPT>(c_base, cr[0]);
+    // the previous group's results, scaled in after the next group's MFMAs
+    // are issued (the MFMA latency is then covered)
+    f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = {0.f, 0.f, 0.f, 0.f};
+    float ps0 = 0.0f, ps1 = 0.0f;
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
         f16 s0[4], s1[4];
         if (kt + 1 < KT) {
             lds_issue_tile<GPT>(a_base + (uint32_t)((kt + 1) * 4096), s_base0 + (uint32_t)((kt + 1) * GPT * 2),
                                 s_base1 + (uint32_t)((kt + 1) * GPT * 2), tr[(kt + 1) & 1]);
-            lds_wait_tile<GPT, 6>(tr[kt & 1], s0, s1);
+            lds_issue_seeds<GPT>(c_base + (uint32_t)((kt + 1) * GPT * 64), cr[(kt + 1) & 1]);
+            lds_wait_tile<GPT, 6 + GPT>(tr[kt & 1], s0, s1);
         } else {
             lds_wait_tile<GPT, 0>(tr[kt & 1], s0, s1);
         }
+#pragma unroll
+        for (int gi = 0; gi < GPT; ++gi) asm volatile("" : "+v"(cr[kt & 1][gi]));  // landed with the tile
         const f16x8* av = tr[kt & 1].av;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            acc0 = mfma16(av[s], dequant8(bw0[kt][s], scale2(s0[s])), acc0);
-            if constexpr (GU) acc1 = mfma16(av[s], dequant8(bw1[kt][s], scale2(s1[s])), acc1);
+        for (int gi = 0; gi < GPT; ++gi) {
+            f32x4 r0 = cr[kt & 1][gi], r1 = cr[kt & 1][gi];
+#pragma unroll
+            for (int s = gi * 4 / GPT; s < (gi + 1) * 4 / GPT; ++s) {
+                r0 = mfma16(av[s], dequant8_biased(bw0[kt][s]), r0);
+                r1 = mfma16(av[s], dequant8_biased(bw1[kt][s]), r1);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                acc0[i] = fmaf(ps0, p0[i], acc0[i]);
+                acc1[i] = fmaf(ps1, p1[i], acc1[i]);
+            }
+            asm volatile("" : "+v"(acc0), "+v"(acc1));  // scaled here, not deferred
+            p0 = r0;
+            p1 = r1;
+            ps0 = (float)s0[gi * 4 / GPT];
+            ps1 = (float)s1[gi * 4 / GPT];
         }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        acc0[i] = fmaf(ps0, p0[i], acc0[i]);
+        acc1[i] = fmaf(ps1, p1[i], acc1[i]);
     }
 }
 
@@ -162,7 +246,7 @@ __device__ __forceinline__ void convert_own_rows(f16* As, int wave, int lane) {
 // other workgroup on the CU dequantises expert weights meanwhile).
 template <int KT>
 __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, float* hand, float* sc, float* topv,
-                                                  uint64_t* etab, float* xs) {
+                                                  uint64_t* etab, float* xs, unsigned rtag) {
     constexpr int SEG = KT * 32;  // columns per wave (H = KT * 128)
     constexpr int NL = SEG / 8;   // 16-byte weight loads per lane
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -229,7 +313,7 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
         }
         lds_barrier();
     }
-    if (wave == 3) router_select<true>(a, t, acc, sc, topv, etab);
+    if (wave == 3) router_select<true>(a, t, acc, sc, topv, etab, a.sync->route, rtag);
     __builtin_amdgcn_s_setprio(0);
     RTR(9)
 }
@@ -243,13 +327,18 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     f16* As = reinterpret_cast<f16*>(smem);
     f16* Ss = reinterpret_cast<f16*>(smem + Lay::as_bytes);  // [4 waves][2][SRM]
-    int* ids_s = reinterpret_cast<int*>(smem + Lay::as_bytes + Lay::ss_bytes);
+    float* Cs = reinterpret_cast<float*>(smem + Lay::as_bytes + Lay::ss_bytes);
+    int* ids_s = reinterpret_cast<int*>(smem + Lay::as_bytes + Lay::ss_bytes + Lay::cs_bytes);
     int* hist = ids_s + kFusedMaxSeq * kMaxTopK;
     int* live = hist + kMaxExperts;
     int* ent = live + kMaxExperts;  // [4 waves][16]
     int* misc = ent + 4 * 16;       // routed live count
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 15;
+    // wave index as a scalar: weight addresses become scalar bases + the lane offset
+    int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, r = lane & 15;
+    // per item: makes the thread indices opaque, so addresses derived from them
+    // are recomputed in each item instead of hoisted (and spilled) across items
+    auto fresh_indices = [&]() { asm volatile("" : "+v"(tid), "+v"(lane), "+v"(r), "+s"(wave)); };
     const int T = a.seq, E = a.n_experts, V = a.n_virtual, G = E + V, K = a.top_k, N = T * K;
     const int H = a.hidden, I = a.inter;
     // gate/up items: 64 rows (one 16-row tile per wave); down items: 128 rows
@@ -263,6 +352,7 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
 
     // this call's base: every workgroup ended the previous call at the same value
     const int S = load_cg(prog + b);
+    const unsigned rtag = (((unsigned)S >> 12) + 1u) & 0xFFFFFFu;  // routing words of this call
     FTR(0)
     int ftr = 2;
     int k = 0;  // steps published by this workgroup
@@ -311,11 +401,35 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
 
     // routing summary: counts per expert, live routed experts ascending, then
     // the shared groups
+    // wave 0: the tagged routing words (N <= 128: two per lane), prefetched
+    // under the last gate/up item, then re-read until every tag is this call's
+    unsigned rw0 = 0, rw1 = 0;
+    bool have_route = false;
+    auto route_prefetch = [&]() {
+        if (wave == 0) {
+            rw0 = lane < N ? load_cg(sy->route + lane) : (rtag << 8);
+            rw1 = lane + 64 < N ? load_cg(sy->route + 64 + lane) : (rtag << 8);
+        }
+        have_route = true;
+    };
     auto need_summary = [&]() {
         if (have_summary) return;
-        wait_steps([&](int t, int& owner, int& step) { owner = t; step = 1; }, T);
+        if (wave == 0) {
+            if (!have_route) route_prefetch();
+            int it = 0;
+            while (__ballot((rw0 >> 8) != rtag || (rw1 >> 8) != rtag)) {
+                if (++it > kSpinLimit) {
+                    if (lane == 0) __hip_atomic_fetch_or(&sy->error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+                if (lane < N) rw0 = load_cg(sy->route + lane);
+                if (lane + 64 < N) rw1 = load_cg(sy->route + 64 + lane);
+            }
+            if (lane < N) ids_s[lane] = (int)(rw0 & 0xFFu);
+            if (lane + 64 < N) ids_s[lane + 64] = (int)(rw1 & 0xFFu);
+        }
         for (int e = tid; e < kMaxExperts; e += 256) hist[e] = 0;
-        for (int i = tid; i < N; i += 256) ids_s[i] = load_cg(a.ids + i);
         __syncthreads();
         for (int i = tid; i < N; i += 256) atomicAdd(&hist[ids_s[i]], 1);
         __syncthreads();
@@ -359,7 +473,7 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
     };
 
     // ---- gate/up item: group g, 64 rows rb*64.. (all_tokens: A = all T rows)
-    auto gate_up_item = [&](int g, int rb, bool all_tokens) {
+    auto gate_up_item = [&](int g, int rb, bool all_tokens, bool prefetch_route) {
         constexpr int KT = KTG;
         constexpr int NG = Lay::NGG;
         constexpr int SROW = kTileRows * NG;
@@ -387,13 +501,19 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
             bw0[kt] = *reinterpret_cast<const u32x4*>(a.gate + toff + (size_t)kt * kTileBytes);
             bw1[kt] = *reinterpret_cast<const u32x4*>(a.up + toff + (size_t)kt * kTileBytes);
         }
-        wait_vm_n(2 * KT);  // A rows and scales (issued before the weights)
+        if (prefetch_route) route_prefetch();  // behind the weights: consumed after the item
+        wait_vm_n(2 * KT + (prefetch_route && wave == 0 ? 2 : 0));  // A rows and scales
         if (stage) convert_own_rows<KT>(As, wave, lane);
         lds_barrier();
+        if (stage) {
+            bias_seeds<KT, GPT>(As, Cs, tid);
+            lds_barrier();
+        }
         if (wave_live) {
             f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-            item_mma<GPT, KT, true>(bw0, bw1, lds_addr(As + (size_t)lane * 8), lds_addr(ssw + r * NG),
-                                    lds_addr(ssw + Lay::SRM + r * NG), acc0, acc1);
+            item_mma<GPT, KT>(bw0, bw1, lds_addr(As + (size_t)lane * 8), lds_addr(ssw + r * NG),
+                              lds_addr(ssw + Lay::SRM + r * NG), lds_addr(Cs) + (uint32_t)(lane >> 4) * 16, acc0,
+                              acc1);
             const int col = rbw * kTileRows + r;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -409,7 +529,12 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
 
     // ---- down item: group g, 128 hidden rows rb*128.. (tiles rb*8 + wave and
     // rb*8 + 4 + wave of this wave)
-    auto down_item = [&](int g, int rb) {
+    // Order of one item: wave 0 polls the gate/up workers of the group (issued
+    // first, so its answer does not queue behind the weights), every wave
+    // issues its weights, then -- once the group's act rows are complete --
+    // the act rows and the scales go to LDS while the weights stream in.
+    // ready(lane, owner, step) names the progress word lane < n_ready waits for.
+    auto down_item = [&](int g, int rb, auto&& ready, int n_ready) {
         constexpr int KT = KTD;
         constexpr int NG = Lay::NGD;
         constexpr int SROW = kTileRows * NG;
@@ -417,6 +542,34 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
         const int cnt = a.dense_dn ? T : token_list(g);
         const int rbw0 = rb * 8 + wave, rbw1 = rbw0 + 4;
         const int rbl0 = min(rbw0, H / kTileRows - 1), rbl1 = min(rbw1, H / kTileRows - 1);
+        int powner = 0, pstep = 0, pv = 0;
+        const bool want = wave == 0 && lane < n_ready;
+        if (want) {
+            ready(lane, powner, pstep);
+            pv = load_cg(prog + powner);
+        }
+        u32x4 bw0[KT], bw1[KT];
+        const size_t toff0 = (size_t)g * a.dn_wstride + (size_t)rbl0 * KT * kTileBytes + (size_t)lane * 16;
+        const size_t toff1 = (size_t)g * a.dn_wstride + (size_t)rbl1 * KT * kTileBytes + (size_t)lane * 16;
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+            bw0[kt] = *reinterpret_cast<const u32x4*>(a.down + toff0 + (size_t)kt * kTileBytes);
+            bw1[kt] = *reinterpret_cast<const u32x4*>(a.down + toff1 + (size_t)kt * kTileBytes);
+        }
+        if (wave == 0) {
+            int it = 0;
+            while (__ballot(want && (int)(pv - (S + pstep)) < 0)) {
+                if (++it > kSpinLimit) {
+                    if (lane == 0) __hip_atomic_fetch_or(&sy->error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+                if (want) pv = load_cg(prog + powner);
+            }
+        }
+        lds_barrier();  // the other waves' weights stay in flight
+        fence_wg_acquire();
+        if (ftr == 8) { FTR(11) }
         if (r < cnt) {
             const int tok = (g < E && !a.dense_dn) ? ent[wave * 16 + r] / K : r;
             const f16* src = a.act + (size_t)(g * T + tok) * I + wave * 32 + 8 * (lane >> 4);
@@ -430,21 +583,17 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
             load_lds16(a.down_s + sb0 + q * 8, ssw + (q & ~63) * 8);
             load_lds16(a.down_s + sb1 + q * 8, ssw + Lay::SRM + (q & ~63) * 8);
         }
-        u32x4 bw0[KT], bw1[KT];
-        const size_t toff0 = (size_t)g * a.dn_wstride + (size_t)rbl0 * KT * kTileBytes + (size_t)lane * 16;
-        const size_t toff1 = (size_t)g * a.dn_wstride + (size_t)rbl1 * KT * kTileBytes + (size_t)lane * 16;
-#pragma unroll
-        for (int kt = 0; kt < KT; ++kt) {
-            bw0[kt] = *reinterpret_cast<const u32x4*>(a.down + toff0 + (size_t)kt * kTileBytes);
-            bw1[kt] = *reinterpret_cast<const u32x4*>(a.down + toff1 + (size_t)kt * kTileBytes);
-        }
-        wait_vm_n(2 * KT);
+        wait_vm<0>();
+        lds_barrier();
+        if (ftr == 8) { FTR(12) }
+        bias_seeds<KT, GPT>(As, Cs, tid);
         lds_barrier();
         if (rbw0 * kTileRows < H) {
             // the two tiles share the A operand: the gate/up MMA shape
             f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-            item_mma<GPT, KT, true>(bw0, bw1, lds_addr(As + (size_t)lane * 8), lds_addr(ssw + r * NG),
-                                    lds_addr(ssw + Lay::SRM + r * NG), acc0, acc1);
+            item_mma<GPT, KT>(bw0, bw1, lds_addr(As + (size_t)lane * 8), lds_addr(ssw + r * NG),
+                              lds_addr(ssw + Lay::SRM + r * NG), lds_addr(Cs) + (uint32_t)(lane >> 4) * 16, acc0,
+                              acc1);
             const bool live1 = rbw1 * kTileRows < H;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -504,7 +653,7 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
         float* sc = hand + 64;
         float* topv = sc + 64;
         uint64_t* etab = reinterpret_cast<uint64_t*>(topv + kMaxTopK);
-        router_token_regs<KTG>(a, b, hand, sc, topv, etab, hand + 256);
+        router_token_regs<KTG>(a, b, hand, sc, topv, etab, hand + 256, rtag);
         publish();
         FTR(1)
     }
@@ -518,21 +667,25 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
     // ---- 2. gate/up (workers T .. P-1). Sparse: shared groups' items first
     // (no routing needed), then the live routed experts'.
     int ngu_total = a.dense ? G * RBG : -1;  // sparse: known with the summary
+#if defined(UOCR_BPRIO)
+    if (b >= P / 2) __builtin_amdgcn_s_setprio(UOCR_BPRIO);
+#endif
 #if defined(UOCR_GU_DELAY)
     if (b >= T) for (int i = 0; i < UOCR_GU_DELAY; ++i) __builtin_amdgcn_s_sleep(32);
 #endif
     if (b >= T) {
         for (int i = b - T;; i += PW) {
+            fresh_indices();
             if (a.dense) {
                 if (i >= ngu_total) break;
-                gate_up_item(i / RBG, i % RBG, true);
+                gate_up_item(i / RBG, i % RBG, true, i + PW >= ngu_total);
             } else if (i < V * RBG) {
-                gate_up_item(E + i / RBG, i % RBG, true);
+                gate_up_item(E + i / RBG, i % RBG, true, false);
             } else {
                 need_summary();
                 const int j = i - V * RBG;
                 if (j >= n_live_r * RBG) break;
-                gate_up_item(live[j / RBG], j % RBG, false);
+                gate_up_item(live[j / RBG], j % RBG, false, false);
             }
             publish();
             if (ftr < 6) { FTR(ftr) ++ftr; }
@@ -544,6 +697,9 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
     // j % RBD); it waits only for its group's gate/up items, so the weight
     // stream runs on from gate/up into down while the router finishes. Sparse:
     // the live groups only (the routing summary first).
+#if defined(UOCR_BPRIO)
+    __builtin_amdgcn_s_setprio(0);
+#endif
     if (!a.dense_dn) need_summary();
     if (!a.dense) ngu_total = (V + n_live_r) * RBG;
     FTR(6)
@@ -571,16 +727,17 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
         step = (owner < T ? 1 : 0) + n_gu_of(owner, ngu_total) + j / P + 1;
     };
     for (int j = my_slot; j < ndn_total; j += P) {
+        fresh_indices();
         const int gpos = j / RBD, rb = j % RBD;
-        wait_steps(
+        if (ftr < 13) { FTR(ftr) ++ftr; }
+        down_item(
+            a.dense_dn ? gpos : live[gpos], rb,
             [&](int q, int& owner, int& step) {
                 const int i = gu_index(gpos, q);
                 owner = T + i % PW;
                 step = i / PW + 1;
             },
             RBG);
-        if (ftr < 13) { FTR(ftr) ++ftr; }
-        down_item(a.dense_dn ? gpos : live[gpos], rb);
         publish();
         if (ftr < 13) { FTR(ftr) ++ftr; }
     }

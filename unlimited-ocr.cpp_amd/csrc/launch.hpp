@@ -110,6 +110,10 @@ constexpr int kFusedMaxGrid = 4096;
 struct FusedSync {
     int progress[kFusedMaxGrid];
     int error;  // a bounded wait timed out (sticky)
+    // routing of this call as (tag << 8) | expert at t * top_k + j, tag =
+    // (base >> 12) + 1 (24 bits): a reader validates each word by its tag, with
+    // no separate wait for the router
+    unsigned route[kFusedMaxSeq * kMaxTopK];
 };
 
 // Decode-sized layer (seq < 256): router_decode / expert passes / combine with
