@@ -167,11 +167,10 @@ __device__ __forceinline__ float wave_max64(float v) {
 // expf table) are LDS of the caller. The greedy scan (strict '>', so the lowest
 // index wins a tie; the pick is then removed) is K rounds of a wave maximum and
 // the lowest lane holding it. COHERENT: ids / weights are written with
-// agent-scope stores that other workgroups read without a cache invalidation;
-// route (optional) also receives (tag << 8) | expert per pick.
+// agent-scope stores that other workgroups read without a cache invalidation.
 template <bool COHERENT>
 __device__ __forceinline__ void router_select(const DecodeArgs& a, int t, float acc, float* sc, float* topv,
-                                              const uint64_t* etab, unsigned* route = nullptr, unsigned tag = 0) {
+                                              const uint64_t* etab) {
     (void)topv;
     const int lane = threadIdx.x & 63;
     const int E = a.n_experts, K = a.top_k;
@@ -216,9 +215,6 @@ __device__ __forceinline__ void router_select(const DecodeArgs& a, int t, float 
     if (rank < K) {
         if constexpr (COHERENT) {
             __hip_atomic_store(a.ids + (size_t)t * K + rank, lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (route)
-                __hip_atomic_store(route + t * K + rank, (tag << 8) | (unsigned)lane, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
         } else {
             a.ids[(size_t)t * K + rank] = lane;
         }

@@ -86,6 +86,17 @@ __device__ __forceinline__ f32x4 load4_cg(const float* p) {
 __device__ __forceinline__ void store_cg_f16(f16* p, f16 v) {
     asm volatile("global_store_short %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
 }
+// 16-byte agent-coherent read (rows other workgroups wrote with sc1 stores)
+// (issue only: the caller waits with wait_rows before using the values)
+__device__ __forceinline__ void load16_cg_issue(f32x4& v, const float* p) {
+    asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=&v"(v) : "v"(p) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_rows(f32x4 (&v)[N]) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
+}
 // 16-byte global -> LDS DMA, agent-coherent read
 __device__ __forceinline__ void load_lds16_cg(const void* src, void* lds_base) {
     __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
@@ -103,7 +114,7 @@ struct FusedLds {
     static constexpr size_t as_bytes = (size_t)KTM * 4 * 64 * 8 * 2;
     static constexpr size_t ss_bytes = ((size_t)4 * 2 * SRM * 2 + 15) / 16 * 16;
     static constexpr size_t cs_bytes = (size_t)KTM * GPT * 16 * 4;  // bias seeds [group][16 tokens] f32
-    static constexpr int n_ints = kFusedMaxSeq * kMaxTopK + 2 * kMaxExperts + 4 * 16 + 4;
+    static constexpr int n_ints = 2 * kFusedMaxSeq + 2 * kMaxExperts + 4 * 16 + 4 + 2 * kFusedMaxSeq * kMaxTopK;
     static constexpr size_t bytes = as_bytes + ss_bytes + cs_bytes + (size_t)n_ints * 4;
 };
 
@@ -246,7 +257,7 @@ __device__ __forceinline__ void convert_own_rows(f16* As, int wave, int lane) {
 // other workgroup on the CU dequantises expert weights meanwhile).
 template <int KT>
 __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, float* hand, float* sc, float* topv,
-                                                  uint64_t* etab, float* xs, unsigned rtag) {
+                                                  uint64_t* etab, float* xs, float* part, unsigned rtag) {
     constexpr int SEG = KT * 32;  // columns per wave (H = KT * 128)
     constexpr int NL = SEG / 8;   // 16-byte weight loads per lane
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -273,9 +284,86 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
     lds_barrier();
     RTR(0)
     const uint32_t xa = lds_addr(xs + wave * SEG);
+
+    // Candidate experts of the token, ahead of the exact chain: this wave's
+    // segment as a blocked sum (8 chains) and the sum of |x w| (part[wave]).
+    auto early_partial = [&]() {
+        float s8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, sa = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            f32x4 c0, c1, w0, w1;
+            asm volatile("ds_read_b128 %0, %2 offset:%3\n\tds_read_b128 %1, %2 offset:%4\n\ts_waitcnt lgkmcnt(0)"
+                         : "=&v"(c0), "=&v"(c1) : "v"(xa), "i"(i * 32), "i"(i * 32 + 16) : "memory");
+            asm volatile(
+                "v_lshlrev_b32 %0, 16, %8\n\tv_and_b32 %1, 0xffff0000, %8\n\t"
+                "v_lshlrev_b32 %2, 16, %9\n\tv_and_b32 %3, 0xffff0000, %9\n\t"
+                "v_lshlrev_b32 %4, 16, %10\n\tv_and_b32 %5, 0xffff0000, %10\n\t"
+                "v_lshlrev_b32 %6, 16, %11\n\tv_and_b32 %7, 0xffff0000, %11"
+                : "=&v"(w0[0]), "=&v"(w0[1]), "=&v"(w0[2]), "=&v"(w0[3]), "=&v"(w1[0]), "=&v"(w1[1]), "=&v"(w1[2]),
+                  "=&v"(w1[3])
+                : "v"(wr[i][0]), "v"(wr[i][1]), "v"(wr[i][2]), "v"(wr[i][3]));
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                s8[c] = fmaf(c0[c], w0[c], s8[c]);
+                s8[4 + c] = fmaf(c1[c], w1[c], s8[4 + c]);
+                sa = fmaf(fabsf(c0[c]), fabsf(w0[c]), sa);
+                sa = fmaf(fabsf(c1[c]), fabsf(w1[c]), sa);
+            }
+        }
+        part[wave * 128 + lane] = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
+        part[wave * 128 + 64 + lane] = sa;
+    };
+    // Every expert that can be among the token's top_k after the exact chain.
+    // The chain's rounding error is at most 2^-24 * H * sum|x w| (recursive
+    // fma summation), the blocked estimate's at most 2^-24 * (SEG / 8 + 6) *
+    // sum|x w|; both with slack. Softmax: candidate when its upper bound
+    // reaches the top_k-th largest lower bound, less the logit distance over
+    // which two probabilities can still round equal (equal scores go to the
+    // lower index). Sigmoid: the same in score space. Published as two tagged
+    // 32-bit halves of the expert mask.
+    auto early_finish = [&]() {
+        const bool valid = lane < E;
+        const float S = ((part[lane] + part[128 + lane]) + part[256 + lane]) + part[384 + lane];
+        const float SA = ((part[64 + lane] + part[192 + lane]) + part[320 + lane]) + part[448 + lane];
+        bool cand;
+        if (__ballot(valid && !(__builtin_isfinite(S) && __builtin_isfinite(SA)))) {
+            cand = valid;
+        } else {
+            const float B = (float)(H + SEG / 8 + 64) * 0x1p-24f * 1.02f * SA + 0x1p-22f * fabsf(S) + 1e-30f;
+            float lo = S - B, hi = S + B;
+            if (a.scoring_sigmoid) {
+                lo = (1.0f - 1e-5f) / (1.0f + __expf(-lo));
+                hi = (1.0f + 1e-5f) / (1.0f + __expf(-hi));
+            }
+            float rem = valid ? lo : -INFINITY, kth = -INFINITY;
+            for (int j = 0; j < a.top_k && j < E; ++j) {
+                kth = wave_max64(rem);
+                const uint64_t tie = __ballot(rem == kth);
+                if (lane == (int)__builtin_ctzll(tie)) rem = -INFINITY;
+            }
+            float slack = 0.0f;
+            if (!a.scoring_sigmoid) {
+                const float mx = wave_max64(valid ? fabsf(hi) : 0.0f);
+                slack = 0x1p-21f * (2.0f + fabsf(kth) + mx);
+            }
+            cand = valid && hi + slack >= kth;
+        }
+        const uint64_t m = __ballot(cand);
+        if (lane < 2) {
+            const uint64_t w = ((uint64_t)rtag << 32) | (uint32_t)(lane == 0 ? m : (m >> 32));
+            __hip_atomic_store(a.sync->cand + 2 * t + lane, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    };
+
+    // every wave estimates its segment first (in parallel); wave 3 selects
+    // the candidates beside wave 0's chain segment
+    early_partial();
+    lds_barrier();
     float acc = 0.0f;
     for (int w = 0; w < 4; ++w) {
-        if (wave == w) {
+        if (wave != w) {
+            if (w == 0 && wave == 3) early_finish();
+        } else {
             if (w > 0) acc = hand[lane];
             RTR(1 + w)
             f32x4 c0, c1, n0, n1;
@@ -313,7 +401,7 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
         }
         lds_barrier();
     }
-    if (wave == 3) router_select<true>(a, t, acc, sc, topv, etab, a.sync->route, rtag);
+    if (wave == 3) router_select<true>(a, t, acc, sc, topv, etab);
     __builtin_amdgcn_s_setprio(0);
     RTR(9)
 }
@@ -328,11 +416,14 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
     f16* As = reinterpret_cast<f16*>(smem);
     f16* Ss = reinterpret_cast<f16*>(smem + Lay::as_bytes);  // [4 waves][2][SRM]
     float* Cs = reinterpret_cast<float*>(smem + Lay::as_bytes + Lay::ss_bytes);
-    int* ids_s = reinterpret_cast<int*>(smem + Lay::as_bytes + Lay::ss_bytes + Lay::cs_bytes);
-    int* hist = ids_s + kFusedMaxSeq * kMaxTopK;
-    int* live = hist + kMaxExperts;
+    // candidate masks per token, token masks per routed group, live groups
+    uint32_t* cm32 = reinterpret_cast<uint32_t*>(smem + Lay::as_bytes + Lay::ss_bytes + Lay::cs_bytes);
+    int* tokmask = reinterpret_cast<int*>(cm32 + 2 * kFusedMaxSeq);
+    int* live = tokmask + kMaxExperts;
     int* ent = live + kMaxExperts;  // [4 waves][16]
     int* misc = ent + 4 * 16;       // routed live count
+    int* ids_c = misc + 4;          // exact routing for the combine
+    float* wts_c = reinterpret_cast<float*>(ids_c + kFusedMaxSeq * kMaxTopK);
 
     // wave index as a scalar: weight addresses become scalar bases + the lane offset
     int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, r = lane & 15;
@@ -399,49 +490,42 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
     bool have_x = false;  // As holds all T token rows as f16
     int n_live_r = 0, n_live = 0;
 
-    // routing summary: counts per expert, live routed experts ascending, then
-    // the shared groups
-    // wave 0: the tagged routing words (N <= 128: two per lane), prefetched
-    // under the last gate/up item, then re-read until every tag is this call's
-    unsigned rw0 = 0, rw1 = 0;
-    bool have_route = false;
-    auto route_prefetch = [&]() {
-        if (wave == 0) {
-            rw0 = lane < N ? load_cg(sy->route + lane) : (rtag << 8);
-            rw1 = lane + 64 < N ? load_cg(sy->route + 64 + lane) : (rtag << 8);
-        }
-        have_route = true;
+    // Routing summary from the candidate masks (a superset of the routing,
+    // published by the router workgroups before their exact chains): per
+    // routed group the mask of its candidate tokens, the live routed groups
+    // ascending, then the shared groups. Wave 0 holds the tagged words
+    // (lane < 2T), prefetched under the last gate/up item and re-read until
+    // every tag is this call's.
+    uint64_t cw = 0;
+    bool have_cw = false;
+    auto cand_prefetch = [&]() {
+        if (wave == 0) cw = lane < 2 * T ? __hip_atomic_load(sy->cand + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                         : ((uint64_t)rtag << 32);
+        have_cw = true;
     };
     auto need_summary = [&]() {
         if (have_summary) return;
         if (wave == 0) {
-            if (!have_route) route_prefetch();
+            if (!have_cw) cand_prefetch();
             int it = 0;
-            while (__ballot((rw0 >> 8) != rtag || (rw1 >> 8) != rtag)) {
+            while (__ballot((uint32_t)(cw >> 32) != rtag)) {
                 if (++it > kSpinLimit) {
                     if (lane == 0) __hip_atomic_fetch_or(&sy->error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     break;
                 }
                 __builtin_amdgcn_s_sleep(1);
-                if (lane < N) rw0 = load_cg(sy->route + lane);
-                if (lane + 64 < N) rw1 = load_cg(sy->route + 64 + lane);
+                if (lane < 2 * T) cw = __hip_atomic_load(sy->cand + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            if (lane < N) ids_s[lane] = (int)(rw0 & 0xFFu);
-            if (lane + 64 < N) ids_s[lane + 64] = (int)(rw1 & 0xFFu);
-        }
-        for (int e = tid; e < kMaxExperts; e += 256) hist[e] = 0;
-        __syncthreads();
-        for (int i = tid; i < N; i += 256) atomicAdd(&hist[ids_s[i]], 1);
-        __syncthreads();
-        if (wave == 0) {
-            int run = 0;
-            for (int e0 = 0; e0 < E; e0 += 64) {
-                const int e = e0 + lane;
-                const int c = e < E ? hist[e] : 0;
-                const uint64_t m = __ballot(c > 0);
-                if (c > 0) live[run + __popcll(m & below)] = e;
-                run += __popcll(m);
-            }
+            if (lane < 2 * T) cm32[lane] = (uint32_t)cw;
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            // lane e: the tokens whose candidates hold expert e
+            int tm = 0;
+            for (int t = 0; t < T; ++t) tm |= (int)((cm32[2 * t + (lane >> 5)] >> (lane & 31)) & 1u) << t;
+            const bool hit = lane < E && tm != 0;
+            tokmask[lane] = lane < E ? tm : 0;
+            const uint64_t m = __ballot(hit);
+            if (hit) live[__popcll(m & below)] = lane;
+            const int run = __popcll(m);
             for (int v = lane; v < V; v += 64) live[run + v] = E + v;
             if (lane == 0) misc[0] = run;
         }
@@ -451,21 +535,18 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
         have_summary = true;
     };
 
-    // this wave's token list for group g (routed: entries t*K+j ascending;
-    // shared: tokens 0..T-1) -> ent[wave][]; returns the count
+    // this wave's token list for group g (routed: its candidate tokens
+    // ascending; shared or dense down: tokens 0..T-1) -> ent[wave][]; returns
+    // the count
     auto token_list = [&](int g) {
         int* el = ent + wave * 16;
-        if (g < E) {
-            int run = 0;
-            for (int base = 0; base < N; base += 64) {
-                const int i = base + lane;
-                const bool hit = i < N && ids_s[i] == g;
-                const uint64_t m = __ballot(hit);
-                if (hit) el[run + __popcll(m & below)] = i;
-                run += __popcll(m);
-            }
+        if (g < E && !a.dense_dn) {
+            const int tm = tokmask[g];
+            const bool hit = lane < T && ((tm >> lane) & 1);
+            const uint64_t m = __ballot(hit);
+            if (hit) el[__popcll(m & below)] = lane;
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            return run;
+            return (int)__popcll(m);
         }
         if (lane < T) el[lane] = lane;
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -473,18 +554,17 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
     };
 
     // ---- gate/up item: group g, 64 rows rb*64.. (all_tokens: A = all T rows)
-    auto gate_up_item = [&](int g, int rb, bool all_tokens, bool prefetch_route) {
+    auto gate_up_item = [&](int g, int rb, bool prefetch_cand) {
         constexpr int KT = KTG;
         constexpr int NG = Lay::NGG;
         constexpr int SROW = kTileRows * NG;
-        const int cnt = all_tokens ? T : token_list(g);
+        const int cnt = T;
         const int rbw = rb * 4 + wave;
         const bool wave_live = rbw * kTileRows < I;
         const int rbl = min(rbw, I / kTileRows - 1);
-        const bool stage = !(all_tokens && have_x);
+        const bool stage = !have_x;
         if (stage && r < cnt) {
-            const int tok = all_tokens ? r : ent[wave * 16 + r] / K;
-            const uint16_t* src = xb + (size_t)tok * H + wave * 32 + 8 * (lane >> 4);
+            const uint16_t* src = xb + (size_t)r * H + wave * 32 + 8 * (lane >> 4);
 #pragma unroll
             for (int kt = 0; kt < KT; ++kt) load_lds16(src + kt * kTileK, As + (size_t)(kt * 4 + wave) * 64 * 8);
         }
@@ -501,8 +581,8 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
             bw0[kt] = *reinterpret_cast<const u32x4*>(a.gate + toff + (size_t)kt * kTileBytes);
             bw1[kt] = *reinterpret_cast<const u32x4*>(a.up + toff + (size_t)kt * kTileBytes);
         }
-        if (prefetch_route) route_prefetch();  // behind the weights: consumed after the item
-        wait_vm_n(2 * KT + (prefetch_route && wave == 0 ? 2 : 0));  // A rows and scales
+        if (prefetch_cand) cand_prefetch();  // behind the weights: consumed after the item
+        wait_vm_n(2 * KT + (prefetch_cand && wave == 0 ? 1 : 0));  // A rows and scales
         if (stage) convert_own_rows<KT>(As, wave, lane);
         lds_barrier();
         if (stage) {
@@ -518,13 +598,10 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int m = 4 * (lane >> 4) + q;
-                if (m < cnt) {
-                    const int tok = all_tokens ? m : ent[wave * 16 + m] / K;
-                    store_cg_f16(a.act + (size_t)(g * T + tok) * I + col, (f16)silu_mul_f(acc0[q], acc1[q]));
-                }
+                if (m < cnt) store_cg_f16(a.act + (size_t)(g * T + m) * I + col, (f16)silu_mul_f(acc0[q], acc1[q]));
             }
         }
-        have_x = all_tokens;
+        have_x = true;
     };
 
     // ---- down item: group g, 128 hidden rows rb*128.. (tiles rb*8 + wave and
@@ -539,7 +616,7 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
         constexpr int NG = Lay::NGD;
         constexpr int SROW = kTileRows * NG;
         have_x = false;
-        const int cnt = a.dense_dn ? T : token_list(g);
+        const int cnt = token_list(g);
         const int rbw0 = rb * 8 + wave, rbw1 = rbw0 + 4;
         const int rbl0 = min(rbw0, H / kTileRows - 1), rbl1 = min(rbw1, H / kTileRows - 1);
         int powner = 0, pstep = 0, pv = 0;
@@ -571,7 +648,7 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
         fence_wg_acquire();
         if (ftr == 8) { FTR(11) }
         if (r < cnt) {
-            const int tok = (g < E && !a.dense_dn) ? ent[wave * 16 + r] / K : r;
+            const int tok = ent[wave * 16 + r];
             const f16* src = a.act + (size_t)(g * T + tok) * I + wave * 32 + 8 * (lane >> 4);
 #pragma unroll
             for (int kt = 0; kt < KT; ++kt) load_lds16_cg(src + kt * kTileK, As + (size_t)(kt * 4 + wave) * 64 * 8);
@@ -599,8 +676,7 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
             for (int q = 0; q < 4; ++q) {
                 const int m = 4 * (lane >> 4) + q;
                 if (m < cnt) {
-                    // dense: y row of (group g, token m) is g*T + m
-                    const int yrow = a.dense_dn ? g * T + m : g < E ? ent[wave * 16 + m] : N + (g - E) * T + m;
+                    const int yrow = g * T + ent[wave * 16 + m];  // (group, token)
                     store_cg(a.y + (size_t)yrow * H + rbw0 * kTileRows + r, acc0[q]);
                     if (live1) store_cg(a.y + (size_t)yrow * H + rbw1 * kTileRows + r, acc1[q]);
                 }
@@ -609,23 +685,29 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
     };
 
     // ---- combine of output columns rb*128 .. rb*128+127 for every token
-    // (src/engine/moe_decoder.cpp:88-97, 110-112). One agent-scope acquire
-    // (an L2 invalidation) and then plain vector loads: cheaper here than a
-    // coherent load per element.
+    // (src/engine/moe_decoder.cpp:88-97, 110-112), y rows read agent-coherent.
     auto combine_block = [&](int rb) {
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         const int t = tid >> 4;
         for (int c = rb * 128 + (tid & 15) * 4; c < min(rb * 128 + 128, H) && t < T; c += 64) {
             float wt[kMaxTopK];
-            f32x4 yv[kMaxTopK];
+            f32x4 yv[kMaxTopK + 2];  // routed rows, then the first two shared rows
 #pragma unroll
             for (int j = 0; j < kMaxTopK; ++j) {
                 if (j < K) {
-                    wt[j] = a.wts[(size_t)t * K + j];
-                    const size_t yrow = a.dense_dn ? (size_t)a.ids[(size_t)t * K + j] * T + t : (size_t)t * K + j;
-                    yv[j] = *reinterpret_cast<const f32x4*>(a.y + yrow * H + c);
+                    wt[j] = wts_c[t * K + j];
+                    const int id = ids_c[t * K + j];
+                    // the exact pick is one of the token's candidates (else its y
+                    // row was not computed: flagged, never silent)
+                    if (!a.dense_dn && !((cm32[2 * t + (id >> 5)] >> (id & 31)) & 1u))
+                        __hip_atomic_fetch_or(&sy->error, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    load16_cg_issue(yv[j], a.y + ((size_t)id * T + t) * H + c);
                 }
             }
+            const size_t sh0 = (size_t)E * T;  // first shared row
+#pragma unroll
+            for (int v = 0; v < 2; ++v)
+                if (v < V) load16_cg_issue(yv[kMaxTopK + v], a.y + (sh0 + (size_t)v * T + t) * H + c);
+            wait_rows(yv);
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < kMaxTopK; ++j)
@@ -633,12 +715,17 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
 #pragma unroll
                     for (int q = 0; q < 4; ++q) acc[q] = fmaf(wt[j], yv[j][q], acc[q]);
             if (V > 0) {
-                const size_t sh0 = a.dense_dn ? (size_t)E * T : (size_t)N;  // first shared row
-                f32x4 sh = *reinterpret_cast<const f32x4*>(a.y + (sh0 + t) * H + c);
+                f32x4 sh = yv[kMaxTopK];
                 for (int v = 1; v < V; ++v) {
-                    const f32x4 y2 = *reinterpret_cast<const f32x4*>(a.y + (sh0 + (size_t)v * T + t) * H + c);
+                    f32x4 y2[1];
+                    if (v < 2) {
+                        y2[0] = yv[kMaxTopK + 1];
+                    } else {
+                        load16_cg_issue(y2[0], a.y + (sh0 + (size_t)v * T + t) * H + c);
+                        wait_rows(y2);
+                    }
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) sh[q] += y2[q];
+                    for (int q = 0; q < 4; ++q) sh[q] += y2[0][q];
                 }
 #pragma unroll
                 for (int q = 0; q < 4; ++q) acc[q] += sh[q];
@@ -653,7 +740,7 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
         float* sc = hand + 64;
         float* topv = sc + 64;
         uint64_t* etab = reinterpret_cast<uint64_t*>(topv + kMaxTopK);
-        router_token_regs<KTG>(a, b, hand, sc, topv, etab, hand + 256, rtag);
+        router_token_regs<KTG>(a, b, hand, sc, topv, etab, hand + 256, hand + 256 + kMaxHidden, rtag);
         publish();
         FTR(1)
     }
@@ -666,7 +753,7 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
 #endif
     // ---- 2. gate/up (workers T .. P-1). Sparse: shared groups' items first
     // (no routing needed), then the live routed experts'.
-    int ngu_total = a.dense ? G * RBG : -1;  // sparse: known with the summary
+    const int ngu_total = G * RBG;
 #if defined(UOCR_BPRIO)
     if (b >= P / 2) __builtin_amdgcn_s_setprio(UOCR_BPRIO);
 #endif
@@ -676,17 +763,8 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
     if (b >= T) {
         for (int i = b - T;; i += PW) {
             fresh_indices();
-            if (a.dense) {
-                if (i >= ngu_total) break;
-                gate_up_item(i / RBG, i % RBG, true, i + PW >= ngu_total);
-            } else if (i < V * RBG) {
-                gate_up_item(E + i / RBG, i % RBG, true, false);
-            } else {
-                need_summary();
-                const int j = i - V * RBG;
-                if (j >= n_live_r * RBG) break;
-                gate_up_item(live[j / RBG], j % RBG, false, false);
-            }
+            if (i >= ngu_total) break;
+            gate_up_item(i / RBG, i % RBG, i + PW >= ngu_total);
             publish();
             if (ftr < 6) { FTR(ftr) ++ftr; }
         }
@@ -700,28 +778,30 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
 #if defined(UOCR_BPRIO)
     __builtin_amdgcn_s_setprio(0);
 #endif
-    if (!a.dense_dn) need_summary();
-    if (!a.dense) ngu_total = (V + n_live_r) * RBG;
+    need_summary();
     FTR(6)
     ftr = 7;
     const int n_dn_groups = a.dense_dn ? G : n_live;
     const int ndn_total = n_dn_groups * RBD;
     // position of gate/up item r of the group at down position gpos
-    auto gu_index = [&](int gpos, int r_) {
-        if (a.dense_dn) return gpos * RBG + r_;
-        if (a.dense) return live[gpos] * RBG + r_;
-        return gpos < n_live_r ? V * RBG + gpos * RBG + r_ : (gpos - n_live_r) * RBG + r_;
-    };
-    // Down items go to "slots" ordered by the gate/up work of the workgroup
-    // behind them (router workgroups first, then workers with fewer gate/up
-    // items), so a second round of down items lands on the least loaded.
-    const int rem = ngu_total % PW;
+    auto gu_index = [&](int gpos, int r_) { return (a.dense_dn ? gpos : live[gpos]) * RBG + r_; };
+    // Down items go to "slots" in the order the workgroups behind them are
+    // expected to be free: workers with one gate/up item fewer, workers that
+    // are first on their CU (issue priority goes to the older workgroup),
+    // the router workgroups (exact chain), then the rest; a second round of
+    // down items lands on the first slots.
+    const int rem = ngu_total % PW;  // workers T .. T+rem-1 hold one item more
+    const int n1 = PW - rem, nA = max(0, min(rem, P / 2 - T));
     auto slot_wg = [&](int sl) {
+        if (sl < n1) return T + rem + sl;
+        sl -= n1;
+        if (sl < nA) return T + sl;
+        sl -= nA;
         if (sl < T) return sl;
-        const int q = sl - T;
-        return q < PW - rem ? T + rem + q : T + (q - (PW - rem));
+        return T + nA + (sl - T);
     };
-    const int my_slot = b < T ? b : ((b - T) >= rem ? T + (b - T - rem) : T + (PW - rem) + (b - T));
+    const int my_slot = b < T ? n1 + nA + b
+                              : (b - T >= rem ? b - T - rem : (b - T < nA ? n1 + (b - T) : n1 + T + (b - T)));
     auto dn_step = [&](int j, int& owner, int& step) {
         owner = slot_wg(j % P);
         step = (owner < T ? 1 : 0) + n_gu_of(owner, ngu_total) + j / P + 1;
@@ -744,16 +824,20 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
     // combine of column block rb by slot (ndn_total + rb) % P, one with the
     // fewest down items, after all of its own (a combine waits only for down
     // items and the router, which never wait for a combine)
+    bool have_route = false;
     for (int rb = 0; rb < RBD; ++rb) {
         if ((ndn_total + rb) % P != my_slot) continue;
-        wait_steps([&](int q, int& owner, int& step) {
-            if (q < T) {  // the router of token q
-                owner = q;
-                step = 1;
-            } else {
-                dn_step((q - T) * RBD + rb, owner, step);
+        if (!have_route) {
+            // the exact routing first (done long before the last down items),
+            // so that the y rows are one round trip after the down items
+            wait_steps([&](int q, int& owner, int& step) { owner = q; step = 1; }, T);
+            for (int i = tid; i < T * K; i += 256) {
+                ids_c[i] = load_cg(a.ids + i);
+                wts_c[i] = load_cg(a.wts + i);
             }
-        }, T + n_dn_groups);
+            have_route = true;
+        }
+        wait_steps([&](int q, int& owner, int& step) { dn_step(q * RBD + rb, owner, step); }, n_dn_groups);
         FTR(13)
         combine_block(rb);
         FTR(14)

@@ -110,10 +110,11 @@ constexpr int kFusedMaxGrid = 4096;
 struct FusedSync {
     int progress[kFusedMaxGrid];
     int error;  // a bounded wait timed out (sticky)
-    // routing of this call as (tag << 8) | expert at t * top_k + j, tag =
-    // (base >> 12) + 1 (24 bits): a reader validates each word by its tag, with
-    // no separate wait for the router
-    unsigned route[kFusedMaxSeq * kMaxTopK];
+    // candidate experts of token t (a superset of its top_k, known before the
+    // exact routing) as (tag << 32) | mask half, experts 0..31 at 2t and 32..63
+    // at 2t + 1; tag = (base >> 12) + 1 (24 bits): a reader validates each word
+    // by its tag, with no separate wait for the router
+    unsigned long long cand[2 * kFusedMaxSeq];
 };
 
 // Decode-sized layer (seq < 256): router_decode / expert passes / combine with
