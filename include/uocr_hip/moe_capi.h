@@ -128,6 +128,13 @@ int uocr_hip_moe_layer_read_timing(uocr_hip_moe_layer* layer, float* stage_ms, i
  * 1 = prefill (LDS-tiled MFMA GEMM). */
 int uocr_hip_moe_layer_path(const uocr_hip_moe_layer* layer, int seq);
 
+/* Sticky fault flags of the single-kernel decode path (no counterpart in the
+ * reference; for callers and tests that verify a run): bit 0 = a bounded wait
+ * between workgroups timed out, bit 1 = an exact top-k pick was outside the
+ * candidate experts the down pass was computed for. Waits for the device,
+ * stores the flags in *flags and, if clear is non-zero, resets them. */
+int uocr_hip_moe_layer_status(uocr_hip_moe_layer* layer, int clear, int* flags);
+
 /* ---- reference operator mirrors (include/uocr/cuda_ops.h) ---------------- */
 
 /* Mirror of uocr::cuda::moe_router_topk (include/uocr/cuda_ops.h:125-131,

@@ -38,6 +38,11 @@ def _check(L, x, got, label):
     assert r <= REL_L2_TOL and m <= MAX_ABS_TOL, label
 
 
+def _status_clear(layer, label):
+    flags = layer.status()
+    assert flags == 0, f"{label}: fused status flags {flags:#x}"
+
+
 @pytest.mark.parametrize("group", [32, 64, 128])
 def test_fused_batch_sizes_one_layer(dev, group):
     """Sparse (seq < 12) and dense (seq >= 12) gate/up on one layer object, the
@@ -49,6 +54,7 @@ def test_fused_batch_sizes_one_layer(dev, group):
         x = synth.bf16_normal(np.random.default_rng(seq * 7 + group), (seq, L.hidden), 1.0)
         print(f"[fused] group={group} seq={seq}", flush=True)
         _check(L, x, _forward(layer, x, dev), f"g{group}-t{seq}")
+    _status_clear(layer, f"g{group}")
     layer.close()
 
 
@@ -116,4 +122,30 @@ def test_fused_graph_replay(dev):
         assert np.array_equal(ids.cpu().numpy(), eager[0]), f"replay {rep}: ids"
         assert np.array_equal(out.cpu().numpy().view(np.uint32), eager[2].view(np.uint32)), f"replay {rep}: out"
         _forward(layer, x_np, dev)  # eager call between replays
+    layer.close()
+
+
+@pytest.mark.parametrize("ulps", [0, 1])
+def test_fused_tied_router_rows(dev, ulps):
+    """Ties at the top-k boundary: five experts lead by a router bias, then a
+    pair whose router rows are identical (ulps=0: equal scores, the lower index
+    wins) or one bf16 ulp apart in one column. The candidate experts must hold
+    every exact pick (status flag bit 1 stays clear) and the output match."""
+    from uocr_hip import MoELayerInt4, synth
+    bias = np.full(64, -1.0, np.float32)
+    bias[[2, 11, 30, 41, 55]] = 2.0
+    bias[[9, 20]] = 1.0
+    L = synth.random_layer(4500 + ulps, router_bias=bias)
+    L.router_bf16[20] = L.router_bf16[9]
+    if ulps:
+        L.router_bf16[20, 100] = L.router_bf16[9, 100] + np.uint16(ulps)
+    layer = MoELayerInt4(L)
+    # small channels 1.. keep the bias order: five leaders, then the pair
+    x = synth.bf16_normal(np.random.default_rng(13), (16, L.hidden), 0.01)
+    x[:, 0] = 1.0
+    got = _forward(layer, x, dev)
+    _check(L, x, got, f"tied-{ulps}")
+    if ulps == 0:
+        assert (got[0] == 9).any(axis=1).all() and not (got[0] == 20).any(), "equal scores: lower index"
+    _status_clear(layer, f"tied-{ulps}")
     layer.close()

@@ -404,6 +404,16 @@ int uocr_hip_moe_layer_path(const uocr_hip_moe_layer* layer, int seq) {
     return (layer && use_prefill(layer, seq)) ? 1 : 0;
 }
 
+int uocr_hip_moe_layer_status(uocr_hip_moe_layer* L, int clear, int* flags) {
+    if (!L || !flags) return fail(UOCR_HIP_EINVAL, "null argument");
+    *flags = 0;
+    if (!L->sync) return UOCR_HIP_OK;
+    HIP_TRY(hipDeviceSynchronize(), "status sync");
+    HIP_TRY(hipMemcpy(flags, &L->sync->error, sizeof(int), hipMemcpyDeviceToHost), "status read");
+    if (clear) HIP_TRY(hipMemset(&L->sync->error, 0, sizeof(int)), "status clear");
+    return UOCR_HIP_OK;
+}
+
 int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x_dtype, int seq,
                                float* out, int* ids_out, float* weights_out, void* workspace,
                                size_t workspace_bytes, void* stream) {

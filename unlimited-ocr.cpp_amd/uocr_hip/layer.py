@@ -80,6 +80,14 @@ class MoELayerInt4:
     def path(self, seq):
         return "prefill" if self.lib.uocr_hip_moe_layer_path(self.handle, seq) else "decode"
 
+    def status(self, clear=True):
+        """Sticky fault flags of the single-kernel decode path (bit 0: a wait
+        between workgroups timed out; bit 1: an exact pick outside the
+        candidate experts). Synchronises the device."""
+        flags = C.c_int(0)
+        check(self.lib.uocr_hip_moe_layer_status(self.handle, 1 if clear else 0, C.byref(flags)))
+        return flags.value
+
     def alloc_workspace(self, seq, device="cuda"):
         import torch
         n = self.workspace_size(seq)
