@@ -119,23 +119,23 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False):
     ms = e0.elapsed_time(e1) / steps
 
     # per-stage durations (HIP events around each launch), same step sequence
+    # (stack: per layer call, over all layers)
     stage = None
-    if not stack:
-        for lay in layers:
-            lay.set_timing(True)
-            lay.read_timing()
-        tot = {}
-        n = 0
-        for i in range(steps):
-            step(i)
-            lay = layers[i % len(layers)]
+    for lay in layers:
+        lay.set_timing(True)
+        lay.read_timing()
+    tot = {}
+    n = 0
+    for i in range(steps):
+        step(i)
+        for lay in (layers if stack else [layers[i % len(layers)]]):
             st, c = lay.read_timing()
             for k, v in st.items():
                 tot[k] = tot.get(k, 0.0) + v
             n += c
-        for lay in layers:
-            lay.set_timing(False)
-        stage = {k: v / max(n, 1) for k, v in tot.items() if v > 0}
+    for lay in layers:
+        lay.set_timing(False)
+    stage = {k: v / max(n, 1) for k, v in tot.items() if v > 0}
 
     torch.cuda.synchronize()
     counts = [np.bincount(t.cpu().numpy().ravel(), minlength=64) for t in ids]
@@ -143,7 +143,7 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False):
            "graph": bool(graph)}
     if stack:
         tb = sum(layer_bytes(L, c, seq)["total"] for L, c in zip(layers_np, counts))
-        res.update(tokens_per_s=seq / (ms * 1e-3), layers=len(layers),
+        res.update(tokens_per_s=seq / (ms * 1e-3), layers=len(layers), stage_ms=stage,
                    hbm_gbs=tb / (ms * 1e-3) / 1e9, hbm_frac=tb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS)
     else:
         lb = [layer_bytes(L, c, seq) for L, c in zip(layers_np, counts)]

@@ -53,6 +53,7 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(DecodeArgs a) {
     __shared__ int ids_s[kDecodeMaxEntries];
     __shared__ int hist[kMaxExperts], offs[kMaxExperts], live[kMaxExperts];
     __shared__ int n_live_s;
+    __shared__ int ipre[kMaxExperts + 1];  // first item of live group i
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int T = a.seq, E = a.n_experts, N = T * a.top_k;
     const int n_rows = GU ? a.inter : a.hidden;
@@ -60,14 +61,16 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(DecodeArgs a) {
 
     // Routing summary, identical in every workgroup: per-expert counts, slot
     // offsets (stable grouping, experts ascending) and the list of live groups
-    // (routed experts with tokens, then the shared-expert groups).
+    // (the shared-expert groups first -- every token, so the longest items --
+    // then the routed experts with tokens).
     for (int e = tid; e < kMaxExperts; e += 256) hist[e] = 0;
     for (int i = tid; i < N; i += 256) ids_s[i] = a.ids[i];
     __syncthreads();
     for (int i = tid; i < N; i += 256) atomicAdd(&hist[ids_s[i]], 1);
     __syncthreads();
     if (wave == 0) {
-        int run_off = 0, run_live = 0;
+        int run_off = 0, run_live = a.n_virtual;
+        for (int v = lane; v < a.n_virtual; v += 64) live[v] = E + v;
         for (int e0 = 0; e0 < E; e0 += 64) {
             const int e = e0 + lane;
             const int c = e < E ? hist[e] : 0;
@@ -83,11 +86,30 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(DecodeArgs a) {
             if (c > 0) live[run_live + __popcll(m & ((1ull << lane) - 1))] = e;
             run_live += __popcll(m);
         }
-        for (int v = lane; v < a.n_virtual; v += 64) live[run_live + v] = E + v;
-        if (lane == 0) n_live_s = run_live + a.n_virtual;
+        if (lane == 0) n_live_s = run_live;
+        // items per live group: RBG row blocks x its 16-token tiles
+        int run_it = 0;
+        for (int i0 = 0; i0 < run_live; i0 += 64) {
+            const int i = i0 + lane;
+            int n = 0;
+            if (i < run_live) {
+                const int g = live[i];
+                const int c = g < E ? hist[g] : T;
+                n = RBG * ((c + kDecBM - 1) / kDecBM);
+            }
+            int inc = n;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int u = __shfl_up(inc, o, kWave);
+                if (lane >= o) inc += u;
+            }
+            if (i < run_live) ipre[i] = run_it + inc - n;
+            run_it += __shfl(inc, 63, kWave);
+        }
+        if (lane == 0) ipre[run_live] = run_it;
     }
     __syncthreads();
-    const int n_items = n_live_s * RBG;
+    const int n_items = ipre[n_live_s];
 
     const int r = lane & 15;
     const uint8_t* wsrc0 = GU ? a.gate : a.down;
@@ -97,9 +119,19 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(DecodeArgs a) {
 
     // work items (live group, 64-row block): grid-strided, so experts without
     // tokens never occupy a workgroup slot
+    // one 16-token tile of one 64-row block per item, so groups with many
+    // tokens (the shared ones see every token) spread over workgroups instead
+    // of serialising their tiles
     for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-        const int g = live[item / RBG];
-        const int rb = (item % RBG) * 4 + wave;
+        int gi = 0;  // live group holding the item: ipre[gi] <= item < ipre[gi + 1]
+        for (int i0 = 0; i0 < n_live_s; i0 += 64) {
+            const int i = i0 + lane;
+            gi += __popcll(__ballot(i < n_live_s && i > 0 && ipre[i] <= item));
+        }
+        const int g = live[gi];
+        const int local = item - ipre[gi];
+        const int m_item = (local / RBG) * kDecBM;
+        const int rb = (local % RBG) * 4 + wave;
         const bool wave_live = rb * kTileRows < n_rows;
         const int cnt = g < E ? hist[g] : T;
         const int slot_base = g < E ? a.n_virtual * T + offs[g] : (g - E) * T;
@@ -131,7 +163,7 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(DecodeArgs a) {
                 for (int kt = 0; kt < KT; ++kt) load_lds16(src + kt * kTileK, As + (size_t)(kt * 4 + wave) * 64 * 8);
             }
         };
-        stage_a(0);
+        stage_a(m_item);
 
         // this wave's scale rows (LDS) and 16 x K weights (registers); no
         // branch around the weight loads (a wave past the last row block
@@ -157,7 +189,7 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(DecodeArgs a) {
         const f16* srow1 = &Ss[wave][GU ? 1 : 0][r * NG];
         const int col = rb * kTileRows + r;
         // one m-tile: MFMAs over all k-tiles and the stores
-        auto tile = [&](int m0, bool first) {
+        auto tile = [&](int m0) {
             if (!wave_live) return;
             const int rows = min(kDecBM, cnt - m0);
             f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
@@ -167,13 +199,6 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(DecodeArgs a) {
             lds_issue_tile<GPT>(a_base, s_base0, s_base1, tr[0]);
 #pragma unroll
             for (int kt = 0; kt < KT; ++kt) {
-                // for later m-tiles the weights are opaque to the optimiser:
-                // hoisting their unpacking out of the m-tile loop would quadruple
-                // the registers they occupy
-                if (!first) {
-                    asm volatile("" : "+v"(bw0[kt]));
-                    if constexpr (GU) asm volatile("" : "+v"(bw1[kt]));
-                }
                 f16 s0[4], s1[4];
                 // this k-tile's LDS operands were issued one k-tile ahead; issue
                 // the next k-tile's before waiting for these
@@ -211,14 +236,7 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(DecodeArgs a) {
         // dequant and MFMAs of early k-tiles overlap the arrival of later ones
         wait_vm_n((GU ? 2 : 1) * KT);
         lds_barrier();
-        tile(0, true);
-        for (int m0 = kDecBM; m0 < cnt; m0 += kDecBM) {
-            __syncthreads();  // every wave is done with the previous tile's As
-            stage_a(m0);
-            wait_vm<0>();
-            lds_barrier();
-            tile(m0, false);
-        }
+        tile(m_item);
         __syncthreads();  // As / Ss / ent are reused by the next item
     }
 }
