@@ -186,11 +186,12 @@ bool use_prefill(const uocr_hip_moe_layer* L, int seq) {
     return seq >= kPrefillMinSeq || !decode_shapes_ok(L->hidden, L->inter);
 }
 
-// Fused decode kernel (router + experts + combine in one launch) up to
-// kFusedMaxSeq tokens, bf16 input without the fused RMSNorm; its gate/up pass
-// covers every group for all tokens (no wait for routing) from kDenseMinSeq
-// tokens, where most experts are live anyway (1 - (1 - 6/64)^12 = 69 % at
-// top-6 of 64). UOCR_FUSED=0 / UOCR_DENSE=0|1 override the choice (testing).
+// Fused decode kernel (router + experts + combine in one launch) for
+// kDenseMinSeq .. kFusedMaxSeq tokens, bf16 input without the fused RMSNorm:
+// its gate/up pass covers every group for all tokens (no wait for routing),
+// worth it once most experts are live anyway (1 - (1 - 6/64)^12 = 69 % at
+// top-6 of 64); fewer tokens take the four-launch decode path.
+// UOCR_FUSED=0 selects that path throughout (testing).
 constexpr int kDenseMinSeq = 12;
 
 int env_int(const char* name, int dflt) {
@@ -200,14 +201,11 @@ int env_int(const char* name, int dflt) {
 
 bool use_fused(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
     static const int on = env_int("UOCR_FUSED", 1);
-    return on && L->sync && seq <= kFusedMaxSeq && x_dtype == UOCR_HIP_DTYPE_BF16 && !L->rms_weight &&
+    return on && L->sync && seq >= kDenseMinSeq && seq <= kFusedMaxSeq && x_dtype == UOCR_HIP_DTYPE_BF16 &&
+           !L->rms_weight &&
            decode_fused_ok(L->hidden, L->inter, L->group) && L->n_experts + L->n_virtual <= kMaxExperts;
 }
 
-bool use_dense(int seq) {
-    static const int force = env_int("UOCR_DENSE", -1);
-    return force >= 0 ? force > 0 : seq >= kDenseMinSeq;
-}
 
 WsPlan plan(const uocr_hip_moe_layer* L, int seq) {
     WsPlan p{};
@@ -486,9 +484,8 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
         da.out = out;
         if (use_fused(L, seq, x_dtype)) {
             da.sync = L->sync;
-            da.dense = use_dense(seq);
             static const int dense_dn = env_int("UOCR_DENSE_DN", 0);
-            da.dense_dn = da.dense && dense_dn > 0;
+            da.dense_dn = dense_dn > 0;
             stage(5);
             HIP_TRY(launch_decode_fused(da, st), "fused decode launch");
             stage(-1);

@@ -1,34 +1,38 @@
-// Fused decode layer (seq <= 16, bf16 input, no fused RMSNorm): router, gate/up,
-// down and combine in ONE persistent kernel driven by an atomic work queue.
+// Fused decode layer (12..16 tokens, bf16 input, no fused RMSNorm): router,
+// gate/up, down and combine in ONE persistent launch (two workgroups per CU,
+// the grid fully resident and the same on every call).
 //
 // The stand-alone decode path (decode_path.hip) runs four kernels in order. At
 // 16 tokens the router is latency-bound (the reference's sequential fmaf chain
 // per (token, expert), src/kernels/cpu_ops.cpp:26-39) and every kernel boundary
-// drains the chip. Here the queue hands out tickets in dependency order:
+// drains the chip. Here every workgroup derives the same static schedule:
 //
-//   [0, T)                 router, one token per workgroup (router_token)
-//   [T, T + G*RBG)         gate/up items (group g, 64 rows): dense mode computes
-//                          every group for all T tokens, so these need no
-//                          routing and stream weights while the router runs;
-//                          sparse mode (few tokens) computes live groups only
-//   [.., + G*RBD)          down items (live group, 64 hidden rows): wait for the
-//                          routing and for the group's gate/up items
+//   workgroups [0, T)   the router of token t: first the candidate experts (a
+//                       bounded estimate of the logits, published at once),
+//                       then the exact chain, scores and top_k
+//   workgroups [T, P)   gate/up items (group g, 64 inter rows) for every group
+//                       and all T tokens, round-robin: no wait for routing
+//   every workgroup     then down items (live group, 128 hidden rows), live =
+//                       a candidate of some token or shared, in slots ordered
+//                       by when their workgroups are expected to be free; a
+//                       down item waits for its group's gate/up items only
+//   one slot per block  the weighted combine of 128 output columns with the
+//                       exact routing (src/engine/moe_decoder.cpp:88-97,
+//                       110-112), after the down items of the block
 //
-// The workgroup that finishes the last down item of a 64-column block of the
-// output runs the weighted combine of that block (src/engine/moe_decoder.cpp:
-// 88-97, 110-112). A workgroup only ever waits for tickets handed out before
-// its own, which are held by running workgroups, so the queue cannot deadlock
-// whatever the number of resident workgroups; every wait is also bounded
-// (kSpinLimit) and records a timeout in FusedSync::error instead of hanging.
+// Waiting is on per-workgroup progress words (FusedSync, layer-owned): a
+// workgroup publishes S + steps done, S being its word at kernel start (every
+// word ends a call at S + kFusedSteps). A workgroup only waits for steps that
+// other resident workgroups reach without waiting for it, and every wait is
+// bounded (kSpinLimit), setting a sticky flag in FusedSync::error on timeout.
 //
-// Cross-workgroup data (ids / weights, act rows, y rows) is written and read
-// with agent-coherent accesses around counter increments (see load_cg); the
-// counters live in a layer-owned FusedSync that the last workgroup to leave
-// returns to zero.
-//
-// act row of (group g, token t) is g * T + t; y is indexed by entry as in the
-// stand-alone path ((t, j) at t * top_k + j, shared group v at T * top_k + v*T + t).
+// Cross-workgroup data (candidate words, ids / weights, act rows, y rows) is
+// written and read with agent-coherent (sc1) accesses around the progress
+// stores; act and y rows are indexed by (group, token): g * T + t.
 #include <hip/hip_runtime.h>
+// Timeline trace build (-DUOCR_FTRACE, never the shipped library): FTR(i)
+// stamps workgroup phase i, RTR(i) router step i, with the 100 MHz wall clock;
+// uocr_ftrace_read / uocr_rtrace_read copy the stamps to the host.
 #if defined(UOCR_FTRACE)
 __device__ unsigned long long uocr_ftrace[4096 * 16];
 extern "C" hipError_t uocr_ftrace_read(void* host, size_t bytes) {
@@ -406,11 +410,9 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
     RTR(9)
 }
 
-#ifndef UOCR_FUSED_WPE
-#define UOCR_FUSED_WPE 2
-#endif
+constexpr int kFusedWGPerCU = 2;  // workgroups per CU (the progress words need them all resident)
 template <int GPT, int KTG, int KTD>
-__global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(DecodeArgs a) {
     using Lay = FusedLds<GPT, KTG, KTD>;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     f16* As = reinterpret_cast<f16*>(smem);
@@ -745,21 +747,8 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
         FTR(1)
     }
 
-#if defined(UOCR_ROUTER_ONLY)
-    __syncthreads();
-    if (tid == 0) store_cg(prog + b, S + kFusedSteps);
-    FTR(15)
-    return;
-#endif
-    // ---- 2. gate/up (workers T .. P-1). Sparse: shared groups' items first
-    // (no routing needed), then the live routed experts'.
+    // ---- 2. gate/up (workers T .. P-1): every group for all tokens
     const int ngu_total = G * RBG;
-#if defined(UOCR_BPRIO)
-    if (b >= P / 2) __builtin_amdgcn_s_setprio(UOCR_BPRIO);
-#endif
-#if defined(UOCR_GU_DELAY)
-    if (b >= T) for (int i = 0; i < UOCR_GU_DELAY; ++i) __builtin_amdgcn_s_sleep(32);
-#endif
     if (b >= T) {
         for (int i = b - T;; i += PW) {
             fresh_indices();
@@ -775,9 +764,6 @@ __global__ __launch_bounds__(256, UOCR_FUSED_WPE) void decode_fused_kernel(Decod
     // j % RBD); it waits only for its group's gate/up items, so the weight
     // stream runs on from gate/up into down while the router finishes. Sparse:
     // the live groups only (the routing summary first).
-#if defined(UOCR_BPRIO)
-    __builtin_amdgcn_s_setprio(0);
-#endif
     need_summary();
     FTR(6)
     ftr = 7;

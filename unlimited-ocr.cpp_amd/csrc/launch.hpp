@@ -140,8 +140,7 @@ struct DecodeArgs {
     const uint16_t* down_s;
     long long gu_wstride, gu_sstride, dn_wstride, dn_sstride;
     FusedSync* sync;           // fused kernel only
-    int dense;                 // fused kernel: gate/up over every group and token
-    int dense_dn;              // fused kernel: down as well (needs dense)
+    int dense_dn;              // fused kernel: down over every group and token as well (testing)
     f16* act;                  // [slots, inter]; fused: [(E + n_virtual) * seq, inter]
     float* y;                  // [slots, hidden]
     float* out;                // [seq, hidden]
