@@ -222,7 +222,8 @@ __device__ __forceinline__ void router_select(const DecodeArgs& a, int t, float 
 }
 
 // One token's routing by one 256-thread workgroup: rsmem = RING chunks of the
-// router matrix, then the token row as f32 (H floats). Waves 1..3 return after
+// router matrix, then the token row as f32 (H floats), then H + 32 floats of
+// scratch for the RMSNorm. Waves 1..3 return after
 // the logits; wave 0 scores, selects and writes ids / weights (and x16) --
 // COHERENT: as agent-scope stores that other workgroups read without a cache
 // invalidation.
@@ -254,16 +255,51 @@ __device__ __forceinline__ void router_token(const DecodeArgs& a, int t, unsigne
 
     if constexpr (RMS) {
         // src/kernels/cpu_ops.cpp:58-67 as the reference build computes it: the
-        // products x*x rounded, summed in column order; the last H % 4 terms fused
+        // products x*x rounded, summed in column order (the last H % 4 terms would
+        // be fused; H is a multiple of 128 on this path)
+        // The rounded products in parallel (LDS after the token row), then one
+        // lane adds them in column order, its LDS reads one 32-column step
+        // ahead of the adds (asm reads with explicit waits: the compiler's
+        // schedule waited on every read). H is a multiple of 128 here.
+        float* pq = xs + H;
+        for (int c = tid; c < H; c += 256) pq[c] = __fmul_rn(xs[c], xs[c]);
+        __syncthreads();
         if (tid == 0) {
+            // 32 columns per step: eight 16-byte reads at immediate offsets,
+            // the next step's issued before this step's adds (one instruction
+            // per column beyond the add)
+            uint32_t pb = lds_addr(pq);
+            f32x4 cur[8], nxt[8];
+            asm volatile("ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:16\n\t"
+                         "ds_read_b128 %2, %8 offset:32\n\tds_read_b128 %3, %8 offset:48\n\t"
+                         "ds_read_b128 %4, %8 offset:64\n\tds_read_b128 %5, %8 offset:80\n\t"
+                         "ds_read_b128 %6, %8 offset:96\n\tds_read_b128 %7, %8 offset:112\n\t"
+                         "s_waitcnt lgkmcnt(0)"
+                         : "=&v"(cur[0]), "=&v"(cur[1]), "=&v"(cur[2]), "=&v"(cur[3]), "=&v"(cur[4]), "=&v"(cur[5]),
+                           "=&v"(cur[6]), "=&v"(cur[7])
+                         : "v"(pb)
+                         : "memory");
             float ss = 0.0f;
-            const int h4 = H & ~3;
-            for (int c = 0; c < h4; c += 4) {
-                const f32x4 v = *reinterpret_cast<const f32x4*>(xs + c);
+            for (int c = 0; c < H; c += 32) {
+                pb += 128u;  // the next step (past the end: the pad, never added)
+                asm volatile("ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:16\n\t"
+                             "ds_read_b128 %2, %8 offset:32\n\tds_read_b128 %3, %8 offset:48\n\t"
+                             "ds_read_b128 %4, %8 offset:64\n\tds_read_b128 %5, %8 offset:80\n\t"
+                             "ds_read_b128 %6, %8 offset:96\n\tds_read_b128 %7, %8 offset:112"
+                             : "=&v"(nxt[0]), "=&v"(nxt[1]), "=&v"(nxt[2]), "=&v"(nxt[3]), "=&v"(nxt[4]), "=&v"(nxt[5]),
+                               "=&v"(nxt[6]), "=&v"(nxt[7])
+                             : "v"(pb)
+                             : "memory");
 #pragma unroll
-                for (int i = 0; i < 4; ++i) ss = __fadd_rn(ss, __fmul_rn(v[i], v[i]));
+                for (int k = 0; k < 8; ++k)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) ss = __fadd_rn(ss, cur[k][q]);
+                asm volatile("s_waitcnt lgkmcnt(0)"
+                             : "+v"(nxt[0]), "+v"(nxt[1]), "+v"(nxt[2]), "+v"(nxt[3]), "+v"(nxt[4]), "+v"(nxt[5]),
+                               "+v"(nxt[6]), "+v"(nxt[7]), "+v"(ss));
+#pragma unroll
+                for (int k = 0; k < 8; ++k) cur[k] = nxt[k];
             }
-            for (int c = h4; c < H; ++c) ss = fmaf(xs[c], xs[c], ss);
             sc[0] = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)H), a.rms_eps)));
         }
         __syncthreads();

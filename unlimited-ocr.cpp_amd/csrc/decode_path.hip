@@ -349,7 +349,7 @@ hipError_t launch_router_decode(const DecodeArgs& a, hipStream_t st) {
     if (a.n_experts > 64 || a.hidden > kMaxHidden || a.hidden % 8) return hipErrorInvalidValue;
     if (a.hidden % kRChunkCols) return hipErrorInvalidValue;
     const dim3 grid(a.seq);
-    const size_t lds = (size_t)kRRing * kRChunkBytes + (size_t)a.hidden * 4;
+    const size_t lds = (size_t)kRRing * kRChunkBytes + (size_t)a.hidden * 8 + 128;
     const bool rms = a.rms_weight != nullptr;
     if (a.x_bf16) {
         if (rms) return launch_rd<uint16_t, true>(a, grid, lds, st);
