@@ -93,30 +93,41 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False):
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
-    g = None
-    if graph:
-        g = torch.cuda.CUDAGraph()
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            step(0)
-        torch.cuda.current_stream().wait_stream(s)
-        torch.cuda.synchronize()
-        with torch.cuda.graph(g):
-            step(0)
-        g.replay()
-        torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    for i in range(steps):
-        if g is not None:
+    def timed(use_graph):
+        """ms per step, eagerly launched or replayed from a hipGraph. A graph
+        holds one call per weight replica (every replica once per replay, so the
+        weights still stream from HBM, not from the memory-side cache)."""
+        per = 1 if stack else len(layers)
+        g = None
+        if use_graph:
+            g = torch.cuda.CUDAGraph()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                for i in range(per):
+                    step(i)
+            torch.cuda.current_stream().wait_stream(s)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g):
+                for i in range(per):
+                    step(i)
             g.replay()
-        else:
-            step(i)
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+            torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        n = max(1, steps // per) if g is not None else steps
+        e0.record()
+        for i in range(n):
+            if g is not None:
+                g.replay()
+            else:
+                step(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / (n * per if g is not None else n)
+
+    ms = timed(graph)
+    ms_eager = ms if not graph else (timed(False) if not stack else None)
 
     # per-stage durations (HIP events around each launch), same step sequence
     # (stack: per layer call, over all layers)
@@ -141,6 +152,8 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False):
     counts = [np.bincount(t.cpu().numpy().ravel(), minlength=64) for t in ids]
     res = {"config": cfg, "workload": wl.name, "seq": seq, "group": group, "ms_per_step": ms,
            "graph": bool(graph)}
+    if ms_eager is not None and graph:
+        res["ms_per_step_eager"] = ms_eager
     if stack:
         tb = sum(layer_bytes(L, c, seq)["total"] for L, c in zip(layers_np, counts))
         res.update(tokens_per_s=seq / (ms * 1e-3), layers=len(layers), stage_ms=stage,
