@@ -122,115 +122,6 @@ struct FusedLds {
     static constexpr size_t bytes = as_bytes + ss_bytes + cs_bytes + (size_t)n_ints * 4;
 };
 
-// Bias seeds of the staged A rows (As, the MFMA fragment layout: region
-// kt*4 + s holds k = kt*128 + s*32 .. +32, lane t + 16c the eight k from 8c of
-// token t): for scale group g of the item and token t, Cs[g][t] =
-// -(1032 * sum of A at the positions that dequant8_biased biases by 1024 +
-// 72 * sum at the positions biased by 64), summed with v_dot2_f32_f16.
-template <int KT, int GPT>
-__device__ __forceinline__ void bias_seeds(const f16* As, float* Cs, int tid) {
-    constexpr int NGI = KT * GPT;
-    const f16x2 one = {(f16)1.0f, (f16)1.0f};
-    for (int p = tid; p < NGI * 16; p += 256) {
-        const int g = p >> 4, t = p & 15, kt = g / GPT, gi = g % GPT;
-        float xe = 0.0f, xo = 0.0f;
-#pragma unroll
-        for (int s = gi * 4 / GPT; s < (gi + 1) * 4 / GPT; ++s)
-            {
-                // asm reads: a plain LDS read after the DMA staging would wait
-                // for every outstanding global load (the weights in flight)
-                u32x4 v[4];
-                asm volatile("ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:256\n\t"
-                             "ds_read_b128 %2, %4 offset:512\n\tds_read_b128 %3, %4 offset:768\n\t"
-                             "s_waitcnt lgkmcnt(0)"
-                             : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
-                             : "v"(lds_addr(As + ((size_t)(kt * 4 + s) * 64 + t) * 8))
-                             : "memory");
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    xe = __builtin_amdgcn_fdot2(as_h2(v[c][0]), one, xe, false);
-                    xo = __builtin_amdgcn_fdot2(as_h2(v[c][1]), one, xo, false);
-                    xe = __builtin_amdgcn_fdot2(as_h2(v[c][2]), one, xe, false);
-                    xo = __builtin_amdgcn_fdot2(as_h2(v[c][3]), one, xo, false);
-                }
-            }
-        Cs[p] = -(1032.0f * xe + 72.0f * xo);
-    }
-}
-
-// The seeds of the GPT groups of one k-tile for this lane's four tokens
-template <int GPT>
-__device__ __forceinline__ void lds_issue_seeds(uint32_t c_addr, f32x4 (&c)[GPT]) {
-    if constexpr (GPT == 4) {
-        asm volatile("ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:64\n\t"
-                     "ds_read_b128 %2, %4 offset:128\n\tds_read_b128 %3, %4 offset:192"
-                     : "=&v"(c[0]), "=&v"(c[1]), "=&v"(c[2]), "=&v"(c[3]) : "v"(c_addr) : "memory");
-    } else if constexpr (GPT == 2) {
-        asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:64"
-                     : "=&v"(c[0]), "=&v"(c[1]) : "v"(c_addr) : "memory");
-    } else {
-        asm volatile("ds_read_b128 %0, %1" : "=&v"(c[0]) : "v"(c_addr) : "memory");
-    }
-}
-
-// One wave's 16 rows x KT k-tiles (two weight tiles sharing the A rows)
-// against the staged A rows. Per scale group the MFMAs run on the biased
-// nibbles from the group's bias seed, then the group result is scaled into
-// the accumulator (f16 scale x f32, one fma per element). LDS operands are read
-// one k-tile ahead (asm reads, explicit lgkmcnt waits).
-template <int GPT, int KT>
-__device__ __forceinline__ void item_mma(const u32x4 (&bw0)[KT], const u32x4 (&bw1)[KT], uint32_t a_base,
-                                         uint32_t s_base0, uint32_t s_base1, uint32_t c_base, f32x4& acc0,
-                                         f32x4& acc1) {
-    TileRegs<GPT> tr[2];
-    f32x4 cr[2][GPT];
-    lds_issue_tile<GPT>(a_base, s_base0, s_base1, tr[0]);
-    lds_issue_seeds<GPT>(c_base, cr[0]);
-    // the previous group's results, scaled in after the next group's MFMAs
-    // are issued (the MFMA latency is then covered)
-    f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = {0.f, 0.f, 0.f, 0.f};
-    float ps0 = 0.0f, ps1 = 0.0f;
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-        f16 s0[4], s1[4];
-        if (kt + 1 < KT) {
-            lds_issue_tile<GPT>(a_base + (uint32_t)((kt + 1) * 4096), s_base0 + (uint32_t)((kt + 1) * GPT * 2),
-                                s_base1 + (uint32_t)((kt + 1) * GPT * 2), tr[(kt + 1) & 1]);
-            lds_issue_seeds<GPT>(c_base + (uint32_t)((kt + 1) * GPT * 64), cr[(kt + 1) & 1]);
-            lds_wait_tile<GPT, 6 + GPT>(tr[kt & 1], s0, s1);
-        } else {
-            lds_wait_tile<GPT, 0>(tr[kt & 1], s0, s1);
-        }
-#pragma unroll
-        for (int gi = 0; gi < GPT; ++gi) asm volatile("" : "+v"(cr[kt & 1][gi]));  // landed with the tile
-        const f16x8* av = tr[kt & 1].av;
-#pragma unroll
-        for (int gi = 0; gi < GPT; ++gi) {
-            f32x4 r0 = cr[kt & 1][gi], r1 = cr[kt & 1][gi];
-#pragma unroll
-            for (int s = gi * 4 / GPT; s < (gi + 1) * 4 / GPT; ++s) {
-                r0 = mfma16(av[s], dequant8_biased(bw0[kt][s]), r0);
-                r1 = mfma16(av[s], dequant8_biased(bw1[kt][s]), r1);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                acc0[i] = fmaf(ps0, p0[i], acc0[i]);
-                acc1[i] = fmaf(ps1, p1[i], acc1[i]);
-            }
-            asm volatile("" : "+v"(acc0), "+v"(acc1));  // scaled here, not deferred
-            p0 = r0;
-            p1 = r1;
-            ps0 = (float)s0[gi * 4 / GPT];
-            ps1 = (float)s1[gi * 4 / GPT];
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        acc0[i] = fmaf(ps0, p0[i], acc0[i]);
-        acc1[i] = fmaf(ps1, p1[i], acc1[i]);
-    }
-}
-
 // bf16 token rows DMA'd into As by this lane -> f16 in place (the lane's own
 // 16 bytes of every k-tile; its DMA has landed once the caller has waited)
 template <int KT>
