@@ -580,39 +580,52 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
     // ---- combine of output columns rb*128 .. rb*128+127 for every token
     // (src/engine/moe_decoder.cpp:88-97, 110-112), y rows read agent-coherent.
     auto combine_block = [&](int rb) {
+        // this thread: token t, columns c0 and c0 + 64 (both chunks' y rows are
+        // requested before the one wait)
         const int t = tid >> 4;
-        for (int c = rb * 128 + (tid & 15) * 4; c < min(rb * 128 + 128, H) && t < T; c += 64) {
-            float wt[kMaxTopK];
-            f32x4 yv[kMaxTopK + 2];  // routed rows, then the first two shared rows
+        if (t >= T) return;
+        constexpr int NY = kMaxTopK + 2;  // routed rows, then the first two shared rows
+        const size_t sh0 = (size_t)E * T;  // first shared row
+        const int c0 = rb * 128 + (tid & 15) * 4;
+        float wt[kMaxTopK];
+        f32x4 yv[2 * NY];
 #pragma unroll
-            for (int j = 0; j < kMaxTopK; ++j) {
-                if (j < K) {
-                    wt[j] = wts_c[t * K + j];
-                    const int id = ids_c[t * K + j];
-                    // the exact pick is one of the token's candidates (else its y
-                    // row was not computed: flagged, never silent)
-                    if (!a.dense_dn && !((cm32[2 * t + (id >> 5)] >> (id & 31)) & 1u))
-                        __hip_atomic_fetch_or(&sy->error, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    load16_cg_issue(yv[j], a.y + ((size_t)id * T + t) * H + c);
-                }
+        for (int j = 0; j < kMaxTopK; ++j) {
+            if (j < K) {
+                wt[j] = wts_c[t * K + j];
+                const int id = ids_c[t * K + j];
+                // the exact pick is one of the token's candidates (else its y
+                // row was not computed: flagged, never silent)
+                if (!a.dense_dn && !((cm32[2 * t + (id >> 5)] >> (id & 31)) & 1u))
+                    __hip_atomic_fetch_or(&sy->error, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    if (c0 + 64 * h < H) load16_cg_issue(yv[h * NY + j], a.y + ((size_t)id * T + t) * H + c0 + 64 * h);
             }
-            const size_t sh0 = (size_t)E * T;  // first shared row
+        }
 #pragma unroll
-            for (int v = 0; v < 2; ++v)
-                if (v < V) load16_cg_issue(yv[kMaxTopK + v], a.y + (sh0 + (size_t)v * T + t) * H + c);
-            wait_rows(yv);
+        for (int v = 0; v < 2; ++v)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                if (v < V && c0 + 64 * h < H)
+                    load16_cg_issue(yv[h * NY + kMaxTopK + v], a.y + (sh0 + (size_t)v * T + t) * H + c0 + 64 * h);
+        wait_rows(yv);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int c = c0 + 64 * h;
+            if (c >= H) continue;
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < kMaxTopK; ++j)
                 if (j < K)
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) acc[q] = fmaf(wt[j], yv[j][q], acc[q]);
+                    for (int q = 0; q < 4; ++q) acc[q] = fmaf(wt[j], yv[h * NY + j][q], acc[q]);
             if (V > 0) {
-                f32x4 sh = yv[kMaxTopK];
+                f32x4 sh = yv[h * NY + kMaxTopK];
                 for (int v = 1; v < V; ++v) {
                     f32x4 y2[1];
                     if (v < 2) {
-                        y2[0] = yv[kMaxTopK + 1];
+                        y2[0] = yv[h * NY + kMaxTopK + 1];
                     } else {
                         load16_cg_issue(y2[0], a.y + (sh0 + (size_t)v * T + t) * H + c);
                         wait_rows(y2);
