@@ -180,9 +180,15 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False):
             res["gate_up_tflops"] = fl_gu / gu / 1e12
             res["gate_up_hbm_frac"] = res["gate_up_gbs"] / HBM_PEAK_GBS
             res["gate_up_mfma_frac"] = res["gate_up_tflops"] / MFMA_PEAK_TFLOPS
-            res["dominant"] = {"kernel": "expert_decode_kernel<4, 10, true> (gate+up)", "ms": stage["gate_up"],
-                               "bytes": avg["gate_up"], "gbs": res["gate_up_gbs"],
-                               "traffic_file": "expert_gate_up_decode_config1_traffic.md"}
+            if seq >= 256:  # prefill path: the large-tile MFMA kernel, MFMA-bound
+                res["dominant"] = {"kernel": f"experts_prefill_big_kernel<{128 // group}, true, 10> (gate+up)",
+                                   "ms": stage["gate_up"], "flops": fl_gu, "tflops": res["gate_up_tflops"],
+                                   "mfma_frac": res["gate_up_mfma_frac"],
+                                   "profile_file": f"experts_prefill_config{cfg}_kernel_stats.md"}
+            else:
+                res["dominant"] = {"kernel": "expert_decode_kernel<4, 10, true> (gate+up)", "ms": stage["gate_up"],
+                                   "bytes": avg["gate_up"], "gbs": res["gate_up_gbs"],
+                                   "traffic_file": "expert_gate_up_decode_config1_traffic.md"}
     for lay in layers:
         lay.close()
     return res

@@ -100,7 +100,8 @@ __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float silu_mul_f(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
+// silu(g) * u with the hardware reciprocal (1 ulp) in place of an IEEE divide
+__device__ __forceinline__ float silu_mul_f(float g, float u) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u; }
 
 // gfx950 direct global->LDS load: each active lane copies 16 bytes from `src`
 // to lds_base + 16 * lane (lds_base must be wave-uniform). No VGPRs are used;

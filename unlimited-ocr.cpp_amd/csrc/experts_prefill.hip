@@ -15,9 +15,67 @@
 //     are dequantised once per workgroup, exactly, into f16 fragments; both land
 //     in MFMA fragment order (1 KiB per 16x32 fragment, lane-contiguous), so every
 //     LDS read is a linear 1 KiB wave read.
+#include <type_traits>
+#include <utility>
+
 #include "launch.hpp"
 
 namespace uocr_hip {
+
+// Global load issued by inline asm (the caller waits with vm_wait and tie):
+// 16, 8 or 4 bytes by the destination's size, at byte offset OFF.
+template <int OFF, typename T>
+__device__ __forceinline__ void gload(T& d, const void* p) {
+    if constexpr (sizeof(T) == 16)
+        asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(d) : "v"(p), "n"(OFF));
+    else if constexpr (sizeof(T) == 8)
+        asm volatile("global_load_dwordx2 %0, %1, off offset:%2" : "=v"(d) : "v"(p), "n"(OFF));
+    else if constexpr (sizeof(T) == 4)
+        asm volatile("global_load_dword %0, %1, off offset:%2" : "=v"(d) : "v"(p), "n"(OFF));
+}
+// 2 bytes, zero-extended
+template <int OFF>
+__device__ __forceinline__ void gload_u16(uint32_t& d, const void* p) {
+    asm volatile("global_load_ushort %0, %1, off offset:%2" : "=v"(d) : "v"(p), "n"(OFF));
+}
+// wait until at most N global loads are outstanding
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N));
+}
+// wait until at most N LDS operations are outstanding
+template <int N>
+__device__ __forceinline__ void lgkm_wait() {
+    asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N));
+}
+// 16-byte LDS read issued by inline asm (waited for with lgkm_wait and tie)
+template <int OFF>
+__device__ __forceinline__ void lds_read16(f16x8& d, uint32_t addr) {
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(d) : "v"(addr), "n"(OFF));
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// 16-byte LDS write issued by inline asm
+template <int OFF>
+__device__ __forceinline__ void lds_write16(uint32_t addr, f16x8 v) {
+    asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(addr), "v"(v), "n"(OFF));
+}
+// the value is used only after this point (orders a use after a vm_wait)
+template <typename T>
+__device__ __forceinline__ void tie(T& v) {
+    asm volatile("" : "+v"(v));
+}
+
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+// f(std::integral_constant<int, i>) for i = 0 .. N-1, in order
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 constexpr int kPreBM = 128;               // slots per m-tile (generic kernel)
 constexpr int kPreBN = 128;               // weight rows per workgroup
@@ -178,6 +236,15 @@ __device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// lgkmcnt for the wait on B fragment f (f = k-step * 8 + 32-row block) of the
+// large-tile k-loop: the ring's reads issued after it, f+1 .. f+3. Staging
+// writes issued meanwhile are not counted: an LDS write can retire before an
+// older read (measured: counting them as if LDS operations retired in issue
+// order lets the wait pass early), while reads return in order among
+// themselves. With the writes uncounted, the count cannot reach the limit
+// before fragment f has landed, whatever the writes do.
+constexpr int lds_reads_after(int f) { return 63 - f < 3 ? 63 - f : 3; }
+
 template <int GPT, bool GU, int KT>
 __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) {
     // B fragments: [buffer][k-step 0..7][n-block 0..7][64 lanes][8 f16]
@@ -196,147 +263,200 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
     const int rows = min(kBigBM, a.counts[e] - m0);
     const int slot0 = a.offsets[e] + m0;
 
-    // A: wave rows wave*64 + j*32 + lane%32 (j = 0, 1); k offset 8 * (lane / 32) in a k-step
-    const f16* arow[2];
-    bool alive[2];
+    // A tile of at most 128 live rows runs in half mode: each wave takes 32
+    // rows (JN = 1) instead of 64 (JN = 2), so it costs half the MFMAs and
+    // activation loads; the tile list puts such tiles last so they fill the
+    // grid's final round.
+    auto body = [&](auto jnc) {
+        constexpr int JN = decltype(jnc)::value;
+        // A: wave rows wave*32*JN + j*32 + lane%32 (j < JN); k offset 8 * (lane / 32) in a k-step
+        const f16* arow[JN];
+        bool alive[JN];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int m = wave * 64 + j * 32 + (lane & 31);
-        alive[j] = m < rows;
-        const int slot = slot0 + (alive[j] ? m : 0);
-        const int row = a.gather ? a.slot_tok[slot] : slot;
-        arow[j] = a.a + (size_t)row * K + 8 * (lane >> 5);
-    }
-    // B dequant units: u = tid + 256 i -> local row block rbl = u / 64, tile lane q = u % 64
-    // (GU: row blocks 0..7 are gate rows of the n-tile's 128 act columns, 8..15 the same up rows)
-    const uint8_t* bsrc[UNITS];
-    const f16* ssrc[UNITS];
-    int bdst[UNITS][4];  // LDS f16 offset of each of the unit's four 8-column runs
-#pragma unroll
-    for (int i = 0; i < UNITS; ++i) {
-        const int u = tid + 256 * i, rbl = u >> 6, q = u & 63;
-        int grow;
-        const uint8_t* wbase;
-        const uint16_t* sbase;
-        if constexpr (GU) {
-            grow = ntile * 8 + (rbl & 7);
-            wbase = (rbl < 8 ? a.w0 : a.w1) + (size_t)e * a.w_stride;
-            sbase = (rbl < 8 ? a.s0 : a.s1) + (size_t)e * a.s_stride;
-        } else {
-            grow = ntile * 16 + rbl;
-            wbase = a.w0 + (size_t)e * a.w_stride;
-            sbase = a.s0 + (size_t)e * a.s_stride;
+        for (int j = 0; j < JN; ++j) {
+            const int m = wave * 32 * JN + j * 32 + (lane & 31);
+            alive[j] = m < rows;
+            const int slot = slot0 + (alive[j] ? m : 0);
+            const int row = a.gather ? a.slot_tok[slot] : slot;
+            arow[j] = a.a + (size_t)row * K + 8 * (lane >> 5);
         }
-        bsrc[i] = wbase + (size_t)grow * KT * kTileBytes + (size_t)q * 16;
-        ssrc[i] = reinterpret_cast<const f16*>(sbase) + (size_t)(grow * kTileRows + (q & 15)) * NG;
-        const int n = rbl * 16 + (q & 15);  // local weight row 0..255
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int kloc = s * 32 + 8 * (q >> 4);  // first column of this run in the k-tile
-            const int ks = kloc >> 4, half = (kloc >> 3) & 1;
-            bdst[i][s] = ((ks * kBigNB + (n >> 5)) * 64 + (n & 31) + 32 * half) * 8;
-        }
-    }
-
-    // raw weights + this k-tile's GPT scales of the unit's row (one load each)
-    u32x4 braw[KT][UNITS];
-    uint32_t bscr[KT][UNITS][(GPT + 1) / 2];
-    auto load_b = [&](int kt) {
+        // B dequant units: u = tid + 256 i -> local row block rbl = u / 64, tile lane q = u % 64
+        // (GU: row blocks 0..7 are gate rows of the n-tile's 128 act columns, 8..15 the same up rows)
+        const uint8_t* bsrc[UNITS];
+        const f16* ssrc[UNITS];
 #pragma unroll
         for (int i = 0; i < UNITS; ++i) {
-            braw[kt][i] = *reinterpret_cast<const u32x4*>(bsrc[i] + (size_t)kt * kTileBytes);
-            const f16* sp = ssrc[i] + kt * GPT;
-            if constexpr (GPT == 4) {
-                const u32x2 v = *reinterpret_cast<const u32x2*>(sp);
-                bscr[kt][i][0] = v[0];
-                bscr[kt][i][1] = v[1];
-            } else if constexpr (GPT == 2) {
-                bscr[kt][i][0] = *reinterpret_cast<const uint32_t*>(sp);
-            } else {
-                bscr[kt][i][0] = *reinterpret_cast<const uint16_t*>(sp);
-            }
-        }
-    };
-    auto scale_of = [&](int kt, int i, int s) -> f16 {
-        const int g = (s * GPT) >> 2;  // group within the k-tile
-        const uint32_t w = bscr[kt][i][g >> 1];
-        const uint16_t h = (uint16_t)((g & 1) ? (w >> 16) : (w & 0xffffu));
-        return __builtin_bit_cast(f16, h);
-    };
-    // dequantise unit i of k-tile kt into its LDS buffer
-    auto stage_unit = [&](int kt, int i) {
-        f16* dst = Bs[kt & 1];
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-            *reinterpret_cast<f16x8*>(dst + bdst[i][s]) = dequant8(braw[kt][i][s], scale2(scale_of(kt, i, s)));
-    };
-    auto stage_b = [&](int kt) {
-#pragma unroll
-        for (int i = 0; i < UNITS; ++i) stage_unit(kt, i);
-    };
-    f16x8 areg[KT][2][8];
-    auto load_a = [&](int kt) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int ks = 0; ks < 8; ++ks)
-                if (alive[j]) areg[kt][j][ks] = *reinterpret_cast<const f16x8*>(arow[j] + kt * kTileK + ks * 16);
-    };
-
-    f32x16 acc[2][kBigNB];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int nb = 0; nb < kBigNB; ++nb) acc[j][nb] = f32x16{};
-
-    load_a(0);
-    load_b(0);
-    if (KT > 1) load_b(1);
-    stage_b(0);
-    __syncthreads();
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-        if (kt + 1 < KT) load_a(kt + 1);
-        if (kt + 2 < KT) load_b(kt + 2);
-        const f16* Bb = Bs[kt & 1];
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-#pragma unroll
-            for (int nb = 0; nb < kBigNB; ++nb) {
-                const f16x8 bf = *reinterpret_cast<const f16x8*>(Bb + ((size_t)(ks * kBigNB + nb) * 64 + lane) * 8);
-#pragma unroll
-                for (int j = 0; j < 2; ++j) acc[j][nb] = mfma32(areg[kt][j][ks], bf, acc[j][nb]);
-            }
-            // next k-tile's weights go to the other buffer (last read before the
-            // previous barrier), one unit after every other k-step so the VALU
-            // work interleaves with the MFMAs in flight
-            if (kt + 1 < KT && (ks & 1)) stage_unit(kt + 1, ks >> 1);
-        }
-        __syncthreads();
-    }
-
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int m = wave * 64 + j * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (m >= rows) continue;
-            const size_t orow = (size_t)(slot0 + m) * a.n_rows;
+            const int u = tid + 256 * i, rbl = u >> 6, q = u & 63;
+            int grow;
+            const uint8_t* wbase;
+            const uint16_t* sbase;
             if constexpr (GU) {
-#pragma unroll
-                for (int nb = 0; nb < kBigNB / 2; ++nb) {
-                    const int col = ntile * (kBigBN / 2) + nb * 32 + (lane & 31);
-                    a.act_out[orow + col] = (f16)silu_mul_f(acc[j][nb][r], acc[j][nb + kBigNB / 2][r]);
-                }
+                grow = ntile * 8 + (rbl & 7);
+                wbase = (rbl < 8 ? a.w0 : a.w1) + (size_t)e * a.w_stride;
+                sbase = (rbl < 8 ? a.s0 : a.s1) + (size_t)e * a.s_stride;
             } else {
+                grow = ntile * 16 + rbl;
+                wbase = a.w0 + (size_t)e * a.w_stride;
+                sbase = a.s0 + (size_t)e * a.s_stride;
+            }
+            bsrc[i] = wbase + (size_t)grow * KT * kTileBytes + (size_t)q * 16;
+            ssrc[i] = reinterpret_cast<const f16*>(sbase) + (size_t)(grow * kTileRows + (q & 15)) * NG;
+        }
+        // LDS destination of unit i's 8-column run s (columns s*32 + 8*(q/16) ..
+        // +7 of local weight row n = (wave + 4i) * 16 + q % 16, in 32x32x16
+        // B-fragment order): byte offset bdst0 + s * 16384 + i * 2048
+        uint32_t bdst0;
+        {
+            const int n = wave * 16 + (lane & 15), q4 = lane >> 4;
+            bdst0 = (uint32_t)((((q4 >> 1) * kBigNB + (n >> 5)) * 64 + (n & 31) + 32 * (q4 & 1)) * 16);
+        }
+
+        // The k-tile pipeline keeps its own load schedule: every global load is
+        // issued by inline asm at a fixed point and every wait is an explicit
+        // vmcnt tied to the registers it guards. Left to itself the compiler sinks
+        // the prefetches to their first use under this register pressure, so each
+        // wait also covers the loads just issued and the pipeline loses its depth.
+        //   * activations: one register pair per k-step (a ring over the k-tile);
+        //     the pair of k-step ks is reloaded with k-tile kt+1's columns right
+        //     after k-tile kt's MFMAs have read it, so every load has most of a
+        //     k-tile to land;
+        //   * weights: B(kt+2) (UNITS weight loads, then UNITS scale loads) at the
+        //     start of k-tile kt, staged into LDS during k-tile kt+1.
+        // Issue order within k-tile kt: B(kt+2), then A(kt+1, ks) after k-step ks.
+        constexpr int AK = JN;         // activation loads per k-step
+        constexpr int NB = 2 * UNITS;  // loads per k-tile of weights
+        u32x4 braw[2][UNITS];
+        typename std::conditional<GPT == 4, u32x2, uint32_t>::type bscr[2][UNITS];
+        f16x8 areg[JN][8];
+        f16x8 bring[6];
+        auto issue_a = [&](auto ktc, auto ksc) {
+            constexpr int kt = decltype(ktc)::value, ks = decltype(ksc)::value;
 #pragma unroll
-                for (int nb = 0; nb < kBigNB; ++nb) {
-                    const int col = ntile * kBigBN + nb * 32 + (lane & 31);
-                    a.y_out[orow + col] = acc[j][nb][r];
+            for (int j = 0; j < JN; ++j) {
+                gload<kt * kTileK * 2 + ks * 32>(areg[j][ks], arow[j]);
+            }
+        };
+        auto issue_b = [&](auto ktc) {
+            constexpr int kt = decltype(ktc)::value;
+#pragma unroll
+            for (int i = 0; i < UNITS; ++i) {
+                gload<0>(braw[kt & 1][i], bsrc[i] + (size_t)kt * kTileBytes);
+            }
+#pragma unroll
+            for (int i = 0; i < UNITS; ++i) {
+                if constexpr (GPT == 1)
+                    gload_u16<kt * 2>(bscr[kt & 1][i], ssrc[i]);
+                else
+                    gload<kt * GPT * 2>(bscr[kt & 1][i], ssrc[i]);
+            }
+        };
+        // wait until at most N loads are outstanding, then let the guarded values be used
+        auto wait_a = [&](auto nc, int ks) {
+            vm_wait<decltype(nc)::value>();
+#pragma unroll
+            for (int j = 0; j < JN; ++j) tie(areg[j][ks]);
+        };
+        auto wait_b = [&](auto nc, int buf) {
+            vm_wait<decltype(nc)::value>();
+#pragma unroll
+            for (int i = 0; i < UNITS; ++i) {
+                tie(braw[buf][i]);
+                tie(bscr[buf][i]);
+            }
+        };
+        auto scale_of = [&](int buf, int i, int s) -> f16 {
+            const int g = (s * GPT) >> 2;  // group within the k-tile
+            uint32_t w;
+            if constexpr (GPT == 4) w = bscr[buf][i][g >> 1];
+            else w = bscr[buf][i];
+            const uint16_t h = (uint16_t)((g & 1) ? (w >> 16) : (w & 0xffffu));
+            return __builtin_bit_cast(f16, h);
+        };
+        // dequantise unit i of k-tile kt into its LDS buffer (4 LDS writes)
+        auto stage_unit = [&](int kt, auto ic) {
+            constexpr int i = decltype(ic)::value;
+            const uint32_t dst = lds_addr(Bs[kt & 1]) + bdst0;
+            static_for<4>([&](auto sc) {
+                constexpr int s = decltype(sc)::value;
+                lds_write16<s * 16384 + i * 2048>(dst, dequant8(braw[kt & 1][i][s], scale2(scale_of(kt & 1, i, s))));
+            });
+        };
+
+        f32x16 acc[JN][kBigNB];
+#pragma unroll
+        for (int j = 0; j < JN; ++j)
+#pragma unroll
+            for (int nb = 0; nb < kBigNB; ++nb) acc[j][nb] = f32x16{};
+
+        // prologue: B(0), B(1), A(0); stage B(0)
+        issue_b(std::integral_constant<int, 0>{});
+        if constexpr (KT > 1) issue_b(std::integral_constant<int, 1>{});
+        static_for<8>([&](auto ksc) { issue_a(std::integral_constant<int, 0>{}, ksc); });
+        wait_b(std::integral_constant<int, (KT > 1 ? NB : 0) + 8 * AK>{}, 0);
+        static_for<UNITS>([&](auto ic) { stage_unit(0, ic); });
+        lgkm_wait<0>();
+        __syncthreads();
+        static_for<KT>([&](auto ktc) {
+            constexpr int kt = decltype(ktc)::value;
+            constexpr bool more = kt + 1 < KT;
+            constexpr int nB2 = kt + 2 < KT ? NB : 0;
+            if constexpr (kt + 2 < KT) issue_b(std::integral_constant<int, kt + 2>{});
+            // B fragments stream from LDS through a 6-deep register ring, read
+            // 4 fragments (8 MFMAs) ahead of their use: fragment f = ks * 8 + nb
+            const uint32_t bb = lds_addr(Bs[kt & 1]) + lane * 16;
+            static_for<4>([&](auto fc) { lds_read16<decltype(fc)::value * 1024>(bring[decltype(fc)::value], bb); });
+            static_for<8 * kBigNB>([&](auto fc) {
+                constexpr int f = decltype(fc)::value, ks = f / kBigNB, nb = f % kBigNB;
+                if constexpr (nb == 0)  // A(kt, ks) was issued before A(kt, ks+1 .. 7), B(kt+2) and A(kt+1, 0 .. ks-1)
+                    wait_a(std::integral_constant<int, AK * (7 - ks) + nB2 + (more ? AK * ks : 0)>{}, ks);
+                lgkm_wait<lds_reads_after(f)>();
+                tie(bring[f % 6]);
+#pragma unroll
+                for (int j = 0; j < JN; ++j) acc[j][nb] = mfma32(areg[j][ks], bring[f % 6], acc[j][nb]);
+                if constexpr (f + 4 < 8 * kBigNB) lds_read16<(f + 4) * 1024>(bring[(f + 4) % 6], bb);
+                if constexpr (nb == kBigNB - 1) {
+                    if constexpr (more) issue_a(std::integral_constant<int, kt + 1>{}, std::integral_constant<int, ks>{});
+                    // next k-tile's weights go to the other buffer (last read before the
+                    // previous barrier), one unit after every other k-step so the VALU
+                    // work interleaves with the MFMAs in flight
+                    if constexpr (more && (ks & 1)) {
+                        // B(kt+1) was issued before A(kt), B(kt+2) and A(kt+1, 0 .. 1)
+                        if constexpr (ks == 1) wait_b(std::integral_constant<int, 8 * AK + nB2 + 2 * AK>{}, (kt + 1) & 1);
+                        stage_unit(kt + 1, std::integral_constant<int, (ks >> 1)>{});
+                    }
+                }
+            });
+            lgkm_wait<0>();  // this k-tile's staging writes (asm, not tracked by the compiler)
+            __syncthreads();
+        });
+
+#pragma unroll
+        for (int j = 0; j < JN; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = wave * 32 * JN + j * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m >= rows) continue;
+                const size_t orow = (size_t)(slot0 + m) * a.n_rows;
+                if constexpr (GU) {
+#pragma unroll
+                    for (int nb = 0; nb < kBigNB / 2; ++nb) {
+                        const int col = ntile * (kBigBN / 2) + nb * 32 + (lane & 31);
+                        a.act_out[orow + col] = (f16)silu_mul_f(acc[j][nb][r], acc[j][nb + kBigNB / 2][r]);
+                    }
+                } else {
+#pragma unroll
+                    for (int nb = 0; nb < kBigNB; ++nb) {
+                        const int col = ntile * kBigBN + nb * 32 + (lane & 31);
+                        a.y_out[orow + col] = acc[j][nb][r];
+                    }
                 }
             }
         }
-    }
+    };
+    if (rows <= kBigBM / 2)
+        body(std::integral_constant<int, 1>{});
+    else
+        body(std::integral_constant<int, 2>{});
 }
 
 template <int GPT, bool GU>

@@ -76,6 +76,8 @@ struct GroupLds {
     int hist[kMaxExperts];
     int offs[kMaxExperts + 1];
     int tile0[kMaxExperts + 1];
+    int short0[kMaxExperts + 1];
+    int nshort[kMaxExperts];
     int run[kMaxExperts];
     int wcnt[kGroupWaves][kMaxExperts];   // per-wave counts of the round
     int wbase[kGroupWaves][kMaxExperts];  // exclusive per-wave prefix of the round
@@ -96,6 +98,35 @@ __device__ __forceinline__ void wave0_exclusive_scan(const int* v, int* out, int
     if (2 * lane < n) out[2 * lane] = ex;
     if (2 * lane + 1 < n) out[2 * lane + 1] = ex + a;
     if (lane == 63) out[n] = inc;
+}
+
+// Tile list order: every expert's tiles of more than bm/2 rows first, then
+// each expert's short last tile (1 .. bm/2 rows), so the short tiles (which
+// the large-tile prefill kernel runs in half mode) fill the grid's last round.
+// Long / short tile counts of a group of c rows:
+__device__ __forceinline__ int short_tiles(int c, int bm) {
+    const int rem = c % bm;
+    return (rem != 0 && rem <= bm / 2) ? 1 : 0;
+}
+__device__ __forceinline__ int long_tiles(int c, int bm) { return (c + bm - 1) / bm - short_tiles(c, bm); }
+// Write the list from the exclusive scans of the long (tile0) and short
+// (short0) counts over Ev groups of hist[] rows. Called by all threads.
+__device__ __forceinline__ void write_tile_list(const GroupArgs& g, const int* hist, const int* tile0,
+                                                const int* short0, int Ev) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int nlong = tile0[Ev];
+    if (tid == 0) *g.n_tiles = nlong + short0[Ev];
+    for (int e = wave; e < Ev; e += kGroupWaves) {
+        const int nt = tile0[e + 1] - tile0[e];
+        for (int m = lane; m < nt; m += 64) {
+            g.tile_e[tile0[e] + m] = e;
+            g.tile_m0[tile0[e] + m] = m * g.bm;
+        }
+        if (lane == 0 && short0[e + 1] > short0[e]) {
+            g.tile_e[nlong + short0[e]] = e;
+            g.tile_m0[nlong + short0[e]] = nt * g.bm;
+        }
+    }
 }
 
 // `ids` / `wts` may live in global memory or LDS. Must be called by all 1024 threads.
@@ -121,10 +152,14 @@ __device__ void group_body(const int* ids, const float* wts, const GroupArgs& g,
     if (wave == 0) wave0_exclusive_scan(s.hist, s.offs, Ev);
     if (wave == 1 && g.tile_e) {
         // tiles per expert into run[] (reset below), then scan into tile0[]
-        for (int e = lane; e < Ev; e += 64) s.run[e] = (s.hist[e] + g.bm - 1) / g.bm;
+        for (int e = lane; e < Ev; e += 64) {
+            s.run[e] = long_tiles(s.hist[e], g.bm);
+            s.nshort[e] = short_tiles(s.hist[e], g.bm);
+        }
     }
     __syncthreads();
     if (g.tile_e && wave == 1) wave0_exclusive_scan(s.run, s.tile0, Ev);
+    if (g.tile_e && wave == 2) wave0_exclusive_scan(s.nshort, s.short0, Ev);
     __syncthreads();
     if (g.counts) {
         for (int e = tid; e < Ev; e += kGroupThreads) {
@@ -133,16 +168,7 @@ __device__ void group_body(const int* ids, const float* wts, const GroupArgs& g,
         }
         if (tid == 0) g.offsets[Ev] = s.offs[Ev];
     }
-    if (g.tile_e) {
-        if (tid == 0) *g.n_tiles = s.tile0[Ev];
-        for (int e = wave; e < Ev; e += kGroupWaves) {
-            const int nt = s.tile0[e + 1] - s.tile0[e];
-            for (int m = lane; m < nt; m += 64) {
-                g.tile_e[s.tile0[e] + m] = e;
-                g.tile_m0[s.tile0[e] + m] = m * g.bm;
-            }
-        }
-    }
+    if (g.tile_e) write_tile_list(g, s.hist, s.tile0, s.short0, Ev);
     for (int e = tid; e < kMaxExperts; e += kGroupThreads) s.run[e] = 0;
     __syncthreads();
     // stable placement of the routed entries, kGroupThreads entries per round
@@ -256,6 +282,7 @@ __global__ __launch_bounds__(kGroupThreads) void group_rank_kernel(GroupArgs g) 
 __global__ __launch_bounds__(kGroupThreads) void group_scan_kernel(GroupArgs g, int n_chunks) {
     extern __shared__ int cc[];  // [n_chunks][E] counts, then bases
     __shared__ int hist[kMaxExperts], offs[kMaxExperts + 1], ntl[kMaxExperts], tile0[kMaxExperts + 1];
+    __shared__ int nsh[kMaxExperts], short0[kMaxExperts + 1];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int E = g.n_experts, Ev = E + g.n_virtual;
     for (int k = tid; k < n_chunks * E; k += kGroupThreads) cc[k] = g.chunk_count[k];
@@ -271,11 +298,13 @@ __global__ __launch_bounds__(kGroupThreads) void group_scan_kernel(GroupArgs g, 
         else
             acc = g.seq;
         hist[e] = acc;
-        ntl[e] = (acc + g.bm - 1) / g.bm;
+        ntl[e] = long_tiles(acc, g.bm);
+        nsh[e] = short_tiles(acc, g.bm);
     }
     __syncthreads();
     if (wave == 0) wave0_exclusive_scan(hist, offs, Ev);
     if (wave == 1) wave0_exclusive_scan(ntl, tile0, Ev);
+    if (wave == 2) wave0_exclusive_scan(nsh, short0, Ev);
     __syncthreads();
     for (int k = tid; k < n_chunks * E; k += kGroupThreads) g.chunk_base[k] = cc[k] + (g.slot_tok ? offs[k % E] : 0);
     for (int e = tid; e < Ev; e += kGroupThreads) {
@@ -286,16 +315,7 @@ __global__ __launch_bounds__(kGroupThreads) void group_scan_kernel(GroupArgs g, 
         if (g.assign_count && e < E) g.assign_count[e] = min(hist[e], g.cap);
     }
     if (tid == 0 && g.counts) g.offsets[Ev] = offs[Ev];
-    if (g.tile_e) {
-        if (tid == 0) *g.n_tiles = tile0[Ev];
-        for (int e = wave; e < Ev; e += kGroupWaves) {
-            const int nt = tile0[e + 1] - tile0[e];
-            for (int m = lane; m < nt; m += 64) {
-                g.tile_e[tile0[e] + m] = e;
-                g.tile_m0[tile0[e] + m] = m * g.bm;
-            }
-        }
-    }
+    if (g.tile_e) write_tile_list(g, hist, tile0, short0, Ev);
     // virtual (shared-expert) groups: every token, weight 1
     if (g.slot_tok)
         for (int v = 0; v < g.n_virtual; ++v)
