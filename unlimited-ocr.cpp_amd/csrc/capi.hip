@@ -166,7 +166,7 @@ int check_qm(const uocr_hip_qmatrix* q, int rows, int cols, int group, const cha
 }
 
 struct WsPlan {
-    size_t x16, ids, wts, counts, offsets, ntiles, slot_tok, slot_w, pos, tile_e, tile_m0, act, y, total;
+    size_t x16, ids, wts, counts, offsets, ntiles, slot_tok, slot_w, pos, tile_e, tile_m0, tile_info, act, y, total;
     size_t lrank, chunk_count, chunk_base;
     int slots, max_tiles, bm;
 };
@@ -231,6 +231,7 @@ WsPlan plan(const uocr_hip_moe_layer* L, int seq) {
     p.pos = take((size_t)seq * L->top_k * 4);
     p.tile_e = take((size_t)p.max_tiles * 4);
     p.tile_m0 = take((size_t)p.max_tiles * 4);
+    p.tile_info = take((size_t)p.max_tiles * 16);
     // act: one row per slot, or per (group, token) for the fused decode kernel
     p.act = take((size_t)std::max(p.slots, Ev * seq) * L->inter * 2);
     // y: one row per entry, or per (group, token) for the fused decode kernel
@@ -553,6 +554,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     g.pos = (int*)(ws + p.pos);
     g.tile_e = (int*)(ws + p.tile_e);
     g.tile_m0 = (int*)(ws + p.tile_m0);
+    g.tile_info = (int*)(ws + p.tile_info);
     g.n_tiles = (int*)(ws + p.ntiles);
     g.lrank = (int*)(ws + p.lrank);
     g.chunk_count = (int*)(ws + p.chunk_count);
@@ -580,6 +582,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     gu.offsets = g.offsets;
     gu.tile_e = g.tile_e;
     gu.tile_m0 = g.tile_m0;
+    gu.tile_info = g.tile_info;
     gu.n_tiles = g.n_tiles;
     gu.act_out = (f16*)(ws + p.act);
     HIP_TRY(launch_experts_prefill(gu, true, p.max_tiles, st),

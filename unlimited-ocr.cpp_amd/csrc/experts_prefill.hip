@@ -231,6 +231,7 @@ __global__ __launch_bounds__(256) void experts_prefill_kernel(ExpertArgs a) {
 // ---------------------------------------------------------------------------
 constexpr int kBigBN = 256;  // weight rows per workgroup
 constexpr int kBigNB = kBigBN / 32;
+constexpr int kEpStride = 288;  // epilogue staging: bytes per row (256 + 32 of padding)
 
 __device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -243,8 +244,23 @@ __device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
 // order lets the wait pass early), while reads return in order among
 // themselves. With the writes uncounted, the count cannot reach the limit
 // before fragment f has landed, whatever the writes do.
-constexpr int lds_reads_after(int f) { return 63 - f < 3 ? 63 - f : 3; }
+constexpr int kRingAhead = 4;               // B fragments read ahead of their use
+constexpr int kRing = kRingAhead + 2;       // register ring size
+constexpr int lds_reads_after(int f) { return 63 - f < kRingAhead - 1 ? 63 - f : kRingAhead - 1; }
 
+// Trace build (-DUOCR_PTRACE, never the shipped library): thread 0 of each
+// workgroup records s_memtime at its start (0), after the prologue (1), after
+// each k-tile (2 + kt) and at its end (13), plus its tile and live rows (14)
+// and s_memrealtime at start (15) and end (12), per pass (gate/up, down);
+// uocr_hip_debug_ptrace copies the table out after a layer call.
+#ifdef UOCR_PTRACE
+__device__ unsigned long long g_ptrace[2][8192][16];
+#define PT(i) do { if (threadIdx.x == 0 && blockIdx.x < 8192) g_ptrace[GU ? 0 : 1][blockIdx.x][i] = __builtin_amdgcn_s_memtime(); } while (0)
+#define PTV(i, v) do { if (threadIdx.x == 0 && blockIdx.x < 8192) g_ptrace[GU ? 0 : 1][blockIdx.x][i] = (v); } while (0)
+#else
+#define PT(i) do {} while (0)
+#define PTV(i, v) do {} while (0)
+#endif
 template <int GPT, bool GU, int KT>
 __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) {
     // B fragments: [buffer][k-step 0..7][n-block 0..7][64 lanes][8 f16]
@@ -256,12 +272,14 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
     const int b = blockIdx.x, xcd = b & 7, local = b >> 3;
     const int tile = (local / n_ntiles) * 8 + xcd, ntile = local % n_ntiles;
     const int n_tiles = *a.n_tiles;
-    const int tile_c = min(tile, n_tiles > 0 ? n_tiles - 1 : 0);
-    const int e = a.tile_e[tile_c], m0 = a.tile_m0[tile_c];
     if (tile >= n_tiles) return;
+    PT(0);
+    PTV(15, __builtin_amdgcn_s_memrealtime());
+    // one 16-byte record per tile: expert, first row, live rows, first slot
+    const int4 ti = *reinterpret_cast<const int4*>(a.tile_info + 4 * tile);
+    const int e = ti.x, rows = ti.z, slot0 = ti.w;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int rows = min(kBigBM, a.counts[e] - m0);
-    const int slot0 = a.offsets[e] + m0;
+    PTV(14, (unsigned long long)tile * 65536 + rows);
 
     // A tile of at most 128 live rows runs in half mode: each wave takes 32
     // rows (JN = 1) instead of 64 (JN = 2), so it costs half the MFMAs and
@@ -328,7 +346,7 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
         u32x4 braw[2][UNITS];
         typename std::conditional<GPT == 4, u32x2, uint32_t>::type bscr[2][UNITS];
         f16x8 areg[JN][8];
-        f16x8 bring[6];
+        f16x8 bring[kRing];
         auto issue_a = [&](auto ktc, auto ksc) {
             constexpr int kt = decltype(ktc)::value, ks = decltype(ksc)::value;
 #pragma unroll
@@ -396,6 +414,7 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
         static_for<UNITS>([&](auto ic) { stage_unit(0, ic); });
         lgkm_wait<0>();
         __syncthreads();
+        PT(1);
         static_for<KT>([&](auto ktc) {
             constexpr int kt = decltype(ktc)::value;
             constexpr bool more = kt + 1 < KT;
@@ -404,16 +423,17 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
             // B fragments stream from LDS through a 6-deep register ring, read
             // 4 fragments (8 MFMAs) ahead of their use: fragment f = ks * 8 + nb
             const uint32_t bb = lds_addr(Bs[kt & 1]) + lane * 16;
-            static_for<4>([&](auto fc) { lds_read16<decltype(fc)::value * 1024>(bring[decltype(fc)::value], bb); });
+            static_for<kRingAhead>([&](auto fc) { lds_read16<decltype(fc)::value * 1024>(bring[decltype(fc)::value], bb); });
             static_for<8 * kBigNB>([&](auto fc) {
                 constexpr int f = decltype(fc)::value, ks = f / kBigNB, nb = f % kBigNB;
                 if constexpr (nb == 0)  // A(kt, ks) was issued before A(kt, ks+1 .. 7), B(kt+2) and A(kt+1, 0 .. ks-1)
                     wait_a(std::integral_constant<int, AK * (7 - ks) + nB2 + (more ? AK * ks : 0)>{}, ks);
                 lgkm_wait<lds_reads_after(f)>();
-                tie(bring[f % 6]);
+                tie(bring[f % kRing]);
 #pragma unroll
-                for (int j = 0; j < JN; ++j) acc[j][nb] = mfma32(areg[j][ks], bring[f % 6], acc[j][nb]);
-                if constexpr (f + 4 < 8 * kBigNB) lds_read16<(f + 4) * 1024>(bring[(f + 4) % 6], bb);
+                for (int j = 0; j < JN; ++j) acc[j][nb] = mfma32(areg[j][ks], bring[f % kRing], acc[j][nb]);
+                if constexpr (f + kRingAhead < 8 * kBigNB)
+                    lds_read16<(f + kRingAhead) * 1024>(bring[(f + kRingAhead) % kRing], bb);
                 if constexpr (nb == kBigNB - 1) {
                     if constexpr (more) issue_a(std::integral_constant<int, kt + 1>{}, std::integral_constant<int, ks>{});
                     // next k-tile's weights go to the other buffer (last read before the
@@ -428,27 +448,53 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
             });
             lgkm_wait<0>();  // this k-tile's staging writes (asm, not tracked by the compiler)
             __syncthreads();
+            PT(2 + kt);
         });
 
+        // Epilogue: each wave stages its 32*JN output rows in LDS, row-major
+        // with a 288-byte row stride (rows 4 apart land 32 banks apart), then
+        // every lane stores 16 contiguous bytes: one store instruction covers
+        // 4 rows x 256 bytes. The k-loop's last barrier has retired every read
+        // of Bs, and each wave only touches its own region.
+        uint8_t* ep = reinterpret_cast<uint8_t*>(&Bs[0][0]) + wave * (64 * kEpStride);
+        const int er = lane >> 4, ec = (lane & 15) * 16;  // store lane: row within 4, byte column
+        auto stage_rows = [&](auto write_vals) {
 #pragma unroll
-        for (int j = 0; j < JN; ++j) {
+            for (int j = 0; j < JN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = wave * 32 * JN + j * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m >= rows) continue;
-                const size_t orow = (size_t)(slot0 + m) * a.n_rows;
-                if constexpr (GU) {
+                for (int r = 0; r < 16; ++r)
+                    write_vals(j, r, ep + (j * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * kEpStride);
+        };
+        if constexpr (GU) {
+            stage_rows([&](int j, int r, uint8_t* row) {
 #pragma unroll
-                    for (int nb = 0; nb < kBigNB / 2; ++nb) {
-                        const int col = ntile * (kBigBN / 2) + nb * 32 + (lane & 31);
-                        a.act_out[orow + col] = (f16)silu_mul_f(acc[j][nb][r], acc[j][nb + kBigNB / 2][r]);
-                    }
-                } else {
+                for (int nb = 0; nb < kBigNB / 2; ++nb)
+                    reinterpret_cast<f16*>(row)[nb * 32 + (lane & 31)] =
+                        (f16)silu_mul_f(acc[j][nb][r], acc[j][nb + kBigNB / 2][r]);
+            });
 #pragma unroll
-                    for (int nb = 0; nb < kBigNB; ++nb) {
-                        const int col = ntile * kBigBN + nb * 32 + (lane & 31);
-                        a.y_out[orow + col] = acc[j][nb][r];
-                    }
+            for (int i = 0; i < 8 * JN; ++i) {
+                const int m = wave * 32 * JN + i * 4 + er;
+                const u32x4 v = *reinterpret_cast<const u32x4*>(ep + (i * 4 + er) * kEpStride + ec);
+                if (m < rows)
+                    *reinterpret_cast<u32x4*>(a.act_out + (size_t)(slot0 + m) * a.n_rows + ntile * (kBigBN / 2) + ec / 2) = v;
+            }
+        } else {
+            // 64 output columns per pass
+#pragma unroll
+            for (int pass = 0; pass < kBigNB / 2; ++pass) {
+                stage_rows([&](int j, int r, uint8_t* row) {
+#pragma unroll
+                    for (int q = 0; q < 2; ++q)
+                        reinterpret_cast<float*>(row)[q * 32 + (lane & 31)] = acc[j][2 * pass + q][r];
+                });
+#pragma unroll
+                for (int i = 0; i < 8 * JN; ++i) {
+                    const int m = wave * 32 * JN + i * 4 + er;
+                    const f32x4 v = *reinterpret_cast<const f32x4*>(ep + (i * 4 + er) * kEpStride + ec);
+                    if (m < rows)
+                        *reinterpret_cast<f32x4*>(a.y_out + (size_t)(slot0 + m) * a.n_rows + ntile * kBigBN + pass * 64 +
+                                                  ec / 4) = v;
                 }
             }
         }
@@ -457,7 +503,16 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
         body(std::integral_constant<int, 1>{});
     else
         body(std::integral_constant<int, 2>{});
+    PT(13);
+    PTV(12, __builtin_amdgcn_s_memrealtime());
 }
+#ifdef UOCR_PTRACE
+}  // namespace uocr_hip
+extern "C" int uocr_hip_debug_ptrace(void* dst, size_t bytes) {
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(uocr_hip::g_ptrace), bytes, 0, hipMemcpyDeviceToHost);
+}
+namespace uocr_hip {
+#endif
 
 template <int GPT, bool GU>
 static bool launch_big(const ExpertArgs& a, int max_tiles, hipStream_t st) {

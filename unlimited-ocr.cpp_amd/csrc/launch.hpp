@@ -57,6 +57,7 @@ struct GroupArgs {
     int* pos;        // [seq * top_k] slot of entry (t, j)
     int* tile_e;     // [max tiles]
     int* tile_m0;    // [max tiles]
+    int* tile_info;  // [max tiles][4]: e, m0, rows, first slot (16-byte aligned)
     int* n_tiles;    // [1]
     // reference [n_experts, cap] assignment tables (moe_router_topk mirror)
     int* assign_token;
@@ -87,6 +88,7 @@ struct ExpertArgs {
     const int* offsets;
     const int* tile_e;
     const int* tile_m0;
+    const int* tile_info;    // [max tiles][4]: e, m0, rows, first slot
     const int* n_tiles;
     f16* act_out;            // gate/up: [slots, n_rows] f16
     float* y_out;            // down: [slots, n_rows] f32

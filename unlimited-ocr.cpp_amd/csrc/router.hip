@@ -111,21 +111,22 @@ __device__ __forceinline__ int short_tiles(int c, int bm) {
 __device__ __forceinline__ int long_tiles(int c, int bm) { return (c + bm - 1) / bm - short_tiles(c, bm); }
 // Write the list from the exclusive scans of the long (tile0) and short
 // (short0) counts over Ev groups of hist[] rows. Called by all threads.
-__device__ __forceinline__ void write_tile_list(const GroupArgs& g, const int* hist, const int* tile0,
-                                                const int* short0, int Ev) {
+__device__ __forceinline__ void write_tile_list(const GroupArgs& g, const int* hist, const int* offs,
+                                                const int* tile0, const int* short0, int Ev) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int nlong = tile0[Ev];
     if (tid == 0) *g.n_tiles = nlong + short0[Ev];
     for (int e = wave; e < Ev; e += kGroupWaves) {
         const int nt = tile0[e + 1] - tile0[e];
-        for (int m = lane; m < nt; m += 64) {
-            g.tile_e[tile0[e] + m] = e;
-            g.tile_m0[tile0[e] + m] = m * g.bm;
-        }
-        if (lane == 0 && short0[e + 1] > short0[e]) {
-            g.tile_e[nlong + short0[e]] = e;
-            g.tile_m0[nlong + short0[e]] = nt * g.bm;
-        }
+        auto put = [&](int idx, int m0) {
+            g.tile_e[idx] = e;
+            g.tile_m0[idx] = m0;
+            if (g.tile_info)
+                *reinterpret_cast<int4*>(g.tile_info + 4 * idx) =
+                    make_int4(e, m0, min(g.bm, hist[e] - m0), offs[e] + m0);
+        };
+        for (int m = lane; m < nt; m += 64) put(tile0[e] + m, m * g.bm);
+        if (lane == 0 && short0[e + 1] > short0[e]) put(nlong + short0[e], nt * g.bm);
     }
 }
 
@@ -168,7 +169,7 @@ __device__ void group_body(const int* ids, const float* wts, const GroupArgs& g,
         }
         if (tid == 0) g.offsets[Ev] = s.offs[Ev];
     }
-    if (g.tile_e) write_tile_list(g, s.hist, s.tile0, s.short0, Ev);
+    if (g.tile_e) write_tile_list(g, s.hist, s.offs, s.tile0, s.short0, Ev);
     for (int e = tid; e < kMaxExperts; e += kGroupThreads) s.run[e] = 0;
     __syncthreads();
     // stable placement of the routed entries, kGroupThreads entries per round
@@ -315,7 +316,7 @@ __global__ __launch_bounds__(kGroupThreads) void group_scan_kernel(GroupArgs g, 
         if (g.assign_count && e < E) g.assign_count[e] = min(hist[e], g.cap);
     }
     if (tid == 0 && g.counts) g.offsets[Ev] = offs[Ev];
-    if (g.tile_e) write_tile_list(g, hist, tile0, short0, Ev);
+    if (g.tile_e) write_tile_list(g, hist, offs, tile0, short0, Ev);
     // virtual (shared-expert) groups: every token, weight 1
     if (g.slot_tok)
         for (int v = 0; v < g.n_virtual; ++v)
