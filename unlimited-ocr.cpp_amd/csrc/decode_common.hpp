@@ -390,26 +390,38 @@ __device__ __forceinline__ void router_token(const DecodeArgs& a, int t, unsigne
                            "=&v"(cur[6]), "=&v"(cur[7])
                          : "v"(pb)
                          : "memory");
-            float ss = 0.0f;
-            for (int c = 0; c < H; c += 32) {
-                pb += 128u;  // the next step (past the end: the pad, never added)
+            // Two 32-column steps per iteration with the two buffers swapping
+            // roles (no register copies between the adds; H / 32 is even).
+            auto read8 = [&](f32x4 (&d)[8], uint32_t p) {
                 asm volatile("ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:16\n\t"
                              "ds_read_b128 %2, %8 offset:32\n\tds_read_b128 %3, %8 offset:48\n\t"
                              "ds_read_b128 %4, %8 offset:64\n\tds_read_b128 %5, %8 offset:80\n\t"
                              "ds_read_b128 %6, %8 offset:96\n\tds_read_b128 %7, %8 offset:112"
-                             : "=&v"(nxt[0]), "=&v"(nxt[1]), "=&v"(nxt[2]), "=&v"(nxt[3]), "=&v"(nxt[4]), "=&v"(nxt[5]),
-                               "=&v"(nxt[6]), "=&v"(nxt[7])
-                             : "v"(pb)
+                             : "=&v"(d[0]), "=&v"(d[1]), "=&v"(d[2]), "=&v"(d[3]), "=&v"(d[4]), "=&v"(d[5]),
+                               "=&v"(d[6]), "=&v"(d[7])
+                             : "v"(p)
                              : "memory");
+            };
+            auto wait8 = [&](f32x4 (&d)[8], float& acc) {
+                asm volatile("s_waitcnt lgkmcnt(0)"
+                             : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]), "+v"(d[4]), "+v"(d[5]), "+v"(d[6]),
+                               "+v"(d[7]), "+v"(acc));
+            };
+            float ss = 0.0f;
+            for (int c = 0; c < H; c += 64) {
+                read8(nxt, pb + 128u);  // the next step
 #pragma unroll
                 for (int k = 0; k < 8; ++k)
 #pragma unroll
                     for (int q = 0; q < 4; ++q) ss = __fadd_rn(ss, cur[k][q]);
-                asm volatile("s_waitcnt lgkmcnt(0)"
-                             : "+v"(nxt[0]), "+v"(nxt[1]), "+v"(nxt[2]), "+v"(nxt[3]), "+v"(nxt[4]), "+v"(nxt[5]),
-                               "+v"(nxt[6]), "+v"(nxt[7]), "+v"(ss));
+                wait8(nxt, ss);
+                read8(cur, pb + 256u);  // the step after (past the end: the pad, never added)
 #pragma unroll
-                for (int k = 0; k < 8; ++k) cur[k] = nxt[k];
+                for (int k = 0; k < 8; ++k)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) ss = __fadd_rn(ss, nxt[k][q]);
+                wait8(cur, ss);
+                pb += 256u;
             }
             sc[0] = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)H), a.rms_eps)));
         }
