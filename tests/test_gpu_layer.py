@@ -82,21 +82,23 @@ def test_config3_prefill_t4096_zipf(dev):
     assert counts.max() > 1000, counts  # the skew the config asks for
 
 
-def test_prefill_full_and_half_mode_tiles(dev):
+@pytest.mark.parametrize("group", [32, 64, 128])
+def test_prefill_full_and_half_mode_tiles(dev, group):
     """600 Zipf-routed tokens, every row checked: groups of several 256-row
     tiles, last tiles of 129..255 rows (full mode) and of 1..128 rows (half
     mode, listed after all full-mode tiles), including the shared groups'
-    88-row last tiles."""
+    88-row last tiles; each quantisation group size has its own scale loads
+    in the large-tile kernel."""
     from uocr_hip import synth
     import oracle as O
-    L = synth.random_layer(4242, router_bias=synth.zipf_bias())
+    L = synth.random_layer(4242, group=group, router_bias=synth.zipf_bias())
     x = synth.bf16_normal(np.random.default_rng(5), (600, L.hidden), 1.0)
     x[:, 0] = 1.0
     ids, _ = O.moe_gate(x, L.router_bf16, L.top_k)
     rem = np.bincount(ids.ravel(), minlength=L.n_experts) % 256
     counts = np.bincount(ids.ravel(), minlength=L.n_experts)
     assert (counts > 256).sum() >= 4 and (rem > 128).sum() >= 2 and ((rem > 0) & (rem <= 128)).sum() >= 8
-    check_parity(L, x, dev, label="prefill-600-zipf")
+    check_parity(L, x, dev, label=f"prefill-600-zipf-g{group}")
 
 
 def test_config4_rmsnorm_residual_t64(dev):

@@ -390,14 +390,11 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
             const uint16_t h = (uint16_t)((g & 1) ? (w >> 16) : (w & 0xffffu));
             return __builtin_bit_cast(f16, h);
         };
-        // dequantise unit i of k-tile kt into its LDS buffer (4 LDS writes)
-        auto stage_unit = [&](int kt, auto ic) {
-            constexpr int i = decltype(ic)::value;
+        // dequantise run s (8 columns) of unit i of k-tile kt into its LDS buffer
+        auto stage_run = [&](int kt, auto ic, auto sc) {
+            constexpr int i = decltype(ic)::value, s = decltype(sc)::value;
             const uint32_t dst = lds_addr(Bs[kt & 1]) + bdst0;
-            static_for<4>([&](auto sc) {
-                constexpr int s = decltype(sc)::value;
-                lds_write16<s * 16384 + i * 2048>(dst, dequant8(braw[kt & 1][i][s], scale2(scale_of(kt & 1, i, s))));
-            });
+            lds_write16<s * 16384 + i * 2048>(dst, dequant8(braw[kt & 1][i][s], scale2(scale_of(kt & 1, i, s))));
         };
 
         f32x16 acc[JN][kBigNB];
@@ -411,7 +408,7 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
         if constexpr (KT > 1) issue_b(std::integral_constant<int, 1>{});
         static_for<8>([&](auto ksc) { issue_a(std::integral_constant<int, 0>{}, ksc); });
         wait_b(std::integral_constant<int, (KT > 1 ? NB : 0) + 8 * AK>{}, 0);
-        static_for<UNITS>([&](auto ic) { stage_unit(0, ic); });
+        static_for<UNITS>([&](auto ic) { static_for<4>([&](auto sc) { stage_run(0, ic, sc); }); });
         lgkm_wait<0>();
         __syncthreads();
         PT(1);
@@ -434,16 +431,17 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
                 for (int j = 0; j < JN; ++j) acc[j][nb] = mfma32(areg[j][ks], bring[f % kRing], acc[j][nb]);
                 if constexpr (f + kRingAhead < 8 * kBigNB)
                     lds_read16<(f + kRingAhead) * 1024>(bring[(f + kRingAhead) % kRing], bb);
-                if constexpr (nb == kBigNB - 1) {
-                    if constexpr (more) issue_a(std::integral_constant<int, kt + 1>{}, std::integral_constant<int, ks>{});
-                    // next k-tile's weights go to the other buffer (last read before the
-                    // previous barrier), one unit after every other k-step so the VALU
-                    // work interleaves with the MFMAs in flight
-                    if constexpr (more && (ks & 1)) {
-                        // B(kt+1) was issued before A(kt), B(kt+2) and A(kt+1, 0 .. 1)
-                        if constexpr (ks == 1) wait_b(std::integral_constant<int, 8 * AK + nB2 + 2 * AK>{}, (kt + 1) & 1);
-                        stage_unit(kt + 1, std::integral_constant<int, (ks >> 1)>{});
-                    }
+                if constexpr (nb == kBigNB - 1 && more)
+                    issue_a(std::integral_constant<int, kt + 1>{}, std::integral_constant<int, ks>{});
+                // next k-tile's weights go to the other buffer (last read before the
+                // previous barrier): one 8-column run (one dequant8, one LDS write)
+                // every third fragment from fragment 8 on, so the VALU work
+                // interleaves with the MFMAs in flight
+                constexpr int run = (f - 8) / 3;
+                if constexpr (more && f >= 8 && (f - 8) % 3 == 0 && run < 4 * UNITS) {
+                    // B(kt+1) was issued before A(kt), B(kt+2) and A(kt+1, 0)
+                    if constexpr (run == 0) wait_b(std::integral_constant<int, 8 * AK + nB2 + AK>{}, (kt + 1) & 1);
+                    stage_run(kt + 1, std::integral_constant<int, run / 4>{}, std::integral_constant<int, run % 4>{});
                 }
             });
             lgkm_wait<0>();  // this k-tile's staging writes (asm, not tracked by the compiler)
