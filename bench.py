@@ -184,7 +184,7 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False):
                 res["dominant"] = {"kernel": f"experts_prefill_big_kernel<{128 // group}, true, 10> (gate+up)",
                                    "ms": stage["gate_up"], "flops": fl_gu, "tflops": res["gate_up_tflops"],
                                    "mfma_frac": res["gate_up_mfma_frac"],
-                                   "profile_file": f"experts_prefill_config{cfg}_kernel_stats.md"}
+                                   "profile_file": "experts_prefill_config3_kernel_stats.md" if cfg == 3 else None}
             else:
                 res["dominant"] = {"kernel": "expert_decode_kernel<4, 10, true> (gate+up)", "ms": stage["gate_up"],
                                    "bytes": avg["gate_up"], "gbs": res["gate_up_gbs"],
