@@ -1,12 +1,14 @@
 // Combine of the prefill path: out[t] = residual + weighted routed rows +
 // shared-expert rows, from the grouped [slots, hidden] expert outputs.
+#include <algorithm>
+
 #include "launch.hpp"
 
 namespace uocr_hip {
 
 // out[t] = residual[t] + (sum_j fma(w[t,j], y[pos[t,j]]) in j order) + shared(t)
 // (src/engine/moe_decoder.cpp:88-97,111-112,179).
-__global__ __launch_bounds__(256) void combine_kernel(CombineArgs c) {
+__global__ __launch_bounds__(1024) void combine_kernel(CombineArgs c) {
     const int t = blockIdx.x;
     const int H = c.hidden;
     for (int col = threadIdx.x * 4; col < H; col += blockDim.x * 4) {
@@ -40,7 +42,10 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs c) {
 
 hipError_t launch_combine(const CombineArgs& c, hipStream_t st) {
     if (c.seq <= 0) return hipSuccess;
-    launch_k(combine_kernel, dim3(c.seq), dim3(256), 0, st, c);
+    // one 16-byte column group per thread, the whole row in one pass
+    // (hidden / 4 threads rounded up to whole waves, at most 1024)
+    const int threads = std::min(1024, ((c.hidden / 4 + 63) / 64) * 64);
+    launch_k(combine_kernel, dim3(c.seq), dim3(threads), 0, st, c);
     return hipGetLastError();
 }
 
