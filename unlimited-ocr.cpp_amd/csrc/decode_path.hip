@@ -245,18 +245,24 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(DecodeArgs a) {
 // Combine: out[t] = residual[t] + (sum_j fma(w[t,j], y[t*K + j]) in j order)
 // + sum_v y[N + v*T + t]   (src/engine/moe_decoder.cpp:88-97,110-112,179)
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void combine_decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(1024) void combine_decode_kernel(DecodeArgs a) {
     const int t = blockIdx.x, tid = threadIdx.x;
     const int T = a.seq, K = a.top_k, N = T * K, H = a.hidden;
     float wt[kMaxTopK];
 #pragma unroll
     for (int j = 0; j < kMaxTopK; ++j) wt[j] = j < K ? a.wts[(size_t)t * K + j] : 0.0f;
     const float* res = a.rms_weight ? static_cast<const float*>(a.x) + (size_t)t * H : nullptr;
-    for (int c = tid * 4; c < H; c += 256 * 4) {
-        f32x4 yv[kMaxTopK];
+    // one 16-byte column group per thread (the launch covers the row in one
+    // pass); every row this thread needs is requested before the first FMA
+    // (indices clamped, so no load sits behind a branch)
+    for (int c = tid * 4; c < H; c += blockDim.x * 4) {
+        f32x4 yv[kMaxTopK], ys[2];
 #pragma unroll
         for (int j = 0; j < kMaxTopK; ++j)
-            if (j < K) yv[j] = *reinterpret_cast<const f32x4*>(a.y + ((size_t)t * K + j) * H + c);
+            yv[j] = *reinterpret_cast<const f32x4*>(a.y + ((size_t)t * K + min(j, K - 1)) * H + c);
+#pragma unroll
+        for (int v = 0; v < 2; ++v)
+            ys[v] = *reinterpret_cast<const f32x4*>(a.y + ((size_t)N + (size_t)min(v, max(a.n_virtual - 1, 0)) * T + t) * H + c);
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < kMaxTopK; ++j)
@@ -264,9 +270,9 @@ __global__ __launch_bounds__(256) void combine_decode_kernel(DecodeArgs a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[i] = fmaf(wt[j], yv[j][i], acc[i]);
         if (a.n_virtual > 0) {
-            f32x4 sh = *reinterpret_cast<const f32x4*>(a.y + ((size_t)N + t) * H + c);
+            f32x4 sh = ys[0];
             for (int v = 1; v < a.n_virtual; ++v) {
-                const f32x4 y2 = *reinterpret_cast<const f32x4*>(a.y + ((size_t)N + (size_t)v * T + t) * H + c);
+                const f32x4 y2 = v < 2 ? ys[1] : *reinterpret_cast<const f32x4*>(a.y + ((size_t)N + (size_t)v * T + t) * H + c);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) sh[i] += y2[i];
             }
@@ -365,7 +371,8 @@ hipError_t launch_experts_decode2(const DecodeArgs& a, bool gate_up, hipStream_t
 }
 
 hipError_t launch_combine_decode(const DecodeArgs& a, hipStream_t st) {
-    launch_k(combine_decode_kernel, dim3(a.seq), dim3(256), 0, st, a);
+    const int threads = std::min(1024, ((a.hidden / 4 + 63) / 64) * 64);
+    launch_k(combine_decode_kernel, dim3(a.seq), dim3(threads), 0, st, a);
     return hipGetLastError();
 }
 
