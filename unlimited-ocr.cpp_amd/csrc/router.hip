@@ -584,9 +584,10 @@ static hipError_t launch_router_t(const RouterArgs& a, hipStream_t st) {
 
 template <typename XT, bool RMS>
 static hipError_t launch_router_w(const RouterArgs& a, hipStream_t st) {
-    // small batches: 4 tokens per workgroup spreads the FMA chains over CUs;
-    // large batches: 16 tokens per workgroup amortise the router-weight stream
-    return a.seq >= 256 ? launch_router_t<XT, RMS, 16>(a, st) : launch_router_t<XT, RMS, 4>(a, st);
+    // 4 tokens per workgroup spread the FMA chains over the CUs; once that
+    // gives 4+ workgroups per CU (4096 tokens on 256 CUs), 16 tokens per
+    // workgroup amortise the router-weight stream
+    return a.seq >= 4096 ? launch_router_t<XT, RMS, 16>(a, st) : launch_router_t<XT, RMS, 4>(a, st);
 }
 
 hipError_t launch_router(const RouterArgs& a, bool x_is_bf16, hipStream_t st) {
