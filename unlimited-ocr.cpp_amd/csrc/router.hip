@@ -187,7 +187,8 @@ __device__ void group_body(const int* ids, const float* wts, const GroupArgs& g,
         }
         for (int k = tid; k < kGroupWaves * kMaxExperts; k += kGroupThreads) (&s.wcnt[0][0])[k] = 0;
         __syncthreads();
-        const bool valid = e >= 0 && e < E;
+        // i < N: past the last round's end, nid still holds an earlier round's id
+        const bool valid = i < N && e >= 0 && e < E;
         uint64_t m = __ballot(valid);
 #pragma unroll
         for (int b = 0; b < 7; ++b) {
@@ -610,6 +611,8 @@ int group_chunks(int seq, int top_k) { return (seq * top_k + kGroupThreads - 1) 
 
 hipError_t launch_group(const GroupArgs& g, hipStream_t st) {
     const int n_chunks = group_chunks(g.seq, g.top_k);
+    // one workgroup for a single 1024-entry round (or without the multi-kernel
+    // scratch); measured slower than rank / scan / place from 6 rounds on
     if (n_chunks <= 1 || !g.lrank) {
         launch_k(group_kernel, dim3(1), dim3(kGroupThreads), 0, st, g);
         return hipGetLastError();
