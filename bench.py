@@ -194,15 +194,30 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False):
     return res
 
 
+def _cpu_model():
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(seconds=10.0):
     """Oracle (port of the reference CPU path) on config 1's 16 tokens, repeated
-    for ~`seconds`, all host threads (tokens run in parallel)."""
+    for ~`seconds`. Threads: the box's CPU share for one GPU (16, or fewer if the
+    host has fewer), one token per thread at a time. The reference itself runs a
+    token's routed experts serially and uses OpenMP only inside the router and
+    shared-expert GEMMs (src/runtime/weights.cpp:51-72, src/kernels/cpu_ops.cpp:11-39);
+    the per-token parallelism here is a stated deviation that favours the CPU."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     from uocr_hip import synth
 
     wl = synth.make_config(1)
-    threads = min(16, os.cpu_count() or 1)
+    nproc = os.cpu_count() or 1
+    threads = min(16, nproc)
     n = 0
     t0 = time.perf_counter()
     while True:
@@ -212,7 +227,11 @@ def cpu_baseline(seconds=10.0):
             break
     dt = time.perf_counter() - t0
     return {"value": n * wl.seq / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"config 1 layer (16 tokens, all routed+shared experts) x{n} runs, {dt:.1f}s"}
+            "nproc": nproc, "cpu_model": _cpu_model(), "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
+            "threading": "tokens in parallel, one thread per token (reference: routed experts serial per "
+                         "token, OpenMP only in router/shared GEMMs)",
+            "sample": f"config 1 layer (16 tokens, all routed+shared experts) x{n} runs, {dt:.1f}s",
+            "note": "reported baseline, not the target"}
 
 
 def measured_traffic(name):

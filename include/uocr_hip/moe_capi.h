@@ -131,9 +131,15 @@ int uocr_hip_moe_layer_path(const uocr_hip_moe_layer* layer, int seq);
 /* Sticky fault flags of the single-kernel decode path (no counterpart in the
  * reference; for callers and tests that verify a run): bit 0 = a bounded wait
  * between workgroups timed out, bit 1 = an exact top-k pick was outside the
- * candidate experts the down pass was computed for. Waits for the device,
- * stores the flags in *flags and, if clear is non-zero, resets them. */
+ * candidate experts the down pass was computed for. Either fault also makes
+ * the affected call's `out` rows NaN, so a result is never silently wrong.
+ * Waits for the device, stores the flags in *flags and, if clear is non-zero,
+ * resets them. */
 int uocr_hip_moe_layer_status(uocr_hip_moe_layer* layer, int clear, int* flags);
+
+/* The same flags copied, stream-ordered and without a host wait, into the
+ * caller's device int `d_flags` (no counterpart in the reference). */
+int uocr_hip_moe_layer_status_async(const uocr_hip_moe_layer* layer, int* d_flags, void* stream);
 
 /* ---- reference operator mirrors (include/uocr/cuda_ops.h) ---------------- */
 
@@ -150,6 +156,12 @@ int uocr_hip_moe_router_topk(const float* router_logits, int seq, int n_experts,
                              int scoring_sigmoid, int* d_ids, float* d_weights,
                              int* d_assign_token, float* d_assign_w, int* d_count, int cap,
                              void* stream);
+
+/* Overflow report of uocr_hip_moe_router_topk (the reference drops entries
+ * past `cap` silently, moe_device.cu:90-95): *flag = 1 if any call since the
+ * last clear routed more than `cap` entries to one expert (only possible when
+ * cap < seq). Synchronises the device; clear != 0 resets the flag. */
+int uocr_hip_moe_router_overflow(int clear, int* flag);
 
 #ifdef __cplusplus
 }

@@ -45,8 +45,10 @@ def _status_clear(layer, label):
 
 @pytest.mark.parametrize("group", [32, 64, 128])
 def test_fused_batch_sizes_one_layer(dev, group):
-    """Sparse (seq < 12) and dense (seq >= 12) gate/up on one layer object, the
-    batch size changing between calls."""
+    """One layer object, the batch size changing between calls: 12..16 tokens
+    run the single-kernel path, 1..11 tokens the four-launch decode path, so
+    the fused kernel's progress words must stay consistent across calls that
+    skip it."""
     from uocr_hip import MoELayerInt4, synth
     L = synth.random_layer(4100 + group, group=group)
     layer = MoELayerInt4(L)
@@ -148,4 +150,22 @@ def test_fused_tied_router_rows(dev, ulps):
     if ulps == 0:
         assert (got[0] == 9).any(axis=1).all() and not (got[0] == 20).any(), "equal scores: lower index"
     _status_clear(layer, f"tied-{ulps}")
+    layer.close()
+
+
+def test_fused_status_async_and_path(dev):
+    """The stream-ordered status copy reads the same (clear) flags as the
+    synchronising query, and 12..16-token bf16 calls take the decode path."""
+    import torch
+    from uocr_hip import MoELayerInt4, synth
+    L = synth.random_layer(4600)
+    layer = MoELayerInt4(L)
+    x = synth.bf16_normal(np.random.default_rng(21), (16, L.hidden), 1.0)
+    _check(L, x, _forward(layer, x, dev), "status-async")
+    flags = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    layer.status_async(flags)
+    torch.cuda.synchronize()
+    assert int(flags.item()) == 0
+    assert layer.path(16) == "decode"
+    _status_clear(layer, "status-async")
     layer.close()

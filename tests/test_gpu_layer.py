@@ -155,7 +155,8 @@ def test_permutation_bit_exact(dev):
     from uocr_hip import ops, synth
 
     rng = np.random.default_rng(3)
-    for seq, E, k in [(1, 64, 6), (16, 64, 6), (517, 64, 6), (2048, 8, 2), (300, 128, 8)]:
+    ops.moe_router_overflow(clear=True)
+    for seq, E, k in [(1, 64, 6), (16, 64, 6), (517, 64, 6), (2048, 8, 2), (300, 128, 8), (1111, 64, 6)]:
         logits = rng.standard_normal((seq, E)).astype(np.float32)
         lg = torch.from_numpy(logits).to(dev)
         cap = seq
@@ -174,8 +175,67 @@ def test_permutation_bit_exact(dev):
         c = cnt.cpu().numpy()
         a = at.cpu().numpy()
         assert np.array_equal(c, np.minimum(counts, cap))
+        aw_h = aw.cpu().numpy()
         for e in range(E):
             assert np.array_equal(a[e, : c[e]], perm[offs[e]: offs[e] + c[e]])
+            # nothing written past an expert's entries (the multi-round grouping
+            # once placed stale entries there)
+            assert (a[e, c[e]:] == -1).all() and (aw_h[e, c[e]:] == 0).all(), e
+        assert ops.moe_router_overflow() == 0
         # brute force: the stable sort of (expert, token) pairs
         flat_tok = np.repeat(np.arange(seq), k)
         assert np.array_equal(perm, flat_tok[np.argsort(ids_o.ravel(), kind="stable")])
+
+
+def test_router_overflow_reported(dev):
+    """cap below an expert's count: the tables keep the first `cap` entries in
+    (token, j) order, count reads min(count, cap), and the overflow flag is
+    raised (the reference drops the rest silently, moe_device.cu:90-95)."""
+    torch = _torch()
+    import oracle as O
+    from uocr_hip import ops
+
+    rng = np.random.default_rng(8)
+    seq, E, k, cap = 64, 8, 2, 8
+    logits = rng.standard_normal((seq, E)).astype(np.float32)
+    lg = torch.from_numpy(logits).to(dev)
+    ids = torch.empty(seq, k, dtype=torch.int32, device=dev)
+    w = torch.empty(seq, k, dtype=torch.float32, device=dev)
+    at = torch.full((E, cap), -1, dtype=torch.int32, device=dev)
+    aw = torch.zeros(E, cap, dtype=torch.float32, device=dev)
+    cnt = torch.empty(E, dtype=torch.int32, device=dev)
+    ops.moe_router_overflow(clear=True)
+    ops.moe_router_topk(lg, k, False, 1.0, False, ids, w, at, aw, cnt, cap)
+    torch.cuda.synchronize()
+    ids_o, _ = O.moe_gate_f32router(logits, np.eye(E, dtype=np.float32), k)
+    counts, offs, perm = O.stable_group(ids_o, E)
+    assert counts.max() > cap
+    assert np.array_equal(cnt.cpu().numpy(), np.minimum(counts, cap))
+    a = at.cpu().numpy()
+    for e in range(E):
+        n = min(counts[e], cap)
+        assert np.array_equal(a[e, :n], perm[offs[e]: offs[e] + n])
+    assert ops.moe_router_overflow(clear=True) == 1
+    assert ops.moe_router_overflow(clear=True) == 0
+
+
+@pytest.mark.parametrize("seq", [5, 16, 300])
+def test_routing_options(dev, seq):
+    """norm_topk_prob = 1, sigmoid scoring and routed_scaling_factor = 2.5 on
+    the decode (5), single-kernel (16, bf16) and prefill (300) paths."""
+    from uocr_hip import synth
+    for norm, sig, scale in [(1, 0, 1.0), (0, 1, 2.5), (1, 1, 2.5)]:
+        L = synth.random_layer(700 + seq + 10 * sig + norm, group=32)
+        L.norm_topk_prob, L.scoring_sigmoid, L.routed_scaling_factor = norm, sig, scale
+        x = synth.bf16_normal(np.random.default_rng(seq + norm), (seq, L.hidden), 1.0)
+        check_parity(L, x, dev, sample=24 if seq > 64 else None, label=f"route-n{norm}-s{sig}-x{scale}-t{seq}")
+
+
+@pytest.mark.parametrize("seq", [5, 16, 300])
+def test_no_shared_experts(dev, seq):
+    """n_shared = 0 with 8 experts, top-2: no shared rows in y, on the decode,
+    single-kernel and prefill paths."""
+    from uocr_hip import synth
+    L = synth.random_layer(800 + seq, n_experts=8, top_k=2, n_shared=0, group=32)
+    x = synth.bf16_normal(np.random.default_rng(seq), (seq, L.hidden), 1.0)
+    check_parity(L, x, dev, sample=24 if seq > 64 else None, label=f"noshared-t{seq}")

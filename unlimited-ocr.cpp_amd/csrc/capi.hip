@@ -191,17 +191,10 @@ bool use_prefill(const uocr_hip_moe_layer* L, int seq) {
 // its gate/up pass covers every group for all tokens (no wait for routing),
 // worth it once most experts are live anyway (1 - (1 - 6/64)^12 = 69 % at
 // top-6 of 64); fewer tokens take the four-launch decode path.
-// UOCR_FUSED=0 selects that path throughout (testing).
 constexpr int kDenseMinSeq = 12;
 
-int env_int(const char* name, int dflt) {
-    const char* e = std::getenv(name);
-    return e ? std::atoi(e) : dflt;
-}
-
 bool use_fused(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
-    static const int on = env_int("UOCR_FUSED", 1);
-    return on && L->sync && seq >= kDenseMinSeq && seq <= kFusedMaxSeq && x_dtype == UOCR_HIP_DTYPE_BF16 &&
+    return L->sync && seq >= kDenseMinSeq && seq <= kFusedMaxSeq && x_dtype == UOCR_HIP_DTYPE_BF16 &&
            !L->rms_weight &&
            decode_fused_ok(L->hidden, L->inter, L->group) && L->n_experts + L->n_virtual <= kMaxExperts;
 }
@@ -396,6 +389,7 @@ size_t uocr_hip_moe_layer_device_bytes(const uocr_hip_moe_layer* layer) {
 
 size_t uocr_hip_moe_layer_workspace_size(const uocr_hip_moe_layer* layer, int seq) {
     if (!layer || seq <= 0) return 0;
+    if (use_prefill(layer, seq) && !group_fits(seq, layer->top_k, layer->n_experts)) return 0;
     return plan(layer, seq).total;
 }
 
@@ -413,6 +407,17 @@ int uocr_hip_moe_layer_status(uocr_hip_moe_layer* L, int clear, int* flags) {
     return UOCR_HIP_OK;
 }
 
+int uocr_hip_moe_layer_status_async(const uocr_hip_moe_layer* L, int* d_flags, void* stream) {
+    if (!L || !d_flags) return fail(UOCR_HIP_EINVAL, "null argument");
+    hipStream_t st = (hipStream_t)stream;
+    if (!L->sync) {
+        HIP_TRY(hipMemsetAsync(d_flags, 0, sizeof(int), st), "status copy");
+        return UOCR_HIP_OK;
+    }
+    HIP_TRY(hipMemcpyAsync(d_flags, &L->sync->error, sizeof(int), hipMemcpyDeviceToDevice, st), "status copy");
+    return UOCR_HIP_OK;
+}
+
 int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x_dtype, int seq,
                                float* out, int* ids_out, float* weights_out, void* workspace,
                                size_t workspace_bytes, void* stream) {
@@ -422,6 +427,9 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     if (L->rms_weight && x_dtype != UOCR_HIP_DTYPE_F32)
         return fail(UOCR_HIP_EINVAL, "a layer with rms_weight adds the residual and needs f32 x");
     if ((uintptr_t)x % 16 || (uintptr_t)out % 16) return fail(UOCR_HIP_EINVAL, "x and out must be 16-byte aligned");
+    if (use_prefill(L, seq) && !group_fits(seq, L->top_k, L->n_experts))
+        return fail(UOCR_HIP_EUNSUPPORTED, "seq * top_k too large for the grouping scan (" + std::to_string(seq) +
+                                               " tokens)");
     const WsPlan p = plan(L, seq);
     if (!workspace || workspace_bytes < p.total)
         return fail(UOCR_HIP_EWORKSPACE, "workspace too small: need " + std::to_string(p.total) + " bytes");
@@ -485,8 +493,6 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
         da.out = out;
         if (use_fused(L, seq, x_dtype)) {
             da.sync = L->sync;
-            static const int dense_dn = env_int("UOCR_DENSE_DN", 0);
-            da.dense_dn = dense_dn > 0;
             stage(5);
             HIP_TRY(launch_decode_fused(da, st), "fused decode launch");
             stage(-1);
@@ -651,6 +657,12 @@ int uocr_hip_moe_layer_read_timing(uocr_hip_moe_layer* L, float* stage_ms, int n
     if (n_calls) *n_calls = L->timed_calls;
     std::memset(L->stage_ms, 0, sizeof(L->stage_ms));
     L->timed_calls = 0;
+    return UOCR_HIP_OK;
+}
+
+int uocr_hip_moe_router_overflow(int clear, int* flag) {
+    if (!flag) return fail(UOCR_HIP_EINVAL, "null argument");
+    HIP_TRY(router_overflow_read(clear, flag), "router overflow flag");
     return UOCR_HIP_OK;
 }
 

@@ -24,37 +24,13 @@
 // workgroup publishes S + steps done, S being its word at kernel start (every
 // word ends a call at S + kFusedSteps). A workgroup only waits for steps that
 // other resident workgroups reach without waiting for it, and every wait is
-// bounded (kSpinLimit), setting a sticky flag in FusedSync::error on timeout.
+// bounded (kSpinLimit): a timeout sets a sticky flag in FusedSync::error and
+// makes the call's outputs NaN (never a silently wrong result).
 //
 // Cross-workgroup data (candidate words, ids / weights, act rows, y rows) is
 // written and read with agent-coherent (sc1) accesses around the progress
 // stores; act and y rows are indexed by (group, token): g * T + t.
 #include <hip/hip_runtime.h>
-// Timeline trace build (-DUOCR_FTRACE, never the shipped library): FTR(i)
-// stamps workgroup phase i, RTR(i) router step i, with the 100 MHz wall clock;
-// uocr_ftrace_read / uocr_rtrace_read copy the stamps to the host.
-#if defined(UOCR_FTRACE)
-__device__ unsigned long long uocr_ftrace[4096 * 16];
-extern "C" hipError_t uocr_ftrace_read(void* host, size_t bytes) {
-    return hipMemcpyFromSymbol(host, HIP_SYMBOL(uocr_ftrace), bytes, 0, hipMemcpyDeviceToHost);
-}
-extern "C" hipError_t uocr_ftrace_clear() {
-    void* p = nullptr;
-    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(uocr_ftrace));
-    return e != hipSuccess ? e : hipMemset(p, 0, sizeof(unsigned long long) * 4096 * 16);
-}
-#define FTR(i) \
-    if (threadIdx.x == 0) uocr_ftrace[blockIdx.x * 16 + (i)] = wall_clock64();
-__device__ unsigned long long uocr_rtrace[64 * 16];
-extern "C" hipError_t uocr_rtrace_read(void* host, size_t bytes) {
-    return hipMemcpyFromSymbol(host, HIP_SYMBOL(uocr_rtrace), bytes, 0, hipMemcpyDeviceToHost);
-}
-#define RTR(i) \
-    if ((threadIdx.x & 63) == 0) uocr_rtrace[blockIdx.x * 16 + (i)] = wall_clock64();
-#else
-#define FTR(i)
-#define RTR(i)
-#endif
 #include "decode_common.hpp"
 
 #include <algorithm>
@@ -65,6 +41,17 @@ namespace uocr_hip {
 
 constexpr int kSpinLimit = 1 << 20;    // bounded waits (~1 s)
 constexpr int kFusedSteps = 1 << 12;   // progress advance per call (> steps of any workgroup)
+
+// A bounded wait ran out: the sticky status bit, and this call's tag in
+// call_fault so that the call's combine writes NaN instead of a result built
+// from incomplete rows. Both stores are released (agent scope) before the
+// caller publishes any further progress, so a workgroup that waited for that
+// progress sees the fault.
+__device__ __forceinline__ void report_timeout(FusedSync* sy, unsigned rtag) {
+    __hip_atomic_fetch_or(&sy->error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&sy->call_fault, rtag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+}
 
 // Cross-workgroup data moves through agent-coherent accesses (sc1: written
 // through to, and read from, the coherence point shared by every XCD's L2), so
@@ -177,7 +164,6 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
         xs[tid + 256 * i] = __uint_as_float(xb[i] << 16);
     }
     lds_barrier();
-    RTR(0)
     const uint32_t xa = lds_addr(xs + wave * SEG);
 
     // Candidate experts of the token, ahead of the exact chain: this wave's
@@ -260,7 +246,6 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
             if (w == 0 && wave == 3) early_finish();
         } else {
             if (w > 0) acc = hand[lane];
-            RTR(1 + w)
             f32x4 c0, c1, n0, n1;
             asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:16\n\ts_waitcnt lgkmcnt(0)"
                          : "=&v"(c0), "=&v"(c1) : "v"(xa) : "memory");
@@ -289,7 +274,6 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
                     c1 = n1;
                 }
             }
-            RTR(5 + w)
             if (w < 3) hand[lane] = acc;
             // the expf table for the selection (wave 0's weight burst is drained)
             if (w == 0 && lane < 32) etab[lane] = uocr_exp2_tab[lane];
@@ -298,7 +282,6 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
     }
     if (wave == 3) router_select<true>(a, t, acc, sc, topv, etab);
     __builtin_amdgcn_s_setprio(0);
-    RTR(9)
 }
 
 constexpr int kFusedWGPerCU = 2;  // workgroups per CU (the progress words need them all resident)
@@ -337,8 +320,6 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
     // this call's base: every workgroup ended the previous call at the same value
     const int S = load_cg(prog + b);
     const unsigned rtag = (((unsigned)S >> 12) + 1u) & 0xFFFFFFu;  // routing words of this call
-    FTR(0)
-    int ftr = 2;
     int k = 0;  // steps published by this workgroup
     auto publish = [&]() {
         __syncthreads();  // every wave's stores of the step are complete
@@ -359,7 +340,7 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
                 int it = 0;
                 while (__ballot(want && (int)(load_cg(prog + owner) - (S + step)) < 0)) {
                     if (++it > kSpinLimit) {
-                        if (lane == 0) __hip_atomic_fetch_or(&sy->error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        if (lane == 0) report_timeout(sy, rtag);
                         break;
                     }
                     __builtin_amdgcn_s_sleep(1);
@@ -403,7 +384,7 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
             int it = 0;
             while (__ballot((uint32_t)(cw >> 32) != rtag)) {
                 if (++it > kSpinLimit) {
-                    if (lane == 0) __hip_atomic_fetch_or(&sy->error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (lane == 0) report_timeout(sy, rtag);
                     break;
                 }
                 __builtin_amdgcn_s_sleep(1);
@@ -433,7 +414,7 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
     // the count
     auto token_list = [&](int g) {
         int* el = ent + wave * 16;
-        if (g < E && !a.dense_dn) {
+        if (g < E) {
             const int tm = tokmask[g];
             const bool hit = lane < T && ((tm >> lane) & 1);
             const uint64_t m = __ballot(hit);
@@ -530,7 +511,7 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
             int it = 0;
             while (__ballot(want && (int)(pv - (S + pstep)) < 0)) {
                 if (++it > kSpinLimit) {
-                    if (lane == 0) __hip_atomic_fetch_or(&sy->error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (lane == 0) report_timeout(sy, rtag);
                     break;
                 }
                 __builtin_amdgcn_s_sleep(1);
@@ -539,7 +520,6 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
         }
         lds_barrier();  // the other waves' weights stay in flight
         fence_wg_acquire();
-        if (ftr == 8) { FTR(11) }
         if (r < cnt) {
             const int tok = ent[wave * 16 + r];
             const f16* src = a.act + (size_t)(g * T + tok) * I + wave * 32 + 8 * (lane >> 4);
@@ -555,7 +535,6 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
         }
         wait_vm<0>();
         lds_barrier();
-        if (ftr == 8) { FTR(12) }
         bias_seeds<KT, GPT>(As, Cs, tid);
         lds_barrier();
         if (rbw0 * kTileRows < H) {
@@ -584,6 +563,9 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
         // requested before the one wait)
         const int t = tid >> 4;
         if (t >= T) return;
+        // a timed-out wait anywhere in this call (reported before the progress
+        // this combine waited for) makes every output of the call NaN
+        bool bad = load_cg(&sy->call_fault) == rtag;
         constexpr int NY = kMaxTopK + 2;  // routed rows, then the first two shared rows
         const size_t sh0 = (size_t)E * T;  // first shared row
         const int c0 = rb * 128 + (tid & 15) * 4;
@@ -596,8 +578,10 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
                 const int id = ids_c[t * K + j];
                 // the exact pick is one of the token's candidates (else its y
                 // row was not computed: flagged, never silent)
-                if (!a.dense_dn && !((cm32[2 * t + (id >> 5)] >> (id & 31)) & 1u))
+                if (!((cm32[2 * t + (id >> 5)] >> (id & 31)) & 1u)) {
                     __hip_atomic_fetch_or(&sy->error, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    bad = true;
+                }
 #pragma unroll
                 for (int h = 0; h < 2; ++h)
                     if (c0 + 64 * h < H) load16_cg_issue(yv[h * NY + j], a.y + ((size_t)id * T + t) * H + c0 + 64 * h);
@@ -636,6 +620,7 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
 #pragma unroll
                 for (int q = 0; q < 4; ++q) acc[q] += sh[q];
             }
+            if (bad) acc = f32x4{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")};
             *reinterpret_cast<f32x4*>(a.out + (size_t)t * H + c) = acc;
         }
     };
@@ -648,7 +633,6 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
         uint64_t* etab = reinterpret_cast<uint64_t*>(topv + kMaxTopK);
         router_token_regs<KTG>(a, b, hand, sc, topv, etab, hand + 256, hand + 256 + kMaxHidden, rtag);
         publish();
-        FTR(1)
     }
 
     // ---- 2. gate/up (workers T .. P-1): every group for all tokens
@@ -659,7 +643,6 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
             if (i >= ngu_total) break;
             gate_up_item(i / RBG, i % RBG, i + PW >= ngu_total);
             publish();
-            if (ftr < 6) { FTR(ftr) ++ftr; }
         }
     }
 
@@ -669,12 +652,10 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
     // stream runs on from gate/up into down while the router finishes. Sparse:
     // the live groups only (the routing summary first).
     need_summary();
-    FTR(6)
-    ftr = 7;
-    const int n_dn_groups = a.dense_dn ? G : n_live;
+    const int n_dn_groups = n_live;
     const int ndn_total = n_dn_groups * RBD;
     // position of gate/up item r of the group at down position gpos
-    auto gu_index = [&](int gpos, int r_) { return (a.dense_dn ? gpos : live[gpos]) * RBG + r_; };
+    auto gu_index = [&](int gpos, int r_) { return live[gpos] * RBG + r_; };
     // Down items go to "slots" in the order the workgroups behind them are
     // expected to be free: workers with one gate/up item fewer, workers that
     // are first on their CU (issue priority goes to the older workgroup),
@@ -699,9 +680,8 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
     for (int j = my_slot; j < ndn_total; j += P) {
         fresh_indices();
         const int gpos = j / RBD, rb = j % RBD;
-        if (ftr < 13) { FTR(ftr) ++ftr; }
         down_item(
-            a.dense_dn ? gpos : live[gpos], rb,
+            live[gpos], rb,
             [&](int q, int& owner, int& step) {
                 const int i = gu_index(gpos, q);
                 owner = T + i % PW;
@@ -709,7 +689,6 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
             },
             RBG);
         publish();
-        if (ftr < 13) { FTR(ftr) ++ftr; }
     }
     // combine of column block rb by slot (ndn_total + rb) % P, one with the
     // fewest down items, after all of its own (a combine waits only for down
@@ -728,15 +707,12 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
             have_route = true;
         }
         wait_steps([&](int q, int& owner, int& step) { dn_step(q * RBD + rb, owner, step); }, n_dn_groups);
-        FTR(13)
         combine_block(rb);
-        FTR(14)
     }
 
     // ---- leave: every workgroup ends the call at S + kFusedSteps
     __syncthreads();
     if (tid == 0) store_cg(prog + b, S + kFusedSteps);
-    FTR(15)
 }
 
 template <int GPT, int KTG, int KTD>
@@ -759,8 +735,30 @@ static hipError_t launch_fused(const DecodeArgs& a, hipStream_t st) {
     // and fully resident (workgroups wait for one another)
     const int grid = std::min(resident, kFusedMaxGrid);
     if (grid <= a.seq) return hipErrorInvalidConfiguration;
-    launch_k((decode_fused_kernel<GPT, KTG, KTD>), dim3(grid), dim3(256), (uint32_t)lds, st, a);
-    return hipGetLastError();
+    // A cooperative launch guarantees that the whole grid is resident at once
+    // (the runtime refuses the launch otherwise, instead of letting waiting
+    // workgroups starve those they wait for). Under stream capture the
+    // cooperative form is not recorded; the kernel is then launched plainly and
+    // relies on the bounded waits (a timeout makes the call's output NaN).
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(st, &cs);
+    if (e != hipSuccess) return e;
+    if (cs != hipStreamCaptureStatusNone) {
+        launch_k((decode_fused_kernel<GPT, KTG, KTD>), dim3(grid), dim3(256), (uint32_t)lds, st, a);
+        return hipGetLastError();
+    }
+    StageEvents& ev = stage_events();
+    if (ev.start && (e = hipEventRecord(ev.start, st)) != hipSuccess) return e;
+    DecodeArgs args = a;
+    void* params[] = {&args};
+    e = hipLaunchCooperativeKernel((const void*)decode_fused_kernel<GPT, KTG, KTD>, dim3(grid), dim3(256), params,
+                                   (unsigned)lds, st);
+    if (e != hipSuccess) return e;
+    if (ev.stop) {
+        ev.start = nullptr;
+        if ((e = hipEventRecord(ev.stop, st)) != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 bool decode_fused_ok(int hidden, int inter, int group) {

@@ -260,9 +260,12 @@ __global__ __launch_bounds__(1024) void combine_decode_kernel(DecodeArgs a) {
 #pragma unroll
         for (int j = 0; j < kMaxTopK; ++j)
             yv[j] = *reinterpret_cast<const f32x4*>(a.y + ((size_t)t * K + min(j, K - 1)) * H + c);
+        // shared rows exist only with a shared MLP (y holds N + n_virtual*T rows)
+        if (a.n_virtual > 0) {
 #pragma unroll
-        for (int v = 0; v < 2; ++v)
-            ys[v] = *reinterpret_cast<const f32x4*>(a.y + ((size_t)N + (size_t)min(v, max(a.n_virtual - 1, 0)) * T + t) * H + c);
+            for (int v = 0; v < 2; ++v)
+                ys[v] = *reinterpret_cast<const f32x4*>(a.y + ((size_t)N + (size_t)min(v, a.n_virtual - 1) * T + t) * H + c);
+        }
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < kMaxTopK; ++j)

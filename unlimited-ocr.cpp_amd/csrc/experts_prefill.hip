@@ -248,19 +248,6 @@ constexpr int kRingAhead = 4;               // B fragments read ahead of their u
 constexpr int kRing = kRingAhead + 2;       // register ring size
 constexpr int lds_reads_after(int f) { return 63 - f < kRingAhead - 1 ? 63 - f : kRingAhead - 1; }
 
-// Trace build (-DUOCR_PTRACE, never the shipped library): thread 0 of each
-// workgroup records s_memtime at its start (0), after the prologue (1), after
-// each k-tile (2 + kt) and at its end (13), plus its tile and live rows (14)
-// and s_memrealtime at start (15) and end (12), per pass (gate/up, down);
-// uocr_hip_debug_ptrace copies the table out after a layer call.
-#ifdef UOCR_PTRACE
-__device__ unsigned long long g_ptrace[2][8192][16];
-#define PT(i) do { if (threadIdx.x == 0 && blockIdx.x < 8192) g_ptrace[GU ? 0 : 1][blockIdx.x][i] = __builtin_amdgcn_s_memtime(); } while (0)
-#define PTV(i, v) do { if (threadIdx.x == 0 && blockIdx.x < 8192) g_ptrace[GU ? 0 : 1][blockIdx.x][i] = (v); } while (0)
-#else
-#define PT(i) do {} while (0)
-#define PTV(i, v) do {} while (0)
-#endif
 template <int GPT, bool GU, int KT>
 __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) {
     // B fragments: [buffer][k-step 0..7][n-block 0..7][64 lanes][8 f16]
@@ -273,13 +260,10 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
     const int tile = (local / n_ntiles) * 8 + xcd, ntile = local % n_ntiles;
     const int n_tiles = *a.n_tiles;
     if (tile >= n_tiles) return;
-    PT(0);
-    PTV(15, __builtin_amdgcn_s_memrealtime());
     // one 16-byte record per tile: expert, first row, live rows, first slot
     const int4 ti = *reinterpret_cast<const int4*>(a.tile_info + 4 * tile);
     const int e = ti.x, rows = ti.z, slot0 = ti.w;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    PTV(14, (unsigned long long)tile * 65536 + rows);
 
     // A tile of at most 128 live rows runs in half mode: each wave takes 32
     // rows (JN = 1) instead of 64 (JN = 2), so it costs half the MFMAs and
@@ -411,7 +395,6 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
         static_for<UNITS>([&](auto ic) { static_for<4>([&](auto sc) { stage_run(0, ic, sc); }); });
         lgkm_wait<0>();
         __syncthreads();
-        PT(1);
         static_for<KT>([&](auto ktc) {
             constexpr int kt = decltype(ktc)::value;
             constexpr bool more = kt + 1 < KT;
@@ -446,7 +429,6 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
             });
             lgkm_wait<0>();  // this k-tile's staging writes (asm, not tracked by the compiler)
             __syncthreads();
-            PT(2 + kt);
         });
 
         // Epilogue: each wave stages its 32*JN output rows in LDS, row-major
@@ -501,16 +483,7 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
         body(std::integral_constant<int, 1>{});
     else
         body(std::integral_constant<int, 2>{});
-    PT(13);
-    PTV(12, __builtin_amdgcn_s_memrealtime());
 }
-#ifdef UOCR_PTRACE
-}  // namespace uocr_hip
-extern "C" int uocr_hip_debug_ptrace(void* dst, size_t bytes) {
-    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(uocr_hip::g_ptrace), bytes, 0, hipMemcpyDeviceToHost);
-}
-namespace uocr_hip {
-#endif
 
 template <int GPT, bool GU>
 static bool launch_big(const ExpertArgs& a, int max_tiles, hipStream_t st) {

@@ -111,7 +111,8 @@ constexpr int kFusedMaxSeq = 16;
 constexpr int kFusedMaxGrid = 4096;
 struct FusedSync {
     int progress[kFusedMaxGrid];
-    int error;  // a bounded wait timed out (sticky)
+    int error;  // sticky: bit 0 a bounded wait timed out, bit 1 an exact pick outside the candidates
+    unsigned call_fault;  // routing tag of the last call with a timed-out wait
     // candidate experts of token t (a superset of its top_k, known before the
     // exact routing) as (tag << 32) | mask half, experts 0..31 at 2t and 32..63
     // at 2t + 1; tag = (base >> 12) + 1 (24 bits): a reader validates each word
@@ -142,7 +143,6 @@ struct DecodeArgs {
     const uint16_t* down_s;
     long long gu_wstride, gu_sstride, dn_wstride, dn_sstride;
     FusedSync* sync;           // fused kernel only
-    int dense_dn;              // fused kernel: down over every group and token as well (testing)
     f16* act;                  // [slots, inter]; fused: [(E + n_virtual) * seq, inter]
     float* y;                  // [slots, hidden]
     float* out;                // [seq, hidden]
@@ -168,6 +168,9 @@ inline bool prefill_big_ok(int hidden, int inter) {
 hipError_t launch_router_from_logits(const RouterArgs& a, const float* logits, hipStream_t st);
 hipError_t launch_group(const GroupArgs& g, hipStream_t st);
 int group_chunks(int seq, int top_k);  // 1024-entry chunks of the multi-workgroup grouping
+constexpr size_t kGroupScanLds = 96 * 1024;  // per-(chunk, expert) counts of the grouping scan
+bool group_fits(int seq, int top_k, int n_experts);  // the grouping scan's LDS holds seq * top_k entries
+hipError_t router_overflow_read(int clear, int* flag);  // sticky count > cap flag of the router mirror
 hipError_t launch_experts_prefill(const ExpertArgs& a, bool gate_up, int max_tiles, hipStream_t st);
 hipError_t launch_combine(const CombineArgs& c, hipStream_t st);
 

@@ -22,6 +22,12 @@
 
 namespace uocr_hip {
 
+// Sticky flag of the moe_router_topk mirror: set when an expert received more
+// entries than the [n_experts, cap] tables hold (the reference drops them
+// silently, src/kernels/cuda/moe_device.cu:90-95). Written with vector atomics,
+// read and cleared by router_overflow_read.
+__device__ int g_router_overflow;
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
@@ -224,7 +230,10 @@ __device__ void group_body(const int* ids, const float* wts, const GroupArgs& g,
         __syncthreads();
     }
     if (g.assign_count)
-        for (int e = tid; e < E; e += kGroupThreads) g.assign_count[e] = min(s.hist[e], g.cap);
+        for (int e = tid; e < E; e += kGroupThreads) {
+            g.assign_count[e] = min(s.hist[e], g.cap);
+            if (s.hist[e] > g.cap) atomicOr(&g_router_overflow, 1);
+        }
     if (g.slot_tok) {
         for (int v = 0; v < g.n_virtual; ++v)
             for (int t = tid; t < g.seq; t += kGroupThreads) {
@@ -314,7 +323,10 @@ __global__ __launch_bounds__(kGroupThreads) void group_scan_kernel(GroupArgs g, 
             g.counts[e] = hist[e];
             g.offsets[e] = offs[e];
         }
-        if (g.assign_count && e < E) g.assign_count[e] = min(hist[e], g.cap);
+        if (g.assign_count && e < E) {
+            g.assign_count[e] = min(hist[e], g.cap);
+            if (hist[e] > g.cap) atomicOr(&g_router_overflow, 1);
+        }
     }
     if (tid == 0 && g.counts) g.offsets[Ev] = offs[Ev];
     if (g.tile_e) write_tile_list(g, hist, offs, tile0, short0, Ev);
@@ -609,6 +621,17 @@ hipError_t launch_router_from_logits(const RouterArgs& a, const float* logits, h
 
 int group_chunks(int seq, int top_k) { return (seq * top_k + kGroupThreads - 1) / kGroupThreads; }
 
+bool group_fits(int seq, int top_k, int n_experts) {
+    return (size_t)group_chunks(seq, top_k) * n_experts * sizeof(int) <= kGroupScanLds;
+}
+
+hipError_t router_overflow_read(int clear, int* flag) {
+    hipError_t e = hipMemcpyFromSymbol(flag, HIP_SYMBOL(g_router_overflow), sizeof(int), 0, hipMemcpyDeviceToHost);
+    if (e != hipSuccess || !clear) return e;
+    const int zero = 0;
+    return hipMemcpyToSymbol(HIP_SYMBOL(g_router_overflow), &zero, sizeof(int), 0, hipMemcpyHostToDevice);
+}
+
 hipError_t launch_group(const GroupArgs& g, hipStream_t st) {
     const int n_chunks = group_chunks(g.seq, g.top_k);
     // one workgroup for a single 1024-entry round (or without the multi-kernel
@@ -618,11 +641,12 @@ hipError_t launch_group(const GroupArgs& g, hipStream_t st) {
         return hipGetLastError();
     }
     if (g.slot_tok && g.assign_token) return hipErrorInvalidValue;  // bases are slots or positions, not both
-    launch_k(group_rank_kernel, dim3(n_chunks), dim3(kGroupThreads), 0, st, g);
+    // checked before the first launch, so an oversized call enqueues nothing
     const size_t lds = (size_t)n_chunks * g.n_experts * sizeof(int);
-    if (lds > 96 * 1024) return hipErrorInvalidValue;
+    if (lds > kGroupScanLds) return hipErrorInvalidValue;
+    launch_k(group_rank_kernel, dim3(n_chunks), dim3(kGroupThreads), 0, st, g);
     static hipError_t attr = hipFuncSetAttribute((const void*)group_scan_kernel,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, kGroupScanLds);
     if (attr != hipSuccess) return attr;
     launch_k(group_scan_kernel, dim3(1), dim3(kGroupThreads), lds, st, g, n_chunks);
     const int n = g.seq * g.top_k;

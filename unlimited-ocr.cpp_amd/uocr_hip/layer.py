@@ -88,6 +88,13 @@ class MoELayerInt4:
         check(self.lib.uocr_hip_moe_layer_status(self.handle, 1 if clear else 0, C.byref(flags)))
         return flags.value
 
+    def status_async(self, d_flags, stream=None):
+        """Copy the same flags into the device int32 tensor `d_flags`,
+        stream-ordered, without waiting for the device."""
+        import torch
+        st = stream if stream is not None else torch.cuda.current_stream().cuda_stream
+        check(self.lib.uocr_hip_moe_layer_status_async(self.handle, d_flags.data_ptr(), st))
+
     def alloc_workspace(self, seq, device="cuda"):
         import torch
         n = self.workspace_size(seq)

@@ -15,3 +15,11 @@ def moe_router_topk(logits, top_k, norm_topk_prob, routed_scaling_factor, scorin
         logits.data_ptr(), seq, n_experts, top_k, int(norm_topk_prob), float(routed_scaling_factor),
         int(scoring_sigmoid), ids.data_ptr(), weights.data_ptr(), assign_token.data_ptr(),
         assign_w.data_ptr(), count.data_ptr(), cap, _stream(stream)))
+
+
+def moe_router_overflow(clear=True):
+    """Sticky count > cap flag of moe_router_topk (synchronises the device)."""
+    import ctypes as C
+    f = C.c_int(0)
+    check(load().uocr_hip_moe_router_overflow(1 if clear else 0, C.byref(f)))
+    return f.value
