@@ -61,3 +61,22 @@ def test_no_cpu_fallback_in_product_sources():
             if f.endswith((".hip", ".hpp", ".h", ".py", ".cpp", ".c")):
                 text = open(os.path.join(dirpath, f), errors="ignore").read()
                 assert "liboracle" not in text and "import oracle" not in text, f
+
+
+def test_upload_rejects_non_integer_zero_points():
+    """Zeros must be integers in [0, 15] (what quantize_int4_awq and the GPTQ
+    files produce); anything else is refused at upload, before any device call."""
+    import numpy as np
+    from uocr_hip import MoELayerInt4, synth
+    from uocr_hip._lib import HipError
+
+    L = synth.random_layer(5, hidden=256, inter=128, n_experts=4, top_k=2, n_shared=0, group=32)
+    L.up[2].zeros = L.up[2].zeros.copy()
+    L.up[2].zeros[3, 1] = 7.5
+    with pytest.raises(HipError) as ei:
+        MoELayerInt4(L)
+    assert ei.value.code == _lib.EUNSUPPORTED and "integers in [0, 15]" in str(ei.value)
+    L.up[2].zeros[3, 1] = 16.0
+    with pytest.raises(HipError) as ei:
+        MoELayerInt4(L)
+    assert ei.value.code == _lib.EUNSUPPORTED

@@ -239,3 +239,41 @@ def test_no_shared_experts(dev, seq):
     L = synth.random_layer(800 + seq, n_experts=8, top_k=2, n_shared=0, group=32)
     x = synth.bf16_normal(np.random.default_rng(seq), (seq, L.hidden), 1.0)
     check_parity(L, x, dev, sample=24 if seq > 64 else None, label=f"noshared-t{seq}")
+
+
+@pytest.mark.parametrize("group", [32, 128])
+@pytest.mark.parametrize("seq,dtype", [(5, "bf16"), (16, "bf16"), (16, "f32"), (300, "bf16")])
+def test_awq_asymmetric_weights(dev, group, seq, dtype):
+    """Weights from the reference's quantize_int4_awq (zeros 0..15, arbitrary f32
+    scales) on every path: decode (5; 16 f32), single-kernel (16 bf16) and
+    prefill (300). Scales are rounded to f16 on upload (relative error
+    <= 2^-11 per scale)."""
+    from helpers import awq_layer
+    from uocr_hip import synth
+    L = awq_layer(1000 + group + seq, group=group)
+    zs = np.concatenate([q.zeros.ravel() for q in L.gate[:2]])
+    assert zs.min() == 0 and zs.max() == 15 and (zs != 8).mean() > 0.5
+    x = synth.bf16_normal(np.random.default_rng(seq), (seq, L.hidden), 1.0)
+    check_parity(L, x, dev, sample=32 if seq > 64 else None, dtype=dtype, label=f"awq-g{group}-t{seq}-{dtype}")
+
+
+def test_awq_config4_form(dev):
+    """AWQ weights in config 4's layer form (RMSNorm prologue + residual, f32 h)."""
+    from helpers import awq_layer
+    from uocr_hip import synth
+    L = awq_layer(1999, group=32)
+    L.rms_weight = np.random.default_rng(3).uniform(0.5, 2.0, L.hidden).astype(np.float32)
+    x = synth.bf16_normal(np.random.default_rng(4), (64, L.hidden), 1.0)
+    check_parity(L, x, dev, dtype="f32", label="awq-rms-t64")
+
+
+@pytest.mark.parametrize("seq", [16, 300])
+def test_symmetric_quantizer_f32_scales(dev, seq):
+    """quantize_int4_symmetric output (zero 8, arbitrary f32 scales amax / 7):
+    the implicit-zero layout with scales that are not bf16-valued."""
+    from helpers import awq_layer
+    from uocr_hip import synth
+    L = awq_layer(2100 + seq, group=32, quantizer="sym")
+    assert all((q.zeros == 8).all() for q in L.down[:3])
+    x = synth.bf16_normal(np.random.default_rng(seq), (seq, L.hidden), 1.0)
+    check_parity(L, x, dev, sample=32 if seq > 64 else None, label=f"sym-f32scale-t{seq}")

@@ -43,33 +43,44 @@ int hip_fail(hipError_t e, const char* what) {
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-uint16_t f32_to_bf16_rne(float f) {
-    uint32_t b;
-    std::memcpy(&b, &f, 4);
-    b = (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
-    return (uint16_t)b;
-}
-
-// Device scale: the reference scale rounded to bf16 (the BASELINE scale format),
-// then stored as the equal f16 value (exact for normal f16; tiny scales round
-// into the f16 subnormal range, an absolute error below 3e-8).
-uint16_t scale_to_device(float s) {
-    const uint16_t b = f32_to_bf16_rne(s);
-    uint32_t bits = (uint32_t)b << 16;
-    float f;
-    std::memcpy(&f, &bits, 4);
-    const _Float16 h = (_Float16)f;
+uint16_t f16_bits(float f) {
+    const _Float16 h = (_Float16)f;  // round to nearest even
     uint16_t out;
     std::memcpy(&out, &h, 2);
     return out;
 }
 
+// Zero points of a reference INT4 matrix: true if every zero equals 8 (the
+// symmetric layout, stored implicitly); otherwise every zero must be an
+// integer in [0, 15] (what quantize_int4_awq and the GPTQ files hold,
+// src/runtime/quant.cpp:60-64, tools/reference/quantize_gptq.py:161).
+int zero_kind(const uocr_hip_qmatrix& q, int row0, int R, bool* symmetric, std::string* err) {
+    const int ng = (q.cols + q.group_size - 1) / q.group_size;
+    bool sym = true;
+    for (int r = row0; r < row0 + R; ++r)
+        for (int g = 0; g < ng; ++g) {
+            const float z = q.zeros[(size_t)r * ng + g];
+            if (z == 8.0f) continue;
+            sym = false;
+            if (!(z >= 0.0f && z <= 15.0f) || z != std::floor(z)) {
+                *err = "zero point " + std::to_string(z) + " at row " + std::to_string(r) + " group " +
+                       std::to_string(g) + ": zeros must be integers in [0, 15]";
+                return UOCR_HIP_EUNSUPPORTED;
+            }
+        }
+    *symmetric = sym;
+    return UOCR_HIP_OK;
+}
+
 // Repack rows [row0, row0 + R) x columns [col0, col0 + K) of a reference-layout
-// INT4 matrix into the tile-16x128 device layout (common.hpp).
-int repack(const uocr_hip_qmatrix& q, int row0, int R, int col0, int K, uint8_t* dst,
-           uint16_t* dsts, std::string* err) {
+// INT4 matrix into the tile-16x128 device layout (common.hpp): nibbles,
+// f16 scales and, if dstz is non-null, f16 zero offsets -(1024 + zero).
+int repack(const uocr_hip_qmatrix& q, int row0, int R, int col0, int K, uint8_t* dst, uint16_t* dsts,
+           uint16_t* dstz, std::string* err) {
     const int G = q.group_size, gpt = kTileK / G, KT = K / kTileK, RB = R / kTileRows;
     const int pr = (q.cols + 1) / 2, ng = (q.cols + G - 1) / G;
+    // the largest |q - zero| the kernels form in f16 before scaling
+    const float qmax = dstz ? 15.0f : 8.0f;
     for (int rb = 0; rb < RB; ++rb)
         for (int kt = 0; kt < KT; ++kt) {
             uint8_t* tile = dst + ((size_t)rb * KT + kt) * kTileBytes;
@@ -93,18 +104,14 @@ int repack(const uocr_hip_qmatrix& q, int row0, int R, int col0, int K, uint8_t*
                     const int g = (col0 + kt * kTileK) / G + gi;
                     const int gl = kt * gpt + gi;  // group index within the slice
                     const size_t idx = (size_t)r * ng + g;
-                    const float z = q.zeros[idx], s = q.scales[idx];
-                    if (z != 8.0f) {
-                        *err = "zero point " + std::to_string(z) + " at row " + std::to_string(r) +
-                               " group " + std::to_string(g) +
-                               ": only the symmetric layout (zeros == 8) is supported";
-                        return UOCR_HIP_EUNSUPPORTED;
-                    }
-                    if (!std::isfinite(s) || std::fabs(s) * 8.0f > 65504.0f) {
+                    const float s = q.scales[idx];
+                    if (!std::isfinite(s) || std::fabs(s) * qmax > 65504.0f) {
                         *err = "scale outside the f16 range at row " + std::to_string(r);
                         return UOCR_HIP_EUNSUPPORTED;
                     }
-                    dsts[((size_t)rb * kTileRows + rr) * scale_row_stride(K, G) + gl] = scale_to_device(s);
+                    const size_t o = ((size_t)rb * kTileRows + rr) * scale_row_stride(K, G) + gl;
+                    dsts[o] = f16_bits(s);
+                    if (dstz) dstz[o] = f16_bits(-(1024.0f + q.zeros[idx]));
                 }
             }
         }
@@ -129,6 +136,9 @@ struct uocr_hip_moe_layer {
     uint16_t* gate_s = nullptr;
     uint16_t* up_s = nullptr;
     uint16_t* down_s = nullptr;
+    uint16_t* gate_z = nullptr;  // zero offsets (null: symmetric layer, zero 8 implicit)
+    uint16_t* up_z = nullptr;
+    uint16_t* down_z = nullptr;
     long long gu_wstride = 0, gu_sstride = 0, dn_wstride = 0, dn_sstride = 0;
     size_t device_bytes = 0;
     bool timing = false;
@@ -144,8 +154,8 @@ namespace {
 
 void free_layer(uocr_hip_moe_layer* L) {
     if (!L) return;
-    void* ptrs[] = {L->router_t, L->router_f32, L->rms_weight, L->gate,  L->up,
-                    L->down,     L->gate_s,     L->up_s,       L->down_s, L->sync};
+    void* ptrs[] = {L->router_t, L->router_f32, L->rms_weight, L->gate,   L->up,   L->down, L->gate_s,
+                    L->up_s,     L->down_s,     L->gate_z,     L->up_z,   L->down_z, L->sync};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     for (auto& e : L->ev)
@@ -291,24 +301,51 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
     L->gu_sstride = (long long)I * scale_row_stride(H, G);
     L->dn_wstride = (long long)H * I / 2;
     L->dn_sstride = (long long)H * scale_row_stride(I, G);
+
+    // zero points: one layout for the whole layer (implicit 8 unless any matrix
+    // holds another zero)
+    bool sym = true;
+    {
+        std::string err;
+        auto scan = [&](const uocr_hip_qmatrix& q, const char* what) -> int {
+            bool s1 = true;
+            const int c = zero_kind(q, 0, q.rows, &s1, &err);
+            if (c) return fail(c, std::string(what) + ": " + err);
+            sym = sym && s1;
+            return UOCR_HIP_OK;
+        };
+        for (int e = 0; e < E; ++e)
+            if ((rc = scan(d->gate[e], "gate")) || (rc = scan(d->up[e], "up")) || (rc = scan(d->down[e], "down"))) {
+                delete L;
+                return rc;
+            }
+        if (S > 0 && ((rc = scan(*d->shared_gate, "shared_gate")) || (rc = scan(*d->shared_up, "shared_up")) ||
+                      (rc = scan(*d->shared_down, "shared_down")))) {
+            delete L;
+            return rc;
+        }
+    }
     std::vector<uint8_t> hg((size_t)Ev * L->gu_wstride), hu(hg.size()), hd((size_t)Ev * L->dn_wstride);
     std::vector<uint16_t> hgs((size_t)Ev * L->gu_sstride), hus(hgs.size()), hds((size_t)Ev * L->dn_sstride);
+    std::vector<uint16_t> hgz(sym ? 0 : hgs.size()), huz(hgz.size()), hdz(sym ? 0 : hds.size());
+    auto zp = [&](std::vector<uint16_t>& v, long long off) -> uint16_t* { return v.empty() ? nullptr : &v[off]; };
 
     // repack experts in parallel (virtual experts E..E+S-1 are slices of the shared MLP)
     std::vector<int> codes(Ev, UOCR_HIP_OK);
     std::vector<std::string> errs(Ev);
     auto work = [&](int e) {
         std::string* err = &errs[e];
+        const long long gw = e * L->gu_wstride, gs = e * L->gu_sstride, dw = e * L->dn_wstride, ds = e * L->dn_sstride;
         int c;
         if (e < E) {
-            if ((c = repack(d->gate[e], 0, I, 0, H, &hg[e * L->gu_wstride], &hgs[e * L->gu_sstride], err))) goto done;
-            if ((c = repack(d->up[e], 0, I, 0, H, &hu[e * L->gu_wstride], &hus[e * L->gu_sstride], err))) goto done;
-            c = repack(d->down[e], 0, H, 0, I, &hd[e * L->dn_wstride], &hds[e * L->dn_sstride], err);
+            if ((c = repack(d->gate[e], 0, I, 0, H, &hg[gw], &hgs[gs], zp(hgz, gs), err))) goto done;
+            if ((c = repack(d->up[e], 0, I, 0, H, &hu[gw], &hus[gs], zp(huz, gs), err))) goto done;
+            c = repack(d->down[e], 0, H, 0, I, &hd[dw], &hds[ds], zp(hdz, ds), err);
         } else {
             const int v = e - E;
-            if ((c = repack(*d->shared_gate, v * I, I, 0, H, &hg[e * L->gu_wstride], &hgs[e * L->gu_sstride], err))) goto done;
-            if ((c = repack(*d->shared_up, v * I, I, 0, H, &hu[e * L->gu_wstride], &hus[e * L->gu_sstride], err))) goto done;
-            c = repack(*d->shared_down, 0, H, v * I, I, &hd[e * L->dn_wstride], &hds[e * L->dn_sstride], err);
+            if ((c = repack(*d->shared_gate, v * I, I, 0, H, &hg[gw], &hgs[gs], zp(hgz, gs), err))) goto done;
+            if ((c = repack(*d->shared_up, v * I, I, 0, H, &hu[gw], &hus[gs], zp(huz, gs), err))) goto done;
+            c = repack(*d->shared_down, 0, H, v * I, I, &hd[dw], &hds[ds], zp(hdz, ds), err);
         }
     done:
         codes[e] = c;
@@ -361,6 +398,9 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
         (rc = up_copy((void**)&L->gate_s, hgs.data(), hgs.size() * 2, "gate scales")) ||
         (rc = up_copy((void**)&L->up_s, hus.data(), hus.size() * 2, "up scales")) ||
         (rc = up_copy((void**)&L->down_s, hds.data(), hds.size() * 2, "down scales")) ||
+        (!sym && (rc = up_copy((void**)&L->gate_z, hgz.data(), hgz.size() * 2, "gate zeros"))) ||
+        (!sym && (rc = up_copy((void**)&L->up_z, huz.data(), huz.size() * 2, "up zeros"))) ||
+        (!sym && (rc = up_copy((void**)&L->down_z, hdz.data(), hdz.size() * 2, "down zeros"))) ||
         (d->rms_weight && (rc = up_copy((void**)&L->rms_weight, d->rms_weight, (size_t)H * 4, "rms weight")))) {
         free_layer(L);
         return rc;
@@ -484,6 +524,9 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
         da.gate_s = L->gate_s;
         da.up_s = L->up_s;
         da.down_s = L->down_s;
+        da.gate_z = L->gate_z;
+        da.up_z = L->up_z;
+        da.down_z = L->down_z;
         da.gu_wstride = L->gu_wstride;
         da.gu_sstride = L->gu_sstride;
         da.dn_wstride = L->dn_wstride;
@@ -577,6 +620,8 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     gu.s0 = L->gate_s;
     gu.w1 = L->up;
     gu.s1 = L->up_s;
+    gu.z0 = L->gate_z;
+    gu.z1 = L->up_z;
     gu.w_stride = L->gu_wstride;
     gu.s_stride = L->gu_sstride;
     gu.n_rows = L->inter;
@@ -602,6 +647,8 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     dn.s0 = L->down_s;
     dn.w1 = nullptr;
     dn.s1 = nullptr;
+    dn.z0 = L->down_z;
+    dn.z1 = nullptr;
     dn.w_stride = L->dn_wstride;
     dn.s_stride = L->dn_sstride;
     dn.n_rows = L->hidden;

@@ -33,12 +33,17 @@ constexpr int kWave = 64;
 // integer ulp), ready for the v_mfma_f32_16x16x32_f16 B operand, and one
 // 1 KiB tile is one fully coalesced wave load.
 //
-// Scales: one per (row, group), stored as f16 (the bf16-valued reference
-// scales convert exactly whenever they are normal f16 numbers), row-major
+// Scales: one per (row, group), the reference's f32 scale rounded to f16
+// (exact for bf16-valued scales that are normal f16 numbers), row-major
 // [rows][scale_row_stride(K, group)] (K / group rounded up to 8, so every row
 // starts 16-byte aligned and a lane fetches all scales of its row with whole
-// 16-byte loads); the zero point is the implicit 8 of the reference's
-// symmetric layout (src/runtime/quant.cpp:82-116).
+// 16-byte loads).
+// Zero points: a layer whose zeros are all 8 (quantize_int4_symmetric,
+// src/runtime/quant.cpp:82-116) stores none -- 8 is implicit. Any other layer
+// (quantize_int4_awq, src/runtime/quant.cpp:39-80, and the GPTQ files, whose
+// zeros are integers in [0, 15]) stores one f16 per (row, group) in the scale
+// layout, holding -(1024 + zero): the offset that turns the biased nibble
+// 1024 + q into q - zero exactly (see dequant8z).
 // ---------------------------------------------------------------------------
 __host__ __device__ constexpr int scale_row_stride(int k, int group) { return ((k / group) + 7) / 8 * 8; }
 
@@ -70,6 +75,41 @@ __device__ __forceinline__ f16x8 dequant8(uint32_t w, f16x2 s2) {
     const f16x2 h1 = (as_h2(__builtin_amdgcn_bitop3_b32(w, 0x00F000F0u, 0x54005400u, 0xEA)) + off1) * s2;
     const f16x2 h2 = (as_h2(__builtin_amdgcn_bitop3_b32(w8, 0x000F000Fu, 0x64006400u, 0xEA)) + off0) * s2;
     const f16x2 h3 = (as_h2(__builtin_amdgcn_bitop3_b32(w8, 0x00F000F0u, 0x54005400u, 0xEA)) + off1) * s2;
+    f16x8 r;
+    r[0] = h0[0]; r[1] = h0[1]; r[2] = h1[0]; r[3] = h1[1];
+    r[4] = h2[0]; r[5] = h2[1]; r[6] = h3[0]; r[7] = h3[1];
+    return r;
+}
+
+// Eight nibbles -> f16x8 of (q - zero) * scale for a stored zero offset
+// zo = -(1024 + zero) (an integer zero in [0, 15]): the biased values 1024 + q
+// and 64 + q of dequant8 plus zo and zo + 960 give q - zero exactly; the
+// product with the f16 scale rounds once (to f16) unless it is exact.
+__device__ __forceinline__ f16x8 dequant8z(uint32_t w, f16x2 s2, f16 zo) {
+    const f16x2 off0 = {zo, zo};
+    const f16 zo1 = zo + (f16)960.0f;
+    const f16x2 off1 = {zo1, zo1};
+    const uint32_t w8 = w >> 8;
+    const f16x2 h0 = (as_h2(__builtin_amdgcn_bitop3_b32(w, 0x000F000Fu, 0x64006400u, 0xEA)) + off0) * s2;
+    const f16x2 h1 = (as_h2(__builtin_amdgcn_bitop3_b32(w, 0x00F000F0u, 0x54005400u, 0xEA)) + off1) * s2;
+    const f16x2 h2 = (as_h2(__builtin_amdgcn_bitop3_b32(w8, 0x000F000Fu, 0x64006400u, 0xEA)) + off0) * s2;
+    const f16x2 h3 = (as_h2(__builtin_amdgcn_bitop3_b32(w8, 0x00F000F0u, 0x54005400u, 0xEA)) + off1) * s2;
+    f16x8 r;
+    r[0] = h0[0]; r[1] = h0[1]; r[2] = h1[0]; r[3] = h1[1];
+    r[4] = h2[0]; r[5] = h2[1]; r[6] = h3[0]; r[7] = h3[1];
+    return r;
+}
+
+// Eight nibbles -> f16x8 of the exact integers q - zero (zo as in dequant8z),
+// the scale left to the caller.
+__device__ __forceinline__ f16x8 dequant8z_unscaled(uint32_t w, f16 zo) {
+    const f16 zo1 = zo + (f16)960.0f;
+    const f16x2 off0 = {zo, zo}, off1 = {zo1, zo1};
+    const uint32_t w8 = w >> 8;
+    const f16x2 h0 = as_h2(__builtin_amdgcn_bitop3_b32(w, 0x000F000Fu, 0x64006400u, 0xEA)) + off0;
+    const f16x2 h1 = as_h2(__builtin_amdgcn_bitop3_b32(w, 0x00F000F0u, 0x54005400u, 0xEA)) + off1;
+    const f16x2 h2 = as_h2(__builtin_amdgcn_bitop3_b32(w8, 0x000F000Fu, 0x64006400u, 0xEA)) + off0;
+    const f16x2 h3 = as_h2(__builtin_amdgcn_bitop3_b32(w8, 0x00F000F0u, 0x54005400u, 0xEA)) + off1;
     f16x8 r;
     r[0] = h0[0]; r[1] = h0[1]; r[2] = h1[0]; r[3] = h1[1];
     r[4] = h2[0]; r[5] = h2[1]; r[6] = h3[0]; r[7] = h3[1];

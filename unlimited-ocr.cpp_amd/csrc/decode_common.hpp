@@ -84,7 +84,8 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 
 // LDS operands of one k-tile: four A fragments (1 KiB apart) and the scale
 // words of one or two scale rows (the GPT groups of the k-tile; MFMA step s
-// uses group (s * GPT) / 4). lds_issue_tile only issues the six reads (the
+// uses group (s * GPT) / 4), plus, with ZP, the zero-offset words of the same
+// rows ZOFF bytes after the scales. lds_issue_tile only issues the reads (the
 // registers must not be used before lds_wait_tile); reading through asm keeps
 // the compiler's LDS-DMA tracking from turning the first read into a wait for
 // every outstanding global load.
@@ -92,10 +93,14 @@ template <int GPT>
 struct TileRegs {
     f16x8 av[4];
     // GPT 4: four scales in 64 bits; GPT 2 / 1: two / one in 32 bits
-    typename std::conditional<GPT == 4, uint64_t, uint32_t>::type w0, w1;
+    typedef typename std::conditional<GPT == 4, uint64_t, uint32_t>::type SW;
+    SW w0, w1, z0, z1;
 };
+// LDS reads lds_issue_tile issues
+template <bool ZP>
+constexpr int tile_reads() { return ZP ? 8 : 6; }
 
-template <int GPT>
+template <int GPT, bool ZP = false, int ZOFF = 0>
 __device__ __forceinline__ void lds_issue_tile(uint32_t a_addr, uint32_t s0_addr, uint32_t s1_addr, TileRegs<GPT>& t) {
 #define UOCR_TILE_READS(SREAD)                                                                        \
     asm volatile("ds_read_b128 %0, %6\n"                                                             \
@@ -105,24 +110,27 @@ __device__ __forceinline__ void lds_issue_tile(uint32_t a_addr, uint32_t s0_addr
                  : "=&v"(t.av[0]), "=&v"(t.av[1]), "=&v"(t.av[2]), "=&v"(t.av[3]), "=&v"(t.w0), "=&v"(t.w1) \
                  : "v"(a_addr), "v"(s0_addr), "v"(s1_addr)                                          \
                  : "memory")
+#define UOCR_ZERO_READS(SREAD)                                                                        \
+    asm volatile(SREAD " %0, %2 offset:%4\n" SREAD " %1, %3 offset:%4\n"                              \
+                 : "=&v"(t.z0), "=&v"(t.z1)                                                         \
+                 : "v"(s0_addr), "v"(s1_addr), "n"(ZOFF)                                            \
+                 : "memory")
     if constexpr (GPT == 4) {
         UOCR_TILE_READS("ds_read_b64");
+        if constexpr (ZP) UOCR_ZERO_READS("ds_read_b64");
     } else if constexpr (GPT == 2) {
         UOCR_TILE_READS("ds_read_b32");
+        if constexpr (ZP) UOCR_ZERO_READS("ds_read_b32");
     } else {
         UOCR_TILE_READS("ds_read_u16");
+        if constexpr (ZP) UOCR_ZERO_READS("ds_read_u16");
     }
 #undef UOCR_TILE_READS
+#undef UOCR_ZERO_READS
 }
 
-// Wait until at most `later` LDS reads (issued after this tile's) are
-// outstanding, then unpack the scales.
-template <int GPT, int LATER>
-__device__ __forceinline__ void lds_wait_tile(TileRegs<GPT>& t, f16* s0, f16* s1) {
-    asm volatile("s_waitcnt lgkmcnt(%6)"
-                 : "+v"(t.av[0]), "+v"(t.av[1]), "+v"(t.av[2]), "+v"(t.av[3]), "+v"(t.w0), "+v"(t.w1)
-                 : "n"(LATER));
-    const uint64_t x0 = t.w0, x1 = t.w1;
+template <int GPT>
+__device__ __forceinline__ void unpack_tile_words(uint64_t x0, uint64_t x1, f16* s0, f16* s1) {
     const uint32_t w0[2] = {(uint32_t)x0, (uint32_t)(x0 >> 32)};
     const uint32_t w1[2] = {(uint32_t)x1, (uint32_t)(x1 >> 32)};
 #pragma unroll
@@ -131,6 +139,25 @@ __device__ __forceinline__ void lds_wait_tile(TileRegs<GPT>& t, f16* s0, f16* s1
         s0[s] = __builtin_bit_cast(f16, (uint16_t)((w0[gi >> 1] >> (16 * (gi & 1))) & 0xffffu));
         s1[s] = __builtin_bit_cast(f16, (uint16_t)((w1[gi >> 1] >> (16 * (gi & 1))) & 0xffffu));
     }
+}
+
+// Wait until at most `later` LDS reads (issued after this tile's) are
+// outstanding, then unpack the scales (and, with ZP, the zero offsets).
+template <int GPT, int LATER, bool ZP = false>
+__device__ __forceinline__ void lds_wait_tile(TileRegs<GPT>& t, f16* s0, f16* s1, f16* z0 = nullptr,
+                                              f16* z1 = nullptr) {
+    if constexpr (ZP) {
+        asm volatile("s_waitcnt lgkmcnt(%8)"
+                     : "+v"(t.av[0]), "+v"(t.av[1]), "+v"(t.av[2]), "+v"(t.av[3]), "+v"(t.w0), "+v"(t.w1), "+v"(t.z0),
+                       "+v"(t.z1)
+                     : "n"(LATER));
+        unpack_tile_words<GPT>(t.z0, t.z1, z0, z1);
+    } else {
+        asm volatile("s_waitcnt lgkmcnt(%6)"
+                     : "+v"(t.av[0]), "+v"(t.av[1]), "+v"(t.av[2]), "+v"(t.av[3]), "+v"(t.w0), "+v"(t.w1)
+                     : "n"(LATER));
+    }
+    unpack_tile_words<GPT>(t.w0, t.w1, s0, s1);
 }
 
 // Workgroup barrier that orders LDS only: __syncthreads() would also wait for
@@ -194,44 +221,60 @@ __device__ __forceinline__ void lds_issue_seeds(uint32_t c_addr, f32x4 (&c)[GPT]
 }
 
 // One wave's 16 rows x KT k-tiles (two weight tiles sharing the A rows, or
-// one: TWO = false)
-// against the staged A rows. Per scale group the MFMAs run on the biased
-// nibbles from the group's bias seed, then the group result is scaled into
-// the accumulator (f16 scale x f32, one fma per element). LDS operands are read
-// one k-tile ahead (asm reads, explicit lgkmcnt waits).
-template <int GPT, int KT, bool TWO = true>
+// one: TWO = false) against the staged A rows. Per scale group the MFMAs run
+// on the biased nibbles from the group's bias seed (ZP: on the exact integers
+// q - zero from a zero seed), then the group result is scaled into the
+// accumulator (f16 scale x f32, one fma per element). LDS operands are read
+// one k-tile ahead (asm reads, explicit lgkmcnt waits). ZOFF: bytes from a
+// scale row to its zero-offset row.
+template <int GPT, int KT, bool TWO = true, bool ZP = false, int ZOFF = 0>
 __device__ __forceinline__ void item_mma(const u32x4 (&bw0)[KT], const u32x4 (&bw1)[KT], uint32_t a_base,
                                          uint32_t s_base0, uint32_t s_base1, uint32_t c_base, f32x4& acc0,
                                          f32x4& acc1) {
+    constexpr int NSEED = ZP ? 0 : GPT;  // seed reads per k-tile
     TileRegs<GPT> tr[2];
     f32x4 cr[2][GPT];
-    lds_issue_tile<GPT>(a_base, s_base0, s_base1, tr[0]);
-    lds_issue_seeds<GPT>(c_base, cr[0]);
+    lds_issue_tile<GPT, ZP, ZOFF>(a_base, s_base0, s_base1, tr[0]);
+    if constexpr (!ZP) lds_issue_seeds<GPT>(c_base, cr[0]);
     // the previous group's results, scaled in after the next group's MFMAs
     // are issued (the MFMA latency is then covered)
     f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = {0.f, 0.f, 0.f, 0.f};
     float ps0 = 0.0f, ps1 = 0.0f;
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
-        f16 s0[4], s1[4];
+        f16 s0[4], s1[4], z0[4], z1[4];
         if (kt + 1 < KT) {
-            lds_issue_tile<GPT>(a_base + (uint32_t)((kt + 1) * 4096), s_base0 + (uint32_t)((kt + 1) * GPT * 2),
-                                s_base1 + (uint32_t)((kt + 1) * GPT * 2), tr[(kt + 1) & 1]);
-            lds_issue_seeds<GPT>(c_base + (uint32_t)((kt + 1) * GPT * 64), cr[(kt + 1) & 1]);
-            lds_wait_tile<GPT, 6 + GPT>(tr[kt & 1], s0, s1);
+            lds_issue_tile<GPT, ZP, ZOFF>(a_base + (uint32_t)((kt + 1) * 4096), s_base0 + (uint32_t)((kt + 1) * GPT * 2),
+                                          s_base1 + (uint32_t)((kt + 1) * GPT * 2), tr[(kt + 1) & 1]);
+            if constexpr (!ZP) lds_issue_seeds<GPT>(c_base + (uint32_t)((kt + 1) * GPT * 64), cr[(kt + 1) & 1]);
+            lds_wait_tile<GPT, tile_reads<ZP>() + NSEED, ZP>(tr[kt & 1], s0, s1, z0, z1);
         } else {
-            lds_wait_tile<GPT, 0>(tr[kt & 1], s0, s1);
+            lds_wait_tile<GPT, 0, ZP>(tr[kt & 1], s0, s1, z0, z1);
         }
+        if constexpr (!ZP) {
 #pragma unroll
-        for (int gi = 0; gi < GPT; ++gi) asm volatile("" : "+v"(cr[kt & 1][gi]));  // landed with the tile
+            for (int gi = 0; gi < GPT; ++gi) asm volatile("" : "+v"(cr[kt & 1][gi]));  // landed with the tile
+        }
         const f16x8* av = tr[kt & 1].av;
 #pragma unroll
         for (int gi = 0; gi < GPT; ++gi) {
-            f32x4 r0 = cr[kt & 1][gi], r1 = cr[kt & 1][gi];
+            f32x4 r0, r1;
+            if constexpr (ZP) {
+                r0 = f32x4{0.f, 0.f, 0.f, 0.f};
+                r1 = r0;
+            } else {
+                r0 = cr[kt & 1][gi];
+                r1 = r0;
+            }
 #pragma unroll
             for (int s = gi * 4 / GPT; s < (gi + 1) * 4 / GPT; ++s) {
-                r0 = mfma16(av[s], dequant8_biased(bw0[kt][s]), r0);
-                if constexpr (TWO) r1 = mfma16(av[s], dequant8_biased(bw1[kt][s]), r1);
+                if constexpr (ZP) {
+                    r0 = mfma16(av[s], dequant8z_unscaled(bw0[kt][s], z0[s]), r0);
+                    if constexpr (TWO) r1 = mfma16(av[s], dequant8z_unscaled(bw1[kt][s], z1[s]), r1);
+                } else {
+                    r0 = mfma16(av[s], dequant8_biased(bw0[kt][s]), r0);
+                    if constexpr (TWO) r1 = mfma16(av[s], dequant8_biased(bw1[kt][s]), r1);
+                }
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {

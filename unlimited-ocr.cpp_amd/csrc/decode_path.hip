@@ -42,13 +42,16 @@ __global__ __launch_bounds__(256) void router_decode_kernel(DecodeArgs a) {
 constexpr int kDecBM = 16;
 constexpr int kDecodeMaxEntries = 256 * kMaxTopK;  // seq < 256
 
-template <int GPT, int KT, bool GU>
+template <int GPT, int KT, bool GU, bool ZP>
 __global__ __launch_bounds__(256) void expert_decode_kernel(DecodeArgs a) {
     constexpr int K = KT * kTileK;
     constexpr int NG = scale_row_stride(K, kTileK / GPT);
     constexpr int SROW = kTileRows * NG;
+    constexpr int NM = GU ? 2 : 1;  // weight matrices per item
     __shared__ __attribute__((aligned(16))) f16 As[KT * 4 * 64 * 8];
-    __shared__ __attribute__((aligned(16))) f16 Ss[4][GU ? 2 : 1][SROW];
+    // per wave: the scale rows of its NM matrices, then (ZP) their zero-offset rows
+    __shared__ __attribute__((aligned(16))) f16 Ss[4][ZP ? 2 * NM : NM][SROW];
+    constexpr int ZOFF = NM * SROW * 2;  // bytes from a scale row to its zero-offset row
     __shared__ int ent[256];
     __shared__ int ids_s[kDecodeMaxEntries];
     __shared__ int hist[kMaxExperts], offs[kMaxExperts], live[kMaxExperts];
@@ -114,6 +117,7 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(DecodeArgs a) {
     const int r = lane & 15;
     const uint8_t* wsrc0 = GU ? a.gate : a.down;
     const uint16_t* ssrc0 = GU ? a.gate_s : a.down_s;
+    const uint16_t* zsrc0 = GU ? a.gate_z : a.down_z;
     const long long wstr = GU ? a.gu_wstride : a.dn_wstride;
     const long long sstr = GU ? a.gu_sstride : a.dn_sstride;
 
@@ -176,6 +180,10 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(DecodeArgs a) {
             for (int i = lane; i * 8 < SROW; i += 64) {
                 load_lds16(ssrc0 + sb + i * 8, &Ss[wave][0][(i & ~63) * 8]);
                 if constexpr (GU) load_lds16(a.up_s + sb + i * 8, &Ss[wave][GU ? 1 : 0][(i & ~63) * 8]);
+                if constexpr (ZP) {
+                    load_lds16(zsrc0 + sb + i * 8, &Ss[wave][NM][(i & ~63) * 8]);
+                    if constexpr (GU) load_lds16(a.up_z + sb + i * 8, &Ss[wave][NM + 1][(i & ~63) * 8]);
+                }
             }
             const size_t toff = (size_t)g * wstr + (size_t)rbl * KT * kTileBytes + (size_t)lane * 16;
 #pragma unroll
@@ -196,24 +204,30 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(DecodeArgs a) {
             const uint32_t a_base = lds_addr(As + (size_t)lane * 8);
             const uint32_t s_base0 = lds_addr(srow0), s_base1 = lds_addr(srow1);
             TileRegs<GPT> tr[2];
-            lds_issue_tile<GPT>(a_base, s_base0, s_base1, tr[0]);
+            lds_issue_tile<GPT, ZP, ZOFF>(a_base, s_base0, s_base1, tr[0]);
 #pragma unroll
             for (int kt = 0; kt < KT; ++kt) {
-                f16 s0[4], s1[4];
+                f16 s0[4], s1[4], z0[4], z1[4];
                 // this k-tile's LDS operands were issued one k-tile ahead; issue
                 // the next k-tile's before waiting for these
                 if (kt + 1 < KT) {
-                    lds_issue_tile<GPT>(a_base + (uint32_t)((kt + 1) * 4096), s_base0 + (uint32_t)((kt + 1) * GPT * 2),
-                                        s_base1 + (uint32_t)((kt + 1) * GPT * 2), tr[(kt + 1) & 1]);
-                    lds_wait_tile<GPT, 6>(tr[kt & 1], s0, s1);
+                    lds_issue_tile<GPT, ZP, ZOFF>(a_base + (uint32_t)((kt + 1) * 4096),
+                                                  s_base0 + (uint32_t)((kt + 1) * GPT * 2),
+                                                  s_base1 + (uint32_t)((kt + 1) * GPT * 2), tr[(kt + 1) & 1]);
+                    lds_wait_tile<GPT, tile_reads<ZP>(), ZP>(tr[kt & 1], s0, s1, z0, z1);
                 } else {
-                    lds_wait_tile<GPT, 0>(tr[kt & 1], s0, s1);
+                    lds_wait_tile<GPT, 0, ZP>(tr[kt & 1], s0, s1, z0, z1);
                 }
                 const f16x8* av = tr[kt & 1].av;
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
-                    acc0 = mfma16(av[s], dequant8(bw0[kt][s], scale2(s0[s])), acc0);
-                    if constexpr (GU) acc1 = mfma16(av[s], dequant8(bw1[kt][s], scale2(s1[s])), acc1);
+                    if constexpr (ZP) {
+                        acc0 = mfma16(av[s], dequant8z(bw0[kt][s], scale2(s0[s]), z0[s]), acc0);
+                        if constexpr (GU) acc1 = mfma16(av[s], dequant8z(bw1[kt][s], scale2(s1[s]), z1[s]), acc1);
+                    } else {
+                        acc0 = mfma16(av[s], dequant8(bw0[kt][s], scale2(s0[s])), acc0);
+                        if constexpr (GU) acc1 = mfma16(av[s], dequant8(bw1[kt][s], scale2(s1[s])), acc1);
+                    }
                 }
             }
 #pragma unroll
@@ -234,7 +248,7 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(DecodeArgs a) {
         // first m-tile: the A rows and scales (issued before the weights) are
         // waited for here, the weights k-tile by k-tile inside tile(), so the
         // dequant and MFMAs of early k-tiles overlap the arrival of later ones
-        wait_vm_n((GU ? 2 : 1) * KT);
+        wait_vm_n(NM * KT);
         lds_barrier();
         tile(m_item);
         __syncthreads();  // As / Ss / ent are reused by the next item
@@ -294,7 +308,7 @@ __global__ __launch_bounds__(1024) void combine_decode_kernel(DecodeArgs a) {
 // ---------------------------------------------------------------------------
 // host launchers
 // ---------------------------------------------------------------------------
-template <int GPT, int KT, bool GU>
+template <int GPT, int KT, bool GU, bool ZP>
 static void launch_expert(const DecodeArgs& a, int n_groups, int n_rows, hipStream_t st) {
     // one generation of resident workgroups (work items are grid-strided);
     // never more workgroups than the worst-case item count
@@ -302,36 +316,41 @@ static void launch_expert(const DecodeArgs& a, int n_groups, int n_rows, hipStre
         int dev = 0, cus = 0, per_cu = 0;
         (void)hipGetDevice(&dev);
         (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, expert_decode_kernel<GPT, KT, GU>, 256, 0);
+        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, expert_decode_kernel<GPT, KT, GU, ZP>, 256, 0);
         return std::max(1, cus * std::max(1, per_cu));
     }();
     const int max_items = n_groups * ((n_rows / kTileRows + 3) / 4);
-    launch_k((expert_decode_kernel<GPT, KT, GU>), dim3(std::min(resident, max_items)), dim3(256), 0, st, a);
+    launch_k((expert_decode_kernel<GPT, KT, GU, ZP>), dim3(std::min(resident, max_items)), dim3(256), 0, st, a);
 }
 
-template <bool GU, int GPT>
+template <bool GU, int GPT, bool ZP>
 static hipError_t launch_expert_kt(const DecodeArgs& a, hipStream_t st) {
     const int K = GU ? a.hidden : a.inter;
     const int n_rows = GU ? a.inter : a.hidden;
     const int ng = a.n_experts + a.n_virtual;
     switch (K / kTileK) {
-        case 1: launch_expert<GPT, 1, GU>(a, ng, n_rows, st); break;
-        case 2: launch_expert<GPT, 2, GU>(a, ng, n_rows, st); break;
-        case 4: launch_expert<GPT, 4, GU>(a, ng, n_rows, st); break;
-        case 7: launch_expert<GPT, 7, GU>(a, ng, n_rows, st); break;
-        case 10: launch_expert<GPT, 10, GU>(a, ng, n_rows, st); break;
-        case 14: launch_expert<GPT, 14, GU>(a, ng, n_rows, st); break;
+        case 1: launch_expert<GPT, 1, GU, ZP>(a, ng, n_rows, st); break;
+        case 2: launch_expert<GPT, 2, GU, ZP>(a, ng, n_rows, st); break;
+        case 4: launch_expert<GPT, 4, GU, ZP>(a, ng, n_rows, st); break;
+        case 7: launch_expert<GPT, 7, GU, ZP>(a, ng, n_rows, st); break;
+        case 10: launch_expert<GPT, 10, GU, ZP>(a, ng, n_rows, st); break;
+        case 14: launch_expert<GPT, 14, GU, ZP>(a, ng, n_rows, st); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
+template <bool GU, int GPT>
+static hipError_t launch_expert_z(const DecodeArgs& a, hipStream_t st) {
+    return a.gate_z ? launch_expert_kt<GU, GPT, true>(a, st) : launch_expert_kt<GU, GPT, false>(a, st);
+}
+
 template <bool GU>
 static hipError_t launch_expert_g(const DecodeArgs& a, hipStream_t st) {
     switch (a.group) {
-        case 32: return launch_expert_kt<GU, 4>(a, st);
-        case 64: return launch_expert_kt<GU, 2>(a, st);
-        case 128: return launch_expert_kt<GU, 1>(a, st);
+        case 32: return launch_expert_z<GU, 4>(a, st);
+        case 64: return launch_expert_z<GU, 2>(a, st);
+        case 128: return launch_expert_z<GU, 1>(a, st);
         default: return hipErrorInvalidValue;
     }
 }

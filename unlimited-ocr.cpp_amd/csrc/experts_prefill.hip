@@ -82,7 +82,7 @@ constexpr int kPreBN = 128;               // weight rows per workgroup
 constexpr int kBigBM = kPrefillBigTileRows; // slots per m-tile (large-tile kernel)
 constexpr int kFragHalfs = 64 * 8;        // f16 per 1 KiB fragment
 
-template <int GPT, bool GU>
+template <int GPT, bool GU, bool ZP>
 __global__ __launch_bounds__(256) void experts_prefill_kernel(ExpertArgs a) {
     // A: 8 m-subtiles x 4 k-steps; B: 8 row blocks x 4 k-steps (fragments of 1 KiB)
     __shared__ __attribute__((aligned(16))) f16 As[8 * 4 * kFragHalfs];
@@ -114,23 +114,29 @@ __global__ __launch_bounds__(256) void experts_prefill_kernel(ExpertArgs a) {
     // (GU: 0..3 gate rows n0..n0+63, 4..7 the same up rows)
     const uint8_t* bsrc[2];
     const f16* ssrc[2];
+    const f16* zsrc[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int rbl = wave + 4 * i;
         int grow;  // global weight row block
         const uint8_t* wbase;
-        const f16* sbase;
+        const uint16_t* sbase;
+        const uint16_t* zbase;
         if constexpr (GU) {
             grow = ntile * 4 + (rbl & 3);
             wbase = (rbl < 4 ? a.w0 : a.w1) + (size_t)e * a.w_stride;
-            sbase = reinterpret_cast<const f16*>(rbl < 4 ? a.s0 : a.s1) + (size_t)e * a.s_stride;
+            sbase = (rbl < 4 ? a.s0 : a.s1) + (size_t)e * a.s_stride;
+            zbase = (rbl < 4 ? a.z0 : a.z1) + (size_t)e * a.s_stride;
         } else {
             grow = ntile * 8 + rbl;
             wbase = a.w0 + (size_t)e * a.w_stride;
-            sbase = reinterpret_cast<const f16*>(a.s0) + (size_t)e * a.s_stride;
+            sbase = a.s0 + (size_t)e * a.s_stride;
+            zbase = a.z0 + (size_t)e * a.s_stride;
         }
         bsrc[i] = wbase + (size_t)grow * KT * kTileBytes + (size_t)lane * 16;
-        ssrc[i] = sbase + (size_t)(grow * kTileRows + (lane & 15)) * NG;
+        const size_t so = (size_t)(grow * kTileRows + (lane & 15)) * NG;
+        ssrc[i] = reinterpret_cast<const f16*>(sbase) + so;
+        zsrc[i] = ZP ? reinterpret_cast<const f16*>(zbase) + so : nullptr;
     }
 
     f32x4 acc[4][4];
@@ -151,12 +157,15 @@ __global__ __launch_bounds__(256) void experts_prefill_kernel(ExpertArgs a) {
             }
         // weights: 16 bytes per lane per row block -> four exact f16 fragments
         u32x4 wv[2];
-        f16 sc[2][4];
+        f16 sc[2][4], zc[2][4];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             wv[i] = *reinterpret_cast<const u32x4*>(bsrc[i] + (size_t)kt * kTileBytes);
 #pragma unroll
-            for (int s = 0; s < 4; ++s) sc[i][s] = ssrc[i][kt * GPT + ((s * GPT) >> 2)];
+            for (int s = 0; s < 4; ++s) {
+                sc[i][s] = ssrc[i][kt * GPT + ((s * GPT) >> 2)];
+                if constexpr (ZP) zc[i][s] = zsrc[i][kt * GPT + ((s * GPT) >> 2)];
+            }
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -164,7 +173,7 @@ __global__ __launch_bounds__(256) void experts_prefill_kernel(ExpertArgs a) {
 #pragma unroll
             for (int s = 0; s < 4; ++s)
                 *reinterpret_cast<f16x8*>(Bs + ((size_t)(rbl * 4 + s) * 64 + lane) * 8) =
-                    dequant8(wv[i][s], scale2(sc[i][s]));
+                    ZP ? dequant8z(wv[i][s], scale2(sc[i][s]), zc[i][s]) : dequant8(wv[i][s], scale2(sc[i][s]));
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
@@ -248,7 +257,7 @@ constexpr int kRingAhead = 4;               // B fragments read ahead of their u
 constexpr int kRing = kRingAhead + 2;       // register ring size
 constexpr int lds_reads_after(int f) { return 63 - f < kRingAhead - 1 ? 63 - f : kRingAhead - 1; }
 
-template <int GPT, bool GU, int KT>
+template <int GPT, bool GU, int KT, bool ZP>
 __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) {
     // B fragments: [buffer][k-step 0..7][n-block 0..7][64 lanes][8 f16]
     __shared__ __attribute__((aligned(16))) f16 Bs[2][8 * kBigNB * kFragHalfs];
@@ -286,6 +295,8 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
         // (GU: row blocks 0..7 are gate rows of the n-tile's 128 act columns, 8..15 the same up rows)
         const uint8_t* bsrc[UNITS];
         const f16* ssrc[UNITS];
+        // zero offsets sit at the same index of the zero array (ZP layers)
+        const ptrdiff_t zdelta = ZP ? (GU ? 0 : a.z0 - a.s0) : 0;
 #pragma unroll
         for (int i = 0; i < UNITS; ++i) {
             const int u = tid + 256 * i, rbl = u >> 6, q = u & 63;
@@ -304,6 +315,11 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
             bsrc[i] = wbase + (size_t)grow * KT * kTileBytes + (size_t)q * 16;
             ssrc[i] = reinterpret_cast<const f16*>(sbase) + (size_t)(grow * kTileRows + (q & 15)) * NG;
         }
+        // gate/up: unit i's matrix is gate for i < UNITS / 2 (row blocks 0..7), up after
+        auto zsrc_of = [&](int i) -> const f16* {
+            if constexpr (GU) return ssrc[i] + (i < UNITS / 2 ? a.z0 - a.s0 : a.z1 - a.s1);
+            else return ssrc[i] + zdelta;
+        };
         // LDS destination of unit i's 8-column run s (columns s*32 + 8*(q/16) ..
         // +7 of local weight row n = (wave + 4i) * 16 + q % 16, in 32x32x16
         // B-fragment order): byte offset bdst0 + s * 16384 + i * 2048
@@ -326,9 +342,9 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
         //     start of k-tile kt, staged into LDS during k-tile kt+1.
         // Issue order within k-tile kt: B(kt+2), then A(kt+1, ks) after k-step ks.
         constexpr int AK = JN;         // activation loads per k-step
-        constexpr int NB = 2 * UNITS;  // loads per k-tile of weights
+        constexpr int NB = (ZP ? 3 : 2) * UNITS;  // loads per k-tile of weights
         u32x4 braw[2][UNITS];
-        typename std::conditional<GPT == 4, u32x2, uint32_t>::type bscr[2][UNITS];
+        typename std::conditional<GPT == 4, u32x2, uint32_t>::type bscr[2][UNITS], bzr[2][UNITS];
         f16x8 areg[JN][8];
         f16x8 bring[kRing];
         auto issue_a = [&](auto ktc, auto ksc) {
@@ -351,6 +367,15 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
                 else
                     gload<kt * GPT * 2>(bscr[kt & 1][i], ssrc[i]);
             }
+            if constexpr (ZP) {
+#pragma unroll
+                for (int i = 0; i < UNITS; ++i) {
+                    if constexpr (GPT == 1)
+                        gload_u16<kt * 2>(bzr[kt & 1][i], zsrc_of(i));
+                    else
+                        gload<kt * GPT * 2>(bzr[kt & 1][i], zsrc_of(i));
+                }
+            }
         };
         // wait until at most N loads are outstanding, then let the guarded values be used
         auto wait_a = [&](auto nc, int ks) {
@@ -364,13 +389,14 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
             for (int i = 0; i < UNITS; ++i) {
                 tie(braw[buf][i]);
                 tie(bscr[buf][i]);
+                if constexpr (ZP) tie(bzr[buf][i]);
             }
         };
-        auto scale_of = [&](int buf, int i, int s) -> f16 {
+        auto word_of = [&](const auto& words, int buf, int i, int s) -> f16 {
             const int g = (s * GPT) >> 2;  // group within the k-tile
             uint32_t w;
-            if constexpr (GPT == 4) w = bscr[buf][i][g >> 1];
-            else w = bscr[buf][i];
+            if constexpr (GPT == 4) w = words[buf][i][g >> 1];
+            else w = words[buf][i];
             const uint16_t h = (uint16_t)((g & 1) ? (w >> 16) : (w & 0xffffu));
             return __builtin_bit_cast(f16, h);
         };
@@ -378,7 +404,11 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
         auto stage_run = [&](int kt, auto ic, auto sc) {
             constexpr int i = decltype(ic)::value, s = decltype(sc)::value;
             const uint32_t dst = lds_addr(Bs[kt & 1]) + bdst0;
-            lds_write16<s * 16384 + i * 2048>(dst, dequant8(braw[kt & 1][i][s], scale2(scale_of(kt & 1, i, s))));
+            const f16 scl = word_of(bscr, kt & 1, i, s);
+            if constexpr (ZP)
+                lds_write16<s * 16384 + i * 2048>(dst, dequant8z(braw[kt & 1][i][s], scale2(scl), word_of(bzr, kt & 1, i, s)));
+            else
+                lds_write16<s * 16384 + i * 2048>(dst, dequant8(braw[kt & 1][i][s], scale2(scl)));
         };
 
         f32x16 acc[JN][kBigNB];
@@ -485,37 +515,37 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
         body(std::integral_constant<int, 2>{});
 }
 
-template <int GPT, bool GU>
+template <int GPT, bool GU, bool ZP>
 static bool launch_big(const ExpertArgs& a, int max_tiles, hipStream_t st) {
     const int n_ntiles = GU ? (a.n_rows / (kBigBN / 2)) : (a.n_rows / kBigBN);
     if (n_ntiles * (GU ? kBigBN / 2 : kBigBN) != a.n_rows) return false;
     const dim3 grid(((max_tiles + 7) / 8) * 8 * n_ntiles);
     switch (a.k / kTileK) {
-        case 7: launch_k((experts_prefill_big_kernel<GPT, GU, 7>), grid, dim3(256), 0, st, a); return true;
-        case 10: launch_k((experts_prefill_big_kernel<GPT, GU, 10>), grid, dim3(256), 0, st, a); return true;
+        case 7: launch_k((experts_prefill_big_kernel<GPT, GU, 7, ZP>), grid, dim3(256), 0, st, a); return true;
+        case 10: launch_k((experts_prefill_big_kernel<GPT, GU, 10, ZP>), grid, dim3(256), 0, st, a); return true;
         default: return false;
     }
 }
 
-template <bool GU>
+template <bool GU, bool ZP>
 static hipError_t launch_prefill_g(const ExpertArgs& a, int max_tiles, hipStream_t st) {
     const int n_ntiles = GU ? (a.n_rows / (kPreBN / 2)) : (a.n_rows / kPreBN);
     const dim3 grid(max_tiles * n_ntiles);
     if (a.bm == kBigBM) {
         bool done = false;
         switch (a.group) {
-            case 32: done = launch_big<4, GU>(a, max_tiles, st); break;
-            case 64: done = launch_big<2, GU>(a, max_tiles, st); break;
-            case 128: done = launch_big<1, GU>(a, max_tiles, st); break;
+            case 32: done = launch_big<4, GU, ZP>(a, max_tiles, st); break;
+            case 64: done = launch_big<2, GU, ZP>(a, max_tiles, st); break;
+            case 128: done = launch_big<1, GU, ZP>(a, max_tiles, st); break;
             default: return hipErrorInvalidValue;
         }
         return done ? hipGetLastError() : hipErrorInvalidValue;
     }
     if (a.bm != kPreBM) return hipErrorInvalidValue;
     switch (a.group) {
-        case 32: launch_k((experts_prefill_kernel<4, GU>), grid, dim3(256), 0, st, a); break;
-        case 64: launch_k((experts_prefill_kernel<2, GU>), grid, dim3(256), 0, st, a); break;
-        case 128: launch_k((experts_prefill_kernel<1, GU>), grid, dim3(256), 0, st, a); break;
+        case 32: launch_k((experts_prefill_kernel<4, GU, ZP>), grid, dim3(256), 0, st, a); break;
+        case 64: launch_k((experts_prefill_kernel<2, GU, ZP>), grid, dim3(256), 0, st, a); break;
+        case 128: launch_k((experts_prefill_kernel<1, GU, ZP>), grid, dim3(256), 0, st, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -524,7 +554,8 @@ static hipError_t launch_prefill_g(const ExpertArgs& a, int max_tiles, hipStream
 hipError_t launch_experts_prefill(const ExpertArgs& a, bool gate_up, int max_tiles, hipStream_t st) {
     if (max_tiles <= 0) return hipSuccess;
     if ((gate_up && a.n_rows % (kPreBN / 2)) || (!gate_up && a.n_rows % kPreBN)) return hipErrorInvalidValue;
-    return gate_up ? launch_prefill_g<true>(a, max_tiles, st) : launch_prefill_g<false>(a, max_tiles, st);
+    if (a.z0) return gate_up ? launch_prefill_g<true, true>(a, max_tiles, st) : launch_prefill_g<false, true>(a, max_tiles, st);
+    return gate_up ? launch_prefill_g<true, false>(a, max_tiles, st) : launch_prefill_g<false, false>(a, max_tiles, st);
 }
 
 }  // namespace uocr_hip

@@ -75,9 +75,11 @@ struct ExpertArgs {
     const f16* a;            // activations: x16 [seq, K] (gathered via slot_tok) or act [slots, K]
     int gather;              // 1: row = slot_tok[slot], 0: row = slot
     const uint8_t* w0;       // packed weights, per expert stride w_stride bytes (gate or down)
-    const uint16_t* s0;      // bf16 scales, per expert stride s_stride elements
+    const uint16_t* s0;      // f16 scales, per expert stride s_stride elements
     const uint8_t* w1;       // second matrix (up) for the fused gate/up pass, else null
     const uint16_t* s1;
+    const uint16_t* z0;      // zero offsets in the scale layout (null: symmetric layer)
+    const uint16_t* z1;
     long long w_stride, s_stride;
     int n_rows;              // output features (N)
     int k;                   // input features (K)
@@ -141,6 +143,9 @@ struct DecodeArgs {
     const uint16_t* gate_s;
     const uint16_t* up_s;
     const uint16_t* down_s;
+    const uint16_t* gate_z;    // zero offsets in the scale layout (null: symmetric layer)
+    const uint16_t* up_z;
+    const uint16_t* down_z;
     long long gu_wstride, gu_sstride, dn_wstride, dn_sstride;
     FusedSync* sync;           // fused kernel only
     f16* act;                  // [slots, inter]; fused: [(E + n_virtual) * seq, inter]
