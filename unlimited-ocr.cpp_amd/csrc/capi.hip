@@ -235,10 +235,12 @@ WsPlan plan(const uocr_hip_moe_layer* L, int seq) {
     p.tile_e = take((size_t)p.max_tiles * 4);
     p.tile_m0 = take((size_t)p.max_tiles * 4);
     p.tile_info = take((size_t)p.max_tiles * 16);
-    // act: one row per slot, or per (group, token) for the fused decode kernel
-    p.act = take((size_t)std::max(p.slots, Ev * seq) * L->inter * 2);
-    // y: one row per entry, or per (group, token) for the fused decode kernel
-    p.y = take((size_t)std::max(p.slots, Ev * seq) * L->hidden * 4);
+    // act / y: one row per slot (y: per entry), or per (group, token) when the
+    // fused decode kernel may run (seq <= kFusedMaxSeq, any input dtype)
+    const bool fused_rows = seq <= kFusedMaxSeq && L->sync && decode_fused_ok(L->hidden, L->inter, L->group);
+    const size_t rows = fused_rows ? (size_t)std::max(p.slots, Ev * seq) : (size_t)p.slots;
+    p.act = take(rows * L->inter * 2);
+    p.y = take(rows * L->hidden * 4);
     const int chunks = group_chunks(seq, L->top_k);
     p.lrank = take((size_t)seq * L->top_k * 4);
     p.chunk_count = take((size_t)chunks * L->n_experts * 4);
