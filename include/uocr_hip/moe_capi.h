@@ -114,6 +114,20 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* layer, const void* x, i
                                int seq, float* out, int* ids_out, float* weights_out,
                                void* workspace, size_t workspace_bytes, void* stream);
 
+/* uocr_hip_moe_layer_forward without a workspace argument and without any
+ * allocation. No counterpart in the reference: for callers that cannot call
+ * hipMalloc (code under HIP graph capture without a pre-allocated workspace,
+ * serving loops or harnesses that forbid allocation). The workspace is a
+ * library-owned device array of 16 MiB per device (held until the process
+ * ends); calls whose uocr_hip_moe_layer_workspace_size exceeds it return
+ * UOCR_HIP_EINVAL (about 250 decode tokens at the Unlimited-OCR shapes).
+ * Every call on one device shares that array: calls that overlap in time on
+ * one device (different streams without ordering) race and must not be
+ * issued. The layer's device must be current. */
+int uocr_hip_moe_layer_forward_noalloc(const uocr_hip_moe_layer* layer, const void* x, int x_dtype,
+                                       int seq, float* out, int* ids_out, float* weights_out,
+                                       void* stream);
+
 /* Per-stage timing of uocr_hip_moe_layer_forward (benchmark support): when
  * enabled, forward records HIP events between its stages on its stream.
  * read_timing synchronizes on the last event and returns the accumulated

@@ -120,6 +120,36 @@ int repack(const uocr_hip_qmatrix& q, int row0, int R, int col0, int K, uint8_t*
 
 }  // namespace
 
+// Device scratch of uocr_hip_moe_layer_forward_noalloc: the workspace of one
+// forward call for callers that cannot allocate (graph capture without a
+// pre-allocated workspace, serving loops that forbid hipMalloc). One copy per
+// device, held until the process ends; the host-side name `scratch` is only a
+// stand-in -- its device address comes from hipGetSymbolAddress, looked up once
+// per device at layer creation (scratch_ptr) and used for every access.
+constexpr size_t kScratchBytes = 16u << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on `device` (the current device); looked up
+// on first use per device.
+int scratch_ptr(int device, void** out) {
+    if (device < 0 || device >= kMaxDevices) return fail(UOCR_HIP_EINVAL, "device index out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        g_scratch_ptr[device] = p;
+    }
+    *out = g_scratch_ptr[device];
+    return UOCR_HIP_OK;
+}
+}  // namespace
+
 constexpr int kStages = 6;  // router, group, gate_up, down, combine, fused
 
 struct uocr_hip_moe_layer {
@@ -408,6 +438,13 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
         return rc;
     }
     {
+        void* sp = nullptr;  // device address of the no-alloc scratch on this device
+        if ((rc = scratch_ptr(L->device, &sp))) {
+            free_layer(L);
+            return rc;
+        }
+    }
+    {
         hipError_t e = hipMalloc((void**)&L->sync, sizeof(FusedSync));
         if (e == hipSuccess) e = hipMemset(L->sync, 0, sizeof(FusedSync));
         if (e != hipSuccess) {
@@ -677,6 +714,21 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     stage(-1);
     if (timing) Lm->pending = true;
     return UOCR_HIP_OK;
+}
+
+int uocr_hip_moe_layer_forward_noalloc(const uocr_hip_moe_layer* L, const void* x, int x_dtype, int seq, float* out,
+                                       int* ids_out, float* weights_out, void* stream) {
+    if (!L) return fail(UOCR_HIP_EINVAL, "null argument");
+    if (seq <= 0) return fail(UOCR_HIP_EINVAL, "seq must be positive");
+    const size_t need = uocr_hip_moe_layer_workspace_size(L, seq);
+    if (need == 0 || need > kScratchBytes)
+        return fail(UOCR_HIP_EINVAL, "seq " + std::to_string(seq) + " needs " + std::to_string(need) +
+                                         " bytes of workspace; the no-alloc scratch holds " +
+                                         std::to_string(kScratchBytes) + " (use uocr_hip_moe_layer_forward)");
+    void* ws = nullptr;
+    int rc = scratch_ptr(L->device, &ws);
+    if (rc) return rc;
+    return uocr_hip_moe_layer_forward(L, x, x_dtype, seq, out, ids_out, weights_out, ws, kScratchBytes, stream);
 }
 
 int uocr_hip_moe_layer_set_timing(uocr_hip_moe_layer* L, int enable) {

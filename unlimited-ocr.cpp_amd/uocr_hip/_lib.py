@@ -62,6 +62,8 @@ SIGNATURES = {
     "uocr_hip_moe_layer_forward": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
                                               C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
                                               C.c_void_p]),
+    "uocr_hip_moe_layer_forward_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
+                                                      C.c_void_p, C.c_void_p, C.c_void_p]),
     "uocr_hip_moe_layer_set_timing": (C.c_int, [C.c_void_p, C.c_int]),
     "uocr_hip_moe_layer_read_timing": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int,
                                                   C.POINTER(C.c_int)]),

@@ -116,6 +116,19 @@ class MoELayerInt4:
             weights.data_ptr() if weights is not None else None,
             ws_ptr, ws_bytes, st))
 
+    def forward_noalloc(self, x, out, ids=None, weights=None, stream=None):
+        """forward() on the library's device scratch (no workspace argument,
+        no allocation; calls on one device must not overlap)."""
+        import torch
+        dt = DTYPE_BF16 if x.dtype == torch.bfloat16 else DTYPE_F32
+        if x.dtype not in (torch.bfloat16, torch.float32):
+            raise TypeError("x must be bf16 or f32")
+        st = stream if stream is not None else torch.cuda.current_stream().cuda_stream
+        check(self.lib.uocr_hip_moe_layer_forward_noalloc(
+            self.handle, x.data_ptr(), dt, x.shape[0], out.data_ptr(),
+            ids.data_ptr() if ids is not None else None,
+            weights.data_ptr() if weights is not None else None, st))
+
     def set_timing(self, enable):
         check(self.lib.uocr_hip_moe_layer_set_timing(self.handle, 1 if enable else 0))
 
