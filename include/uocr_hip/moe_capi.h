@@ -171,6 +171,91 @@ int uocr_hip_moe_router_topk(const float* router_logits, int seq, int n_experts,
                              int* d_assign_token, float* d_assign_w, int* d_count, int cap,
                              void* stream);
 
+/* ---- expert operator mirrors on the reference's device layout ------------
+ * Tables as GpuDecoder::upload_expert_table builds them (src/engine/
+ * gpu_decoder.cu:316-358): INT4 packed rows [n_experts][rows][ceil(cols/2)]
+ * bytes (low nibble = even column; expert stride *_pstride bytes), f32 scales
+ * and zeros [n_experts][rows][ng] (expert stride *_sstride floats, row stride
+ * ng); value = (q - zero) * scale. Assignment tables [n_experts, cap] and
+ * count[n_experts] as moe_router_topk writes them (entries past
+ * min(count, cap) are ignored). Activations f32. Weights are dequantised to
+ * bf16 and multiplied with bf16 activations, f32 accumulation (the
+ * reference's tensor-core numerics). `bn` / `bm` are accepted and ignored.
+ * This build requires hidden and inter multiples of 64 and group % 32 == 0
+ * (else UOCR_HIP_EUNSUPPORTED). The down projections ADD w * y into `out`
+ * with f32 atomics (the caller zeroes `out`, as in the reference); the order
+ * of those additions is not fixed. */
+
+/* Mirror of uocr::cuda::moe_grouped_gate_up_int4 (include/uocr/cuda_ops.h:
+ * 170-175, src/kernels/cuda/moe_gemm_int4.cu:736-760): act[e, s, :] =
+ * silu(gate_e x_t) * up_e x_t for t = assign_token[e, s], s < count[e]. */
+int uocr_hip_moe_grouped_gate_up_int4(const float* x, const uint8_t* gate_packed, const float* gate_scales,
+                                      const float* gate_zeros, int gate_pstride, int gate_sstride, int gate_ng,
+                                      const uint8_t* up_packed, const float* up_scales, const float* up_zeros,
+                                      int up_pstride, int up_sstride, int up_ng, const int* assign_token,
+                                      const int* count, int n_experts, int cap, int hidden, int inter, int group,
+                                      float* act, int bn, int bm, void* stream);
+
+/* Mirror of uocr::cuda::moe_grouped_down_int4 (cuda_ops.h:177-181,
+ * moe_gemm_int4.cu:762-786): out[t] += assign_w[e, s] * down_e act[e, s]. */
+int uocr_hip_moe_grouped_down_int4(const float* act, const uint8_t* packed, const float* scales,
+                                   const float* zeros, int pstride, int sstride, int ng, const int* assign_token,
+                                   const float* assign_w, const int* count, int n_experts, int cap, int hidden,
+                                   int inter, int group, float* out, int bn, int bm, void* stream);
+
+/* Mirror of uocr::cuda::moe_experts_masked_int4 (cuda_ops.h:145-155,
+ * moe_device.cu:322-347): the grouped gate/up, then the grouped down. `seq`
+ * is unused, as in the reference. */
+int uocr_hip_moe_experts_masked_int4(const float* x, int seq, const uint8_t* gate_packed,
+                                     const float* gate_scales, const float* gate_zeros, int gate_pstride,
+                                     int gate_sstride, int gate_ng, const uint8_t* up_packed,
+                                     const float* up_scales, const float* up_zeros, int up_pstride,
+                                     int up_sstride, int up_ng, const uint8_t* down_packed,
+                                     const float* down_scales, const float* down_zeros, int down_pstride,
+                                     int down_sstride, int down_ng, const int* assign_token,
+                                     const float* assign_w, const int* count, int n_experts, int cap,
+                                     int hidden, int inter, int group, float* act, float* out, void* stream);
+
+/* BF16 experts: device arrays of n_experts row-major bf16 matrix pointers,
+ * gate_w / up_w [inter, hidden], down_w [hidden, inter].
+ * Mirror of uocr::cuda::moe_grouped_gate_up_bf16 (cuda_ops.h:192-195,
+ * src/kernels/cuda/moe_gemm_bf16.cu:122-353). */
+int uocr_hip_moe_grouped_gate_up_bf16(const float* x, const uint16_t* const* gate_w,
+                                      const uint16_t* const* up_w, const int* assign_token, const int* count,
+                                      int n_experts, int cap, int hidden, int inter, float* act, int bn, int bm,
+                                      void* stream);
+
+/* Mirror of uocr::cuda::moe_grouped_down_bf16 (cuda_ops.h:197-200). */
+int uocr_hip_moe_grouped_down_bf16(const float* act, const uint16_t* const* down_w, const int* assign_token,
+                                   const float* assign_w, const int* count, int n_experts, int cap, int hidden,
+                                   int inter, float* out, int bn, int bm, void* stream);
+
+/* Mirror of uocr::cuda::moe_experts_masked (cuda_ops.h:139-143,
+ * moe_device.cu:300-320): bf16 gate/up, then bf16 down. */
+int uocr_hip_moe_experts_masked(const float* x, int seq, const uint16_t* const* gate_w,
+                                const uint16_t* const* up_w, const uint16_t* const* down_w,
+                                const int* assign_token, const float* assign_w, const int* count,
+                                int n_experts, int cap, int hidden, int inter, float* act, float* out,
+                                void* stream);
+
+/* Mirror of uocr::cuda::moe_gemm_int4 (cuda_ops.h:204-207,
+ * moe_gemm_int4.cu:793-800): y[m, n] = x[m, :] . dequant(W)[n, :] for one
+ * INT4 matrix (packed [n, ceil(k/2)], scales / zeros [n, ceil(k/group_size)]),
+ * the per-expert GEMM of the host-grouping path. The _tc* variants are the
+ * reference's tuning entry points (cuda_ops.h:211-239): same product, the tile
+ * parameters are ignored. Requires n % 64 == 0, k % 32 == 0, group_size % 32 == 0. */
+int uocr_hip_moe_gemm_int4(const float* x, const uint8_t* packed, const float* scales, const float* zeros,
+                           int m, int n, int k, int group_size, float* y, void* stream);
+int uocr_hip_moe_gemm_int4_tc(const float* x, const uint8_t* packed, const float* scales, const float* zeros,
+                              int m, int n, int k, int group_size, float* y, void* stream);
+int uocr_hip_moe_gemm_int4_tc_n(const float* x, const uint8_t* packed, const float* scales, const float* zeros,
+                                int m, int n, int k, int group_size, float* y, int bn, void* stream);
+int uocr_hip_moe_gemm_int4_tc_nk(const float* x, const uint8_t* packed, const float* scales, const float* zeros,
+                                 int m, int n, int k, int group_size, float* y, int bn, int bk, void* stream);
+int uocr_hip_moe_gemm_int4_tc_pipe(const float* x, const uint8_t* packed, const float* scales,
+                                   const float* zeros, int m, int n, int k, int group_size, float* y, int bn,
+                                   void* stream);
+
 /* Overflow report of uocr_hip_moe_router_topk (the reference drops entries
  * past `cap` silently, moe_device.cu:90-95): *flag = 1 if any call since the
  * last clear routed more than `cap` entries to one expert (only possible when

@@ -31,6 +31,12 @@ int fail(int code, const std::string& msg) {
     return code;
 }
 
+}  // namespace
+
+int uocr_hip::set_error(int code, const std::string& msg) { return fail(code, msg); }
+
+namespace {
+
 int hip_fail(hipError_t e, const char* what) {
     return fail(UOCR_HIP_EHIP, std::string(what) + ": " + hipGetErrorString(e));
 }

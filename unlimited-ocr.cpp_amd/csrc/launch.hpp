@@ -4,6 +4,8 @@
 #include <hip/hip_ext.h>
 #include <stdint.h>
 
+#include <string>
+
 #include "common.hpp"
 
 namespace uocr_hip {
@@ -178,5 +180,24 @@ bool group_fits(int seq, int top_k, int n_experts);  // the grouping scan's LDS 
 hipError_t router_overflow_read(int clear, int* flag);  // sticky count > cap flag of the router mirror
 hipError_t launch_experts_prefill(const ExpertArgs& a, bool gate_up, int max_tiles, hipStream_t st);
 hipError_t launch_combine(const CombineArgs& c, hipStream_t st);
+
+// reference-layout operator mirrors (mirrors.hip)
+int set_error(int code, const std::string& msg);  // capi.hip: thread's last error text
+bool mirror_shapes_ok(int k, int n, int group, bool int4);
+hipError_t mirror_gate_up_int4(const float* x, const uint8_t* gp, const float* gs, const float* gz, long long gps,
+                               long long gss, int gng, const uint8_t* up, const float* us, const float* uz,
+                               long long ups, long long uss, int ung, const int* assign_token, const int* count,
+                               int n_experts, int cap, int hidden, int inter, int group, float* act, hipStream_t st);
+hipError_t mirror_down_int4(const float* act, const uint8_t* p, const float* s, const float* z, long long ps,
+                            long long ss, int ng, const int* assign_token, const float* assign_w, const int* count,
+                            int n_experts, int cap, int hidden, int inter, int group, float* out, hipStream_t st);
+hipError_t mirror_gemm_int4(const float* x, const uint8_t* p, const float* s, const float* z, int m, int n, int k,
+                            int group, float* y, hipStream_t st);
+hipError_t mirror_gate_up_bf16(const float* x, const uint16_t* const* gw, const uint16_t* const* uw,
+                               const int* assign_token, const int* count, int n_experts, int cap, int hidden,
+                               int inter, float* act, hipStream_t st);
+hipError_t mirror_down_bf16(const float* act, const uint16_t* const* dw, const int* assign_token,
+                            const float* assign_w, const int* count, int n_experts, int cap, int hidden, int inter,
+                            float* out, hipStream_t st);
 
 }  // namespace uocr_hip

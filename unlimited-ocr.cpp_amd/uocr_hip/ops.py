@@ -23,3 +23,104 @@ def moe_router_overflow(clear=True):
     f = C.c_int(0)
     check(load().uocr_hip_moe_router_overflow(1 if clear else 0, C.byref(f)))
     return f.value
+
+
+class RefInt4Table:
+    """Per-expert INT4 tables in the reference's device layout
+    (GpuDecoder::upload_expert_table, src/engine/gpu_decoder.cu:316-358):
+    packed [E, rows, ceil(cols/2)] u8, scales / zeros [E, rows, ng] f32."""
+
+    def __init__(self, qmats, device):
+        import numpy as np
+        import torch
+        q0 = qmats[0]
+        self.rows, self.cols, self.group = q0.rows, q0.cols, q0.group
+        self.ng = (q0.cols + q0.group - 1) // q0.group
+        self.packed = torch.from_numpy(np.stack([q.packed for q in qmats])).to(device)
+        self.scales = torch.from_numpy(np.stack([q.scales for q in qmats]).astype(np.float32)).to(device)
+        self.zeros = torch.from_numpy(np.stack([q.zeros for q in qmats]).astype(np.float32)).to(device)
+        self.pstride = self.rows * ((self.cols + 1) // 2)
+        self.sstride = self.rows * self.ng
+
+    def args(self):
+        return [self.packed.data_ptr(), self.scales.data_ptr(), self.zeros.data_ptr(),
+                self.pstride, self.sstride, self.ng]
+
+
+def moe_grouped_gate_up_int4(x, gate, up, assign_token, count, cap, act, bn=16, bm=64, stream=None):
+    """Mirror of uocr::cuda::moe_grouped_gate_up_int4 (cuda_ops.h:170-175)."""
+    E = gate.packed.shape[0]
+    check(load().uocr_hip_moe_grouped_gate_up_int4(
+        x.data_ptr(), *gate.args(), *up.args(), assign_token.data_ptr(), count.data_ptr(), E, cap,
+        gate.cols, gate.rows, gate.group, act.data_ptr(), bn, bm, _stream(stream)))
+
+
+def moe_grouped_down_int4(act, down, assign_token, assign_w, count, cap, out, bn=16, bm=64, stream=None):
+    """Mirror of uocr::cuda::moe_grouped_down_int4 (cuda_ops.h:177-181)."""
+    E = down.packed.shape[0]
+    check(load().uocr_hip_moe_grouped_down_int4(
+        act.data_ptr(), *down.args(), assign_token.data_ptr(), assign_w.data_ptr(), count.data_ptr(), E, cap,
+        down.rows, down.cols, down.group, out.data_ptr(), bn, bm, _stream(stream)))
+
+
+def moe_experts_masked_int4(x, gate, up, down, assign_token, assign_w, count, cap, act, out, stream=None):
+    """Mirror of uocr::cuda::moe_experts_masked_int4 (cuda_ops.h:145-155)."""
+    E = gate.packed.shape[0]
+    check(load().uocr_hip_moe_experts_masked_int4(
+        x.data_ptr(), x.shape[0], *gate.args(), *up.args(), *down.args(), assign_token.data_ptr(),
+        assign_w.data_ptr(), count.data_ptr(), E, cap, gate.cols, gate.rows, gate.group, act.data_ptr(),
+        out.data_ptr(), _stream(stream)))
+
+
+def _ptr_array(mats, device):
+    import torch
+    return torch.tensor([m.data_ptr() for m in mats], dtype=torch.int64, device=device)
+
+
+def moe_experts_masked(x, gate_w, up_w, down_w, assign_token, assign_w, count, cap, act, out, stream=None):
+    """Mirror of uocr::cuda::moe_experts_masked (cuda_ops.h:139-143). gate_w /
+    up_w / down_w: lists of per-expert bf16 device tensors."""
+    dev = x.device
+    pg, pu, pd = _ptr_array(gate_w, dev), _ptr_array(up_w, dev), _ptr_array(down_w, dev)
+    inter, hidden = gate_w[0].shape
+    check(load().uocr_hip_moe_experts_masked(
+        x.data_ptr(), x.shape[0], pg.data_ptr(), pu.data_ptr(), pd.data_ptr(), assign_token.data_ptr(),
+        assign_w.data_ptr(), count.data_ptr(), len(gate_w), cap, hidden, inter, act.data_ptr(), out.data_ptr(),
+        _stream(stream)))
+    return pg, pu, pd  # keep alive until the stream has run
+
+
+def moe_grouped_gate_up_bf16(x, gate_w, up_w, assign_token, count, cap, act, bn=16, bm=64, stream=None):
+    """Mirror of uocr::cuda::moe_grouped_gate_up_bf16 (cuda_ops.h:192-195)."""
+    dev = x.device
+    pg, pu = _ptr_array(gate_w, dev), _ptr_array(up_w, dev)
+    inter, hidden = gate_w[0].shape
+    check(load().uocr_hip_moe_grouped_gate_up_bf16(
+        x.data_ptr(), pg.data_ptr(), pu.data_ptr(), assign_token.data_ptr(), count.data_ptr(), len(gate_w), cap,
+        hidden, inter, act.data_ptr(), bn, bm, _stream(stream)))
+    return pg, pu
+
+
+def moe_grouped_down_bf16(act, down_w, assign_token, assign_w, count, cap, out, bn=16, bm=64, stream=None):
+    """Mirror of uocr::cuda::moe_grouped_down_bf16 (cuda_ops.h:197-200)."""
+    dev = act.device
+    pd = _ptr_array(down_w, dev)
+    hidden, inter = down_w[0].shape
+    check(load().uocr_hip_moe_grouped_down_bf16(
+        act.data_ptr(), pd.data_ptr(), assign_token.data_ptr(), assign_w.data_ptr(), count.data_ptr(), len(down_w),
+        cap, hidden, inter, out.data_ptr(), bn, bm, _stream(stream)))
+    return pd
+
+
+def moe_gemm_int4(x, packed, scales, zeros, n, k, group, y, variant="", stream=None):
+    """Mirror of uocr::cuda::moe_gemm_int4 and its _tc* variants (cuda_ops.h:204-239)."""
+    lib = load()
+    m = x.shape[0]
+    base = [x.data_ptr(), packed.data_ptr(), scales.data_ptr(), zeros.data_ptr(), m, n, k, group, y.data_ptr()]
+    if variant in ("", "_tc"):
+        rc = getattr(lib, "uocr_hip_moe_gemm_int4" + variant)(*base, _stream(stream))
+    elif variant in ("_tc_n", "_tc_pipe"):
+        rc = getattr(lib, "uocr_hip_moe_gemm_int4" + variant)(*base, 16, _stream(stream))
+    else:
+        rc = lib.uocr_hip_moe_gemm_int4_tc_nk(*base, 16, 64, _stream(stream))
+    check(rc)
