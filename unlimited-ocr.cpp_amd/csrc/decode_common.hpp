@@ -56,14 +56,14 @@ template <int N>
 __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
-// s_waitcnt vmcnt(n) for a wave-uniform runtime n (values above 31 wait for 0)
+// s_waitcnt vmcnt(n) for a wave-uniform runtime n (values above 63 wait for 0)
 __device__ __forceinline__ void wait_vm_n(int n) {
     switch (n) {
 #define UOCR_VM(k) case k: wait_vm<k>(); break;
-        UOCR_VM(1) UOCR_VM(2) UOCR_VM(3) UOCR_VM(4) UOCR_VM(5) UOCR_VM(6) UOCR_VM(7) UOCR_VM(8)
-        UOCR_VM(9) UOCR_VM(10) UOCR_VM(11) UOCR_VM(12) UOCR_VM(13) UOCR_VM(14) UOCR_VM(15) UOCR_VM(16)
-        UOCR_VM(17) UOCR_VM(18) UOCR_VM(19) UOCR_VM(20) UOCR_VM(21) UOCR_VM(22) UOCR_VM(23) UOCR_VM(24)
-        UOCR_VM(25) UOCR_VM(26) UOCR_VM(27) UOCR_VM(28) UOCR_VM(29) UOCR_VM(30) UOCR_VM(31)
+#define UOCR_VM8(b) UOCR_VM(b) UOCR_VM(b + 1) UOCR_VM(b + 2) UOCR_VM(b + 3) UOCR_VM(b + 4) UOCR_VM(b + 5) UOCR_VM(b + 6) UOCR_VM(b + 7)
+        UOCR_VM8(1) UOCR_VM8(9) UOCR_VM8(17) UOCR_VM8(25) UOCR_VM8(33) UOCR_VM8(41) UOCR_VM8(49)
+        UOCR_VM(57) UOCR_VM(58) UOCR_VM(59) UOCR_VM(60) UOCR_VM(61) UOCR_VM(62) UOCR_VM(63)
+#undef UOCR_VM8
 #undef UOCR_VM
         default: wait_vm<0>(); break;
     }

@@ -57,11 +57,18 @@ __device__ __forceinline__ void report_timeout(FusedSync* sy, unsigned rtag) {
 // through to, and read from, the coherence point shared by every XCD's L2), so
 // publishing needs no L2-wide writeback and reading no L2 invalidation -- both
 // serialise per XCD and cost far more than the few rows exchanged. Publish =
-// the stores, every wave's vmcnt(0) (__syncthreads), then a counter increment;
+// the stores, an explicit vmcnt(0) in every wave (the workgroup barrier does
+// not wait for outstanding stores), the barrier, then a counter increment;
 // consume = spin on the counter, then the loads. The workgroup-scope fences
 // only keep the compiler from moving accesses across those points.
 __device__ __forceinline__ void fence_wg_release() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup"); }
 __device__ __forceinline__ void fence_wg_acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup"); }
+
+// Wait until every memory operation this wave issued has completed (stores
+// included: on gfx9 vmcnt counts them). The asm carries a memory clobber, so
+// the compiler keeps every earlier store before it; the waitcnt builtin alone
+// would let a store sink past the wait.
+__device__ __forceinline__ void store_fence() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 template <typename U>
 __device__ __forceinline__ U load_cg(const U* p) {
@@ -77,16 +84,12 @@ __device__ __forceinline__ f32x4 load4_cg(const float* p) {
 __device__ __forceinline__ void store_cg_f16(f16* p, f16 v) {
     asm volatile("global_store_short %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
 }
-// 16-byte agent-coherent read (rows other workgroups wrote with sc1 stores)
-// (issue only: the caller waits with wait_rows before using the values)
-__device__ __forceinline__ void load16_cg_issue(f32x4& v, const float* p) {
-    asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=&v"(v) : "v"(p) : "memory");
-}
-template <int N>
-__device__ __forceinline__ void wait_rows(f32x4 (&v)[N]) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#pragma unroll
-    for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
+// 16-byte agent-coherent read of y (rows other workgroups wrote with sc1
+// stores): a buffer load with the sc1 policy, so the compiler tracks its
+// completion like any other load. `byte_off` < 2^31 (the y rows of one call).
+__device__ __forceinline__ f32x4 load16_cg(const float* base, size_t byte_off) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, 0x7fffffff, 0x00020000);
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)byte_off, 0, 16 /* sc1 */));
 }
 // 16-byte global -> LDS DMA, agent-coherent read
 __device__ __forceinline__ void load_lds16_cg(const void* src, void* lds_base) {
@@ -324,13 +327,33 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
     const int S = load_cg(prog + b);
     const unsigned rtag = (((unsigned)S >> 12) + 1u) & 0xFFFFFFu;  // routing words of this call
     int k = 0;  // steps published by this workgroup
+    // publish: every wave waits for its own stores (a workgroup barrier does
+    // not), the barrier, then one progress store
     auto publish = [&]() {
-        __syncthreads();  // every wave's stores of the step are complete
+        store_fence();
+        __syncthreads();
         ++k;
         if (tid == 0) {
             fence_wg_release();
             store_cg(prog + b, S + k);
         }
+    };
+    // An item's publish is deferred until the worker's next item has issued its
+    // weights: flush(n) waits for everything but the n loads issued last (the
+    // pending stores are older), so the store acknowledgements come back while
+    // the next weights stream.
+    bool pend = false;
+    auto flush = [&](int n_after) {
+        if (!pend) return;
+        wait_vm_n(n_after);
+        asm volatile("" ::: "memory");
+        __syncthreads();
+        ++k;
+        if (tid == 0) {
+            fence_wg_release();
+            store_cg(prog + b, S + k);
+        }
+        pend = false;
     };
     // wave 0: until, for every lane with want, prog[owner] >= S + step; then the
     // whole workgroup proceeds
@@ -462,6 +485,7 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
             bw0[kt] = *reinterpret_cast<const u32x4*>(a.gate + toff + (size_t)kt * kTileBytes);
             bw1[kt] = *reinterpret_cast<const u32x4*>(a.up + toff + (size_t)kt * kTileBytes);
         }
+        flush(2 * KT);  // the previous item: its stores are older than the A rows and scales
         if (prefetch_cand) cand_prefetch();  // behind the weights: consumed after the item
         wait_vm_n(2 * KT + (prefetch_cand && wave == 0 ? 1 : 0));  // A rows and scales
         if (stage) convert_own_rows<KT>(As, wave, lane);
@@ -514,6 +538,7 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
             bw0[kt] = *reinterpret_cast<const u32x4*>(a.down + toff0 + (size_t)kt * kTileBytes);
             bw1[kt] = *reinterpret_cast<const u32x4*>(a.down + toff1 + (size_t)kt * kTileBytes);
         }
+        flush(2 * KT);  // the previous item (its stores are older than these weights)
         if (wave == 0) {
             int it = 0;
             while (__ballot(want && (int)(pv - (S + pstep)) < 0)) {
@@ -597,7 +622,7 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
                 }
 #pragma unroll
                 for (int h = 0; h < 2; ++h)
-                    if (c0 + 64 * h < H) load16_cg_issue(yv[h * NY + j], a.y + ((size_t)id * T + t) * H + c0 + 64 * h);
+                    if (c0 + 64 * h < H) yv[h * NY + j] = load16_cg(a.y, (((size_t)id * T + t) * H + c0 + 64 * h) * 4);
             }
         }
 #pragma unroll
@@ -605,8 +630,7 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
 #pragma unroll
             for (int h = 0; h < 2; ++h)
                 if (v < V && c0 + 64 * h < H)
-                    load16_cg_issue(yv[h * NY + kMaxTopK + v], a.y + (sh0 + (size_t)v * T + t) * H + c0 + 64 * h);
-        wait_rows(yv);
+                    yv[h * NY + kMaxTopK + v] = load16_cg(a.y, ((sh0 + (size_t)v * T + t) * H + c0 + 64 * h) * 4);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int c = c0 + 64 * h;
@@ -620,15 +644,9 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
             if (V > 0) {
                 f32x4 sh = yv[h * NY + kMaxTopK];
                 for (int v = 1; v < V; ++v) {
-                    f32x4 y2[1];
-                    if (v < 2) {
-                        y2[0] = yv[h * NY + kMaxTopK + 1];
-                    } else {
-                        load16_cg_issue(y2[0], a.y + (sh0 + (size_t)v * T + t) * H + c);
-                        wait_rows(y2);
-                    }
+                    const f32x4 y2 = v < 2 ? yv[h * NY + kMaxTopK + 1] : load16_cg(a.y, ((sh0 + (size_t)v * T + t) * H + c) * 4);
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) sh[q] += y2[0][q];
+                    for (int q = 0; q < 4; ++q) sh[q] += y2[q];
                 }
 #pragma unroll
                 for (int q = 0; q < 4; ++q) acc[q] += sh[q];
@@ -655,7 +673,7 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
             fresh_indices();
             if (i >= ngu_total) break;
             gate_up_item(i / RBG, i % RBG, i + PW >= ngu_total);
-            publish();
+            pend = true;
         }
     }
 
@@ -701,8 +719,9 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
                 step = i / PW + 1;
             },
             RBG);
-        publish();
+        pend = true;
     }
+    flush(0);
     // combine of column block rb by slot (ndn_total + rb) % P, one with the
     // fewest down items, after all of its own (a combine waits only for down
     // items and the router, which never wait for a combine)
