@@ -84,10 +84,15 @@ typedef struct uocr_hip_moe_layer uocr_hip_moe_layer;
  * GpuDecoder::upload_expert_table (src/engine/gpu_decoder.cu:316-358) for the
  * gate/up/down tables plus the router and shared-expert uploads
  * (gpu_decoder.cu:185-187). Requirements: hidden and inter multiples of 128,
- * group_size in {32, 64, 128} dividing inter, symmetric zero point (all
- * zeros == 8, the layout of quantize_int4_symmetric, src/runtime/quant.cpp:82-116),
- * |8 * scale| within the f16 range. Scales are stored as bf16 (exact for
- * bf16-valued scales). Allocates device memory; not for the per-call path. */
+ * group_size in {32, 64, 128} dividing inter; zeros integer-valued in [0, 15]
+ * (quantize_int4_awq's asymmetric layout, src/runtime/quant.cpp:39-80, or the
+ * symmetric zero 8 of quantize_int4_symmetric, quant.cpp:82-116; a layer whose
+ * zeros are all 8 takes the zero-free fast path); |15 * scale| (all-8 zeros:
+ * |8 * scale|) within the f16 range. Scales are stored as f16 (round to
+ * nearest: relative error <= 2^-11 per scale in f16's normal range; exact for
+ * bf16-valued scales there), zeros exactly. Anything else is
+ * UOCR_HIP_EUNSUPPORTED with the reason in uocr_hip_last_error(). Allocates
+ * device memory; not for the per-call path. */
 int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* desc, uocr_hip_moe_layer** out);
 int uocr_hip_moe_layer_destroy(uocr_hip_moe_layer* layer);
 
@@ -261,6 +266,16 @@ int uocr_hip_moe_gemm_int4_tc_pipe(const float* x, const uint8_t* packed, const 
  * last clear routed more than `cap` entries to one expert (only possible when
  * cap < seq). Synchronises the device; clear != 0 resets the flag. */
 int uocr_hip_moe_router_overflow(int clear, int* flag);
+
+/* Host-only check of the fused decode kernel's static schedule (no device
+ * work; no counterpart in the reference, whose decode runs one kernel per
+ * stage): replays the wait/publish program of every workgroup for a grid of
+ * `grid` workgroups, `seq` router workgroups, `n_groups` expert groups of
+ * `rbg` gate/up and `rbd` down items each, and the live groups `live`
+ * (n_live entries, in the kernel's order). UOCR_HIP_OK if every workgroup
+ * finishes and every item is published where the schedule says; else
+ * UOCR_HIP_EINVAL with the first violation in uocr_hip_last_error(). */
+int uocr_hip_fused_schedule_check(int seq, int grid, int n_groups, int rbg, int rbd, const int* live, int n_live);
 
 #ifdef __cplusplus
 }

@@ -11,6 +11,7 @@
 #include <thread>
 #include <vector>
 
+#include "fused_schedule.hpp"
 #include "launch.hpp"
 #include "uocr_hip/moe_capi.h"
 
@@ -805,6 +806,92 @@ int uocr_hip_moe_router_topk(const float* logits, int seq, int n_experts, int to
     g.assign_count = d_count;
     g.cap = cap;
     HIP_TRY(launch_group(g, st), "group launch");
+    return UOCR_HIP_OK;
+}
+
+// Host replay of the fused decode kernel's schedule (FusedSchedule, the same
+// code the kernel runs): every workgroup's program as a sequence of waits and
+// progress publishes -- routers publish once; workers publish one step per
+// gate/up item, then wait for and publish each down item, then wait for their
+// combine blocks -- executed until no workgroup can move. Fails if a workgroup
+// is left waiting (a cycle or an unreachable step), if an item is published by
+// another workgroup or at another step than gu_step / dn_step name, or if the
+// slot mapping is not a bijection.
+int uocr_hip_fused_schedule_check(int seq, int grid, int n_groups, int rbg, int rbd, const int* live, int n_live) {
+    using uocr_hip::FusedSchedule;
+    if (seq < 1 || grid <= seq + 1 || n_groups < 1 || rbg < 1 || rbd < 1 || n_live < 0 || n_live > n_groups ||
+        (n_live > 0 && !live))
+        return fail(UOCR_HIP_EINVAL, "bad schedule shape");
+    const FusedSchedule sch(seq, grid, n_groups, rbg, rbd, n_live);
+    const int T = seq, P = grid;
+    for (int b = 0; b < P; ++b)
+        if (sch.slot_of(b) < 0 || sch.slot_of(b) >= P || sch.slot_wg(sch.slot_of(b)) != b)
+            return fail(UOCR_HIP_EINVAL, "slot mapping is not a bijection at workgroup " + std::to_string(b));
+    struct Act {
+        std::vector<std::pair<int, int>> waits;  // (owner, step)
+        int kind, item;                          // kind 0 router, 1 gate/up, 2 down, 3 combine (no publish)
+    };
+    std::vector<std::vector<Act>> prog(P);
+    for (int b = 0; b < P; ++b) {
+        auto& pr = prog[b];
+        if (b < T) pr.push_back({{}, 0, b});
+        for (int i = b - T; b >= T && i < sch.ngu_total; i += sch.PW) pr.push_back({{}, 1, i});
+        for (int j = sch.slot_of(b); j < sch.ndn_total; j += P) {
+            Act a{{}, 2, j};
+            for (int q = 0; q < rbg; ++q) {
+                int o = 0, st = 0;
+                sch.gu_step(live[j / rbd] * rbg + q, o, st);
+                a.waits.push_back({o, st});
+            }
+            pr.push_back(a);
+        }
+        for (int rb = 0; rb < rbd; ++rb) {
+            if (sch.combine_slot(rb) != sch.slot_of(b)) continue;
+            Act a{{}, 3, rb};
+            for (int q = 0; q < T; ++q) a.waits.push_back({q, 1});
+            for (int q = 0; q < n_live; ++q) {
+                int o = 0, st = 0;
+                sch.dn_step(q * rbd + rb, o, st);
+                a.waits.push_back({o, st});
+            }
+            pr.push_back(a);
+        }
+        int n_gu = 0;
+        for (const Act& a : pr) n_gu += a.kind == 1;
+        if (n_gu != sch.n_gu_of(b))
+            return fail(UOCR_HIP_EINVAL, "n_gu_of disagrees with the items of workgroup " + std::to_string(b));
+    }
+    std::vector<int> done(P, 0), pc(P, 0);
+    for (bool moved = true; moved;) {
+        moved = false;
+        for (int b = 0; b < P; ++b) {
+            while (pc[b] < (int)prog[b].size()) {
+                const Act& a = prog[b][pc[b]];
+                bool ok = true;
+                for (const auto& w : a.waits) ok = ok && w.first >= 0 && w.first < P && done[w.first] >= w.second;
+                if (!ok) break;
+                if (a.kind != 3) {
+                    ++done[b];
+                    int o = b, st = done[b];
+                    if (a.kind == 1) sch.gu_step(a.item, o, st);
+                    if (a.kind == 2) sch.dn_step(a.item, o, st);
+                    if (a.kind == 0 && st != 1) o = -1;
+                    if (o != b || st != done[b])
+                        return fail(UOCR_HIP_EINVAL, "item " + std::to_string(a.item) + " (kind " +
+                                                         std::to_string(a.kind) + ") published by workgroup " +
+                                                         std::to_string(b) + " at step " + std::to_string(done[b]) +
+                                                         ", the schedule names " + std::to_string(o) + " / " +
+                                                         std::to_string(st));
+                }
+                ++pc[b];
+                moved = true;
+            }
+        }
+    }
+    for (int b = 0; b < P; ++b)
+        if (pc[b] < (int)prog[b].size())
+            return fail(UOCR_HIP_EINVAL, "workgroup " + std::to_string(b) + " is left waiting (item kind " +
+                                             std::to_string(prog[b][pc[b]].kind) + ")");
     return UOCR_HIP_OK;
 }
 

@@ -32,6 +32,7 @@
 // stores; act and y rows are indexed by (group, token): g * T + t.
 #include <hip/hip_runtime.h>
 #include "decode_common.hpp"
+#include "fused_schedule.hpp"
 
 #include <algorithm>
 
@@ -377,15 +378,6 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
         fence_wg_acquire();
     };
 
-    // ---- schedule (identical arithmetic in every workgroup)
-    // gate/up item i -> worker T + i % PW, its step i / PW + 1; down item j ->
-    // workgroup j % P, its step n_router + n_gateup + j / P + 1
-    auto n_gu_of = [&](int w, int ngu_total) {
-        if (w < T) return 0;
-        const int q = w - T;
-        return ngu_total > q ? (ngu_total - 1 - q) / PW + 1 : 0;
-    };
-
     bool have_summary = false;
     bool have_x = false;  // As holds all T token rows as f16
     int n_live_r = 0, n_live = 0;
@@ -684,40 +676,17 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
     // the live groups only (the routing summary first).
     need_summary();
     const int n_dn_groups = n_live;
-    const int ndn_total = n_dn_groups * RBD;
+    const FusedSchedule sch(T, P, G, RBG, RBD, n_live);  // identical in every workgroup
+    const int ndn_total = sch.ndn_total;
     // position of gate/up item r of the group at down position gpos
     auto gu_index = [&](int gpos, int r_) { return live[gpos] * RBG + r_; };
-    // Down items go to "slots" in the order the workgroups behind them are
-    // expected to be free: workers with one gate/up item fewer, workers that
-    // are first on their CU (issue priority goes to the older workgroup),
-    // the router workgroups (exact chain), then the rest; a second round of
-    // down items lands on the first slots.
-    const int rem = ngu_total % PW;  // workers T .. T+rem-1 hold one item more
-    const int n1 = PW - rem, nA = max(0, min(rem, P / 2 - T));
-    auto slot_wg = [&](int sl) {
-        if (sl < n1) return T + rem + sl;
-        sl -= n1;
-        if (sl < nA) return T + sl;
-        sl -= nA;
-        if (sl < T) return sl;
-        return T + nA + (sl - T);
-    };
-    const int my_slot = b < T ? n1 + nA + b
-                              : (b - T >= rem ? b - T - rem : (b - T < nA ? n1 + (b - T) : n1 + T + (b - T)));
-    auto dn_step = [&](int j, int& owner, int& step) {
-        owner = slot_wg(j % P);
-        step = (owner < T ? 1 : 0) + n_gu_of(owner, ngu_total) + j / P + 1;
-    };
+    const int my_slot = sch.slot_of(b);
     for (int j = my_slot; j < ndn_total; j += P) {
         fresh_indices();
         const int gpos = j / RBD, rb = j % RBD;
         down_item(
             live[gpos], rb,
-            [&](int q, int& owner, int& step) {
-                const int i = gu_index(gpos, q);
-                owner = T + i % PW;
-                step = i / PW + 1;
-            },
+            [&](int q, int& owner, int& step) { sch.gu_step(gu_index(gpos, q), owner, step); },
             RBG);
         pend = true;
     }
@@ -727,7 +696,7 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
     // items and the router, which never wait for a combine)
     bool have_route = false;
     for (int rb = 0; rb < RBD; ++rb) {
-        if ((ndn_total + rb) % P != my_slot) continue;
+        if (sch.combine_slot(rb) != my_slot) continue;
         if (!have_route) {
             // the exact routing first (done long before the last down items),
             // so that the y rows are one round trip after the down items
@@ -738,7 +707,7 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
             }
             have_route = true;
         }
-        wait_steps([&](int q, int& owner, int& step) { dn_step(q * RBD + rb, owner, step); }, n_dn_groups);
+        wait_steps([&](int q, int& owner, int& step) { sch.dn_step(q * RBD + rb, owner, step); }, n_dn_groups);
         combine_block(rb);
     }
 

@@ -11,6 +11,11 @@
 // expf over every binary32 input is run at build time by gen_expf_fixups.c,
 // which writes the few inputs where this restatement and glibc still disagree
 // into expf_exceptions.h.
+// Provenance: the table values are 2^(i/32) (a mathematical constant set) and
+// the polynomial is the degree-3 fit published in ARM optimized-routines
+// (math/expf.c, exp2f_data.c; Copyright (c) 2017-2018 Arm Limited,
+// SPDX-License-Identifier: MIT OR Apache-2.0 WITH LLVM-exception), the code
+// glibc >= 2.28 ships as sysdeps/ieee754/flt-32/e_expf.c.
 #pragma once
 #include <math.h>
 #include <stdint.h>

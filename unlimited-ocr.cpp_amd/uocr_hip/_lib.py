@@ -59,6 +59,7 @@ SIGNATURES = {
     "uocr_hip_moe_layer_status": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_int)]),
     "uocr_hip_moe_layer_status_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
     "uocr_hip_moe_router_overflow": (C.c_int, [C.c_int, C.POINTER(C.c_int)]),
+    "uocr_hip_fused_schedule_check": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int), C.c_int]),
     "uocr_hip_moe_layer_forward": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
                                               C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
                                               C.c_void_p]),
