@@ -32,6 +32,7 @@ extern "C" {
 #define UOCR_HIP_ENOMEM (-3)      /* device allocation failed (creation calls only) */
 #define UOCR_HIP_EWORKSPACE (-4)  /* caller workspace smaller than the size query */
 #define UOCR_HIP_EHIP (-5)        /* a HIP runtime call failed; see uocr_hip_last_error() */
+#define UOCR_HIP_ENOTFOUND (-6)   /* a named tensor is absent (weight ingest) */
 
 #define UOCR_HIP_DTYPE_F32 0
 #define UOCR_HIP_DTYPE_BF16 1
@@ -76,6 +77,11 @@ typedef struct {
     const uocr_hip_qmatrix* shared_down;       /* [hidden, n_shared*inter] or NULL */
     const float* rms_weight;    /* optional post-attention RMSNorm weight [hidden] */
     float rms_eps;              /* rms_norm_eps */
+    const float* router_f32;    /* optional f32 router [n_experts, hidden]; replaces
+                                   router_bf16 (the router of an AWQ-folded layer,
+                                   weights.cpp:199-207, is f32). Such a layer routes
+                                   with the f32-weight router kernel on every path
+                                   and never takes the fused decode kernel. */
 } uocr_hip_layer_desc;
 
 typedef struct uocr_hip_moe_layer uocr_hip_moe_layer;
@@ -276,6 +282,47 @@ int uocr_hip_moe_router_overflow(int clear, int* flag);
  * finishes and every item is published where the schedule says; else
  * UOCR_HIP_EINVAL with the first violation in uocr_hip_last_error(). */
 int uocr_hip_fused_schedule_check(int seq, int grid, int n_groups, int rbg, int rbd, const int* live, int n_live);
+
+/* ---- Weight ingest (host only, no device work) ----
+ * A safetensors file read whole into host memory: the counterpart of
+ * uocr::SafetensorsFile (src/runtime/safetensors.cpp:30-137). Names, dtypes
+ * (F32/BF16/F16/I32/I8/U8/I4/U4), shapes and the string-valued "__metadata__"
+ * entries as the reference reads them. */
+typedef struct uocr_hip_st_file uocr_hip_st_file;
+int uocr_hip_st_open(const char* path, uocr_hip_st_file** out);
+int uocr_hip_st_close(uocr_hip_st_file* file);
+int uocr_hip_st_contains(const uocr_hip_st_file* file, const char* name); /* 1 or 0 */
+int uocr_hip_st_numel(const uocr_hip_st_file* file, const char* name, size_t* n);
+/* SafetensorsFile::read_f32 (safetensors.cpp:88-127): F32/BF16/F16/I32/I8/U8
+ * converted to f32 into dst (n must equal the tensor's element count). */
+int uocr_hip_st_read_f32(const uocr_hip_st_file* file, const char* name, float* dst, size_t n);
+/* SafetensorsFile::read_u8 (safetensors.cpp:129-137): U8/I8 bytes. */
+int uocr_hip_st_read_u8(const uocr_hip_st_file* file, const char* name, uint8_t* dst, size_t n);
+/* *value = the metadata string for key, or NULL (valid until close). */
+int uocr_hip_st_metadata(const uocr_hip_st_file* file, const char* key, const char** value);
+
+/* Group size of a pre-quantized (GPTQ) file: the integer "group" of its
+ * "uocr_int4" JSON metadata, else fallback_group (weights.cpp:140-151). */
+int uocr_hip_gptq_group(const uocr_hip_st_file* file, int fallback_group);
+/* make_quantized's pre-quantized branch (weights.cpp:138-165): the INT4 matrix
+ * <weight_name>.packed (U8 [rows, ceil(cols/2)]), .scales and .zeros (F32
+ * [rows, ceil(cols/group)]) with the file's group, as a uocr_hip_qmatrix whose
+ * arrays the file owns until uocr_hip_st_close. rows/cols are the dense
+ * weight's shape (the checkpoint tensor's, weights.cpp:132-135). Returns
+ * UOCR_HIP_ENOTFOUND if <weight_name>.packed is absent (the reference then
+ * quantizes the dense weight itself), UOCR_HIP_EINVAL on the reference's
+ * element-count mismatches. */
+int uocr_hip_gptq_qmatrix(const uocr_hip_st_file* file, const char* weight_name, int rows, int cols,
+                          int fallback_group, uocr_hip_qmatrix* out);
+/* AWQ expert input scale (apply_expert_input_scale, weights.cpp:199-207) for
+ * the tensors this layer takes: rms_weight[j] /= s[j] in place, and the bf16
+ * router materialised as f32 with column c times s[c] into router_f32
+ * [n_experts, hidden] (pass it as uocr_hip_layer_desc.router_f32). The shared
+ * gate/up columns take uocr_hip_scale_columns_f32 on their f32 values. */
+int uocr_hip_fold_expert_input_scale(const float* s, int hidden, float* rms_weight, const uint16_t* router_bf16,
+                                     int n_experts, float* router_f32);
+/* scale_columns (weights.cpp:185-197): out[r, c] = w[r, c] * s[c]. */
+int uocr_hip_scale_columns_f32(const float* w, int rows, int cols, const float* s, float* out);
 
 #ifdef __cplusplus
 }

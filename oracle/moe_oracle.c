@@ -291,6 +291,24 @@ void orc_moe_gate_f32router(const float* x, const float* router_f32, int rows, i
     free(logits);
 }
 
+/* src/runtime/weights.cpp:185-197 (scale_columns): the matrix as f32, column c
+ * times s[c], one rounding per element. */
+void orc_scale_columns(const float* w, int rows, int cols, const float* s, float* out) {
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c) out[(size_t)r * cols + c] = w[(size_t)r * cols + c] * s[c];
+}
+
+/* src/runtime/weights.cpp:199-207 (apply_expert_input_scale), for the norm and
+ * the router: norm[j] /= s[j]; router = scale_columns(bf16 -> f32 router, s).
+ * The shared gate/up take orc_scale_columns on their f32 values. */
+void orc_fold_expert_input_scale(const float* s, int hidden, float* rms_weight,
+                                 const uint16_t* router_bf16, int n_experts, float* router_f32) {
+    for (int j = 0; j < hidden; ++j) rms_weight[j] /= s[j];
+    for (int e = 0; e < n_experts; ++e)
+        for (int c = 0; c < hidden; ++c)
+            router_f32[(size_t)e * hidden + c] = orc_bf16_to_f32(router_bf16[(size_t)e * hidden + c]) * s[c];
+}
+
 /* src/engine/gpu_decoder.cu:602-609: for t, for j: e_tokens[ids[t,j]].push_back(t)
  * -- a stable counting sort of the (t, j) entries by expert. */
 void orc_stable_group(const int* ids, int seq, int top_k, int n_experts, int* counts,
@@ -365,8 +383,12 @@ void orc_moe_layer(const orc_layer* L, const float* h, int seq, const int* sel, 
         orc_rmsnorm(h, L->rms_weight, xn, seq, H, L->rms_eps);
         x = xn;
     }
-    orc_moe_gate(x, L->router_bf16, seq, H, L->n_experts, L->top_k, L->norm_topk_prob,
-                 L->routed_scaling_factor, L->scoring_sigmoid, ids, weights);
+    if (L->router_f32)
+        orc_moe_gate_f32router(x, L->router_f32, seq, H, L->n_experts, L->top_k, L->norm_topk_prob,
+                               L->routed_scaling_factor, L->scoring_sigmoid, ids, weights);
+    else
+        orc_moe_gate(x, L->router_bf16, seq, H, L->n_experts, L->top_k, L->norm_topk_prob,
+                     L->routed_scaling_factor, L->scoring_sigmoid, ids, weights);
     const int n = sel ? n_sel : seq;
     (void)threads;
 #pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1)

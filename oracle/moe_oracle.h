@@ -51,6 +51,8 @@ typedef struct {
     orc_qmatrix shared_gate, shared_up, shared_down;
     const float* rms_weight;         /* optional post-attention RMSNorm weight [hidden] */
     float rms_eps;
+    const float* router_f32;         /* optional f32 router [n_experts, hidden] (an AWQ-folded
+                                        router, weights.cpp:185-207); replaces router_bf16 */
 } orc_layer;
 
 float orc_bf16_to_f32(uint16_t h);
@@ -78,6 +80,14 @@ void orc_moe_gate(const float* x, const uint16_t* router_bf16, int rows, int hid
 void orc_moe_gate_f32router(const float* x, const float* router_f32, int rows, int hidden,
                             int n_experts, int top_k, int norm_topk_prob, float scaling,
                             int sigmoid, int* ids, float* weights);
+
+/* AWQ expert input scale, src/runtime/weights.cpp:185-207: the post-attention
+ * norm weight divided by s (in place), the bf16 router materialised as f32
+ * with column c multiplied by s[c] (router_f32 [n_experts, hidden]). */
+void orc_fold_expert_input_scale(const float* s, int hidden, float* rms_weight,
+                                 const uint16_t* router_bf16, int n_experts, float* router_f32);
+/* weights.cpp:185-197: out[r, c] = w[r, c] * s[c] (w already materialised as f32). */
+void orc_scale_columns(const float* w, int rows, int cols, const float* s, float* out);
 
 void orc_stable_group(const int* ids, int seq, int top_k, int n_experts, int* counts,
                       int* offsets, int* perm_token, int* perm_j);

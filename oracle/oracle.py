@@ -33,7 +33,8 @@ class LayerC(C.Structure):
                 ("routed_scaling_factor", C.c_float), ("scoring_sigmoid", C.c_int),
                 ("router_bf16", C.c_void_p), ("gate", C.POINTER(QMatC)), ("up", C.POINTER(QMatC)),
                 ("down", C.POINTER(QMatC)), ("shared_gate", QMatC), ("shared_up", QMatC),
-                ("shared_down", QMatC), ("rms_weight", C.c_void_p), ("rms_eps", C.c_float)]
+                ("shared_down", QMatC), ("rms_weight", C.c_void_p), ("rms_eps", C.c_float),
+                ("router_f32", C.c_void_p)]
 
 
 def build():
@@ -61,6 +62,8 @@ def lib():
         L.orc_softmax.argtypes = [f32p, C.c_int, C.c_int]
         L.orc_silu_mul.argtypes = [f32p, f32p, f32p, C.c_longlong]
         L.orc_rmsnorm.argtypes = [f32p, f32p, f32p, C.c_int, C.c_int, C.c_float]
+        L.orc_fold_expert_input_scale.argtypes = [f32p, C.c_int, f32p, u16p, C.c_int, f32p]
+        L.orc_scale_columns.argtypes = [f32p, C.c_int, C.c_int, f32p, f32p]
         L.orc_moe_gate.argtypes = [f32p, u16p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                    C.c_float, C.c_int, i32p, f32p]
         L.orc_moe_gate_f32router.argtypes = [f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int,
@@ -156,6 +159,24 @@ def stable_group(ids, n_experts):
     return counts, offs, perm
 
 
+def fold_expert_input_scale(s, rms_weight, router_bf16):
+    """weights.cpp:199-207 for the norm and the router: returns (rms_weight / s,
+    f32 router with column c times s[c])."""
+    s = np.ascontiguousarray(s, np.float32)
+    rms = np.array(rms_weight, np.float32, copy=True)
+    rb = np.ascontiguousarray(router_bf16, np.uint16)
+    rf = np.empty(rb.shape, np.float32)
+    lib().orc_fold_expert_input_scale(s, len(s), rms, rb, rb.shape[0], rf)
+    return rms, rf
+
+
+def scale_columns(w, s):
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(w)
+    lib().orc_scale_columns(w, w.shape[0], w.shape[1], np.ascontiguousarray(s, np.float32), out)
+    return out
+
+
 def rmsnorm(x, w, eps):
     x = np.ascontiguousarray(x, np.float32)
     out = np.empty_like(x)
@@ -181,9 +202,14 @@ def layer_c(L):
     if L.rms_weight is not None:
         rms = np.ascontiguousarray(L.rms_weight, np.float32)
         keep.append(rms)
+    rf = getattr(L, "router_f32", None)
+    if rf is not None:
+        rf = np.ascontiguousarray(rf, np.float32)
+        keep.append(rf)
     lc = LayerC(L.hidden, L.inter, L.n_shared * L.inter, E, L.top_k, L.norm_topk_prob,
                 L.routed_scaling_factor, L.scoring_sigmoid, router.ctypes.data, gate, up, down,
-                sg, su, sd, rms.ctypes.data if rms is not None else None, L.rms_eps)
+                sg, su, sd, rms.ctypes.data if rms is not None else None, L.rms_eps,
+                rf.ctypes.data if rf is not None else None)
     return lc, keep
 
 

@@ -241,7 +241,7 @@ bool use_prefill(const uocr_hip_moe_layer* L, int seq) {
 constexpr int kDenseMinSeq = 12;
 
 bool use_fused(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
-    return L->sync && seq >= kDenseMinSeq && seq <= kFusedMaxSeq && x_dtype == UOCR_HIP_DTYPE_BF16 &&
+    return L->sync && L->router_t && seq >= kDenseMinSeq && seq <= kFusedMaxSeq && x_dtype == UOCR_HIP_DTYPE_BF16 &&
            !L->rms_weight &&
            decode_fused_ok(L->hidden, L->inter, L->group) && L->n_experts + L->n_virtual <= kMaxExperts;
 }
@@ -306,7 +306,8 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
     if (d->top_k <= 0 || d->top_k > kMaxTopK || d->top_k > E)
         return fail(UOCR_HIP_EINVAL, "top_k must be in [1, min(8, n_experts)]");
     if (d->n_shared < 0 || E + d->n_shared > kMaxExperts) return fail(UOCR_HIP_EINVAL, "bad n_shared");
-    if (!d->router_bf16 || !d->gate || !d->up || !d->down) return fail(UOCR_HIP_EINVAL, "null weight pointer");
+    if ((!d->router_bf16 && !d->router_f32) || !d->gate || !d->up || !d->down)
+        return fail(UOCR_HIP_EINVAL, "null weight pointer");
     const int G = d->gate[0].group_size;
     if (G != 32 && G != 64 && G != 128) return fail(UOCR_HIP_EUNSUPPORTED, "group_size must be 32, 64 or 128");
     int rc;
@@ -405,11 +406,16 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
             return fail(codes[e], m);
         }
 
-    // router W as [H/8][E][8] so lane e's 16-byte loads are coalesced across the wave
-    std::vector<uint16_t> rt((size_t)H * E);
-    for (int c8 = 0; c8 < H / 8; ++c8)
-        for (int e = 0; e < E; ++e)
-            for (int i = 0; i < 8; ++i) rt[((size_t)c8 * E + e) * 8 + i] = d->router_bf16[(size_t)e * H + c8 * 8 + i];
+    // router W (bf16) as [H/8][E][8] so lane e's 16-byte loads are coalesced
+    // across the wave; an f32 router has no bf16 form (its layer takes the
+    // f32-weight router on every path)
+    std::vector<uint16_t> rt;
+    if (!d->router_f32) {
+        rt.resize((size_t)H * E);
+        for (int c8 = 0; c8 < H / 8; ++c8)
+            for (int e = 0; e < E; ++e)
+                for (int i = 0; i < 8; ++i) rt[((size_t)c8 * E + e) * 8 + i] = d->router_bf16[(size_t)e * H + c8 * 8 + i];
+    }
 
     // and as f32 [H/4][64][4] for the decode router (experts padded to 64 with
     // zeros, so a 64-column chunk is one contiguous 16 KiB block)
@@ -417,8 +423,15 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
     for (int c4 = 0; c4 < H / 4; ++c4)
         for (int e = 0; e < E; ++e)
             for (int i = 0; i < 4; ++i) {
-                const uint32_t bits = (uint32_t)d->router_bf16[(size_t)e * H + c4 * 4 + i] << 16;
-                std::memcpy(&rf[((size_t)c4 * 64 + e) * 4 + i], &bits, 4);
+                const size_t src = (size_t)e * H + c4 * 4 + i;
+                float v;
+                if (d->router_f32) {
+                    v = d->router_f32[src];
+                } else {
+                    const uint32_t bits = (uint32_t)d->router_bf16[src] << 16;
+                    std::memcpy(&v, &bits, 4);
+                }
+                rf[((size_t)c4 * 64 + e) * 4 + i] = v;
             }
 
     auto up_copy = [&](void** dst, const void* src, size_t bytes, const char* what) -> int {
@@ -429,7 +442,7 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
         L->device_bytes += bytes;
         return UOCR_HIP_OK;
     };
-    if ((rc = up_copy((void**)&L->router_t, rt.data(), rt.size() * 2, "router")) ||
+    if ((!rt.empty() && (rc = up_copy((void**)&L->router_t, rt.data(), rt.size() * 2, "router"))) ||
         (rc = up_copy((void**)&L->router_f32, rf.data(), rf.size() * 4, "router f32")) ||
         (rc = up_copy((void**)&L->gate, hg.data(), hg.size(), "gate")) ||
         (rc = up_copy((void**)&L->up, hu.data(), hu.size(), "up")) ||
@@ -557,6 +570,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
         da.rms_weight = L->rms_weight;
         da.rms_eps = L->rms_eps;
         da.router_f32 = L->router_f32;
+        da.router_unfused = L->router_t == nullptr;
         da.router_t = L->router_t;
         da.norm_topk_prob = L->norm_topk_prob;
         da.scoring_sigmoid = L->scoring_sigmoid;
@@ -588,7 +602,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
             if (timing) Lm->pending = true;
             return UOCR_HIP_OK;
         }
-        if (seq <= kRouterDecodeMaxSeq) {
+        if (seq <= kRouterDecodeMaxSeq || !L->router_t) {
             HIP_TRY(launch_router_decode(da, st), "router launch");
         } else {
             RouterArgs ra{};
@@ -654,7 +668,32 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     g.lrank = (int*)(ws + p.lrank);
     g.chunk_count = (int*)(ws + p.chunk_count);
     g.chunk_base = (int*)(ws + p.chunk_base);
-    HIP_TRY(launch_router(ra, x_dtype == UOCR_HIP_DTYPE_BF16, st), "router launch");
+    if (L->router_t) {
+        HIP_TRY(launch_router(ra, x_dtype == UOCR_HIP_DTYPE_BF16, st), "router launch");
+    } else {
+        // f32 router: the per-token f32-weight router (same outputs)
+        DecodeArgs da{};
+        da.x = x;
+        da.x_bf16 = x_dtype == UOCR_HIP_DTYPE_BF16;
+        da.seq = seq;
+        da.hidden = L->hidden;
+        da.inter = L->inter;
+        da.n_experts = L->n_experts;
+        da.top_k = L->top_k;
+        da.n_virtual = L->n_virtual;
+        da.group = L->group;
+        da.rms_weight = L->rms_weight;
+        da.rms_eps = L->rms_eps;
+        da.router_f32 = L->router_f32;
+        da.router_unfused = L->router_t == nullptr;
+        da.norm_topk_prob = L->norm_topk_prob;
+        da.scoring_sigmoid = L->scoring_sigmoid;
+        da.scaling = L->scaling;
+        da.x16 = x16;
+        da.ids = ids;
+        da.wts = wts;
+        HIP_TRY(launch_router_decode(da, st), "router launch");
+    }
     stage(1);
     HIP_TRY(launch_group(g, st), "group launch");
     stage(2);

@@ -375,6 +375,240 @@ __device__ __forceinline__ void router_select(const DecodeArgs& a, int t, float 
     }
 }
 
+// One 128-column chunk of the router chain (lane e: its expert, columns
+// ascending) with the multiply-accumulate step MAC(x, w) spelled by the caller.
+#define UOCR_RCHUNK(MAC) \
+    "s_waitcnt lgkmcnt(0)\n" \
+    "ds_read_b128 v[64:67], %[w] offset:0\n" \
+    "ds_read_b128 v[68:71], %[x] offset:0\n" \
+    "ds_read_b128 v[72:75], %[w] offset:1024\n" \
+    "ds_read_b128 v[76:79], %[x] offset:16\n" \
+    "ds_read_b128 v[80:83], %[w] offset:2048\n" \
+    "ds_read_b128 v[84:87], %[x] offset:32\n" \
+    "ds_read_b128 v[88:91], %[w] offset:3072\n" \
+    "ds_read_b128 v[92:95], %[x] offset:48\n" \
+    "ds_read_b128 v[96:99], %[w] offset:4096\n" \
+    "ds_read_b128 v[100:103], %[x] offset:64\n" \
+    "ds_read_b128 v[104:107], %[w] offset:5120\n" \
+    "ds_read_b128 v[108:111], %[x] offset:80\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v68", "v64") \
+    MAC("v69", "v65") \
+    MAC("v70", "v66") \
+    MAC("v71", "v67") \
+    "ds_read_b128 v[64:67], %[w] offset:6144\n" \
+    "ds_read_b128 v[68:71], %[x] offset:96\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v76", "v72") \
+    MAC("v77", "v73") \
+    MAC("v78", "v74") \
+    MAC("v79", "v75") \
+    "ds_read_b128 v[72:75], %[w] offset:7168\n" \
+    "ds_read_b128 v[76:79], %[x] offset:112\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v84", "v80") \
+    MAC("v85", "v81") \
+    MAC("v86", "v82") \
+    MAC("v87", "v83") \
+    "ds_read_b128 v[80:83], %[w] offset:8192\n" \
+    "ds_read_b128 v[84:87], %[x] offset:128\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v92", "v88") \
+    MAC("v93", "v89") \
+    MAC("v94", "v90") \
+    MAC("v95", "v91") \
+    "ds_read_b128 v[88:91], %[w] offset:9216\n" \
+    "ds_read_b128 v[92:95], %[x] offset:144\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v100", "v96") \
+    MAC("v101", "v97") \
+    MAC("v102", "v98") \
+    MAC("v103", "v99") \
+    "ds_read_b128 v[96:99], %[w] offset:10240\n" \
+    "ds_read_b128 v[100:103], %[x] offset:160\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v108", "v104") \
+    MAC("v109", "v105") \
+    MAC("v110", "v106") \
+    MAC("v111", "v107") \
+    "ds_read_b128 v[104:107], %[w] offset:11264\n" \
+    "ds_read_b128 v[108:111], %[x] offset:176\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v68", "v64") \
+    MAC("v69", "v65") \
+    MAC("v70", "v66") \
+    MAC("v71", "v67") \
+    "ds_read_b128 v[64:67], %[w] offset:12288\n" \
+    "ds_read_b128 v[68:71], %[x] offset:192\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v76", "v72") \
+    MAC("v77", "v73") \
+    MAC("v78", "v74") \
+    MAC("v79", "v75") \
+    "ds_read_b128 v[72:75], %[w] offset:13312\n" \
+    "ds_read_b128 v[76:79], %[x] offset:208\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v84", "v80") \
+    MAC("v85", "v81") \
+    MAC("v86", "v82") \
+    MAC("v87", "v83") \
+    "ds_read_b128 v[80:83], %[w] offset:14336\n" \
+    "ds_read_b128 v[84:87], %[x] offset:224\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v92", "v88") \
+    MAC("v93", "v89") \
+    MAC("v94", "v90") \
+    MAC("v95", "v91") \
+    "ds_read_b128 v[88:91], %[w] offset:15360\n" \
+    "ds_read_b128 v[92:95], %[x] offset:240\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v100", "v96") \
+    MAC("v101", "v97") \
+    MAC("v102", "v98") \
+    MAC("v103", "v99") \
+    "ds_read_b128 v[96:99], %[w] offset:16384\n" \
+    "ds_read_b128 v[100:103], %[x] offset:256\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v108", "v104") \
+    MAC("v109", "v105") \
+    MAC("v110", "v106") \
+    MAC("v111", "v107") \
+    "ds_read_b128 v[104:107], %[w] offset:17408\n" \
+    "ds_read_b128 v[108:111], %[x] offset:272\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v68", "v64") \
+    MAC("v69", "v65") \
+    MAC("v70", "v66") \
+    MAC("v71", "v67") \
+    "ds_read_b128 v[64:67], %[w] offset:18432\n" \
+    "ds_read_b128 v[68:71], %[x] offset:288\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v76", "v72") \
+    MAC("v77", "v73") \
+    MAC("v78", "v74") \
+    MAC("v79", "v75") \
+    "ds_read_b128 v[72:75], %[w] offset:19456\n" \
+    "ds_read_b128 v[76:79], %[x] offset:304\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v84", "v80") \
+    MAC("v85", "v81") \
+    MAC("v86", "v82") \
+    MAC("v87", "v83") \
+    "ds_read_b128 v[80:83], %[w] offset:20480\n" \
+    "ds_read_b128 v[84:87], %[x] offset:320\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v92", "v88") \
+    MAC("v93", "v89") \
+    MAC("v94", "v90") \
+    MAC("v95", "v91") \
+    "ds_read_b128 v[88:91], %[w] offset:21504\n" \
+    "ds_read_b128 v[92:95], %[x] offset:336\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v100", "v96") \
+    MAC("v101", "v97") \
+    MAC("v102", "v98") \
+    MAC("v103", "v99") \
+    "ds_read_b128 v[96:99], %[w] offset:22528\n" \
+    "ds_read_b128 v[100:103], %[x] offset:352\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v108", "v104") \
+    MAC("v109", "v105") \
+    MAC("v110", "v106") \
+    MAC("v111", "v107") \
+    "ds_read_b128 v[104:107], %[w] offset:23552\n" \
+    "ds_read_b128 v[108:111], %[x] offset:368\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v68", "v64") \
+    MAC("v69", "v65") \
+    MAC("v70", "v66") \
+    MAC("v71", "v67") \
+    "ds_read_b128 v[64:67], %[w] offset:24576\n" \
+    "ds_read_b128 v[68:71], %[x] offset:384\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v76", "v72") \
+    MAC("v77", "v73") \
+    MAC("v78", "v74") \
+    MAC("v79", "v75") \
+    "ds_read_b128 v[72:75], %[w] offset:25600\n" \
+    "ds_read_b128 v[76:79], %[x] offset:400\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v84", "v80") \
+    MAC("v85", "v81") \
+    MAC("v86", "v82") \
+    MAC("v87", "v83") \
+    "ds_read_b128 v[80:83], %[w] offset:26624\n" \
+    "ds_read_b128 v[84:87], %[x] offset:416\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v92", "v88") \
+    MAC("v93", "v89") \
+    MAC("v94", "v90") \
+    MAC("v95", "v91") \
+    "ds_read_b128 v[88:91], %[w] offset:27648\n" \
+    "ds_read_b128 v[92:95], %[x] offset:432\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v100", "v96") \
+    MAC("v101", "v97") \
+    MAC("v102", "v98") \
+    MAC("v103", "v99") \
+    "ds_read_b128 v[96:99], %[w] offset:28672\n" \
+    "ds_read_b128 v[100:103], %[x] offset:448\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v108", "v104") \
+    MAC("v109", "v105") \
+    MAC("v110", "v106") \
+    MAC("v111", "v107") \
+    "ds_read_b128 v[104:107], %[w] offset:29696\n" \
+    "ds_read_b128 v[108:111], %[x] offset:464\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v68", "v64") \
+    MAC("v69", "v65") \
+    MAC("v70", "v66") \
+    MAC("v71", "v67") \
+    "ds_read_b128 v[64:67], %[w] offset:30720\n" \
+    "ds_read_b128 v[68:71], %[x] offset:480\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v76", "v72") \
+    MAC("v77", "v73") \
+    MAC("v78", "v74") \
+    MAC("v79", "v75") \
+    "ds_read_b128 v[72:75], %[w] offset:31744\n" \
+    "ds_read_b128 v[76:79], %[x] offset:496\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v84", "v80") \
+    MAC("v85", "v81") \
+    MAC("v86", "v82") \
+    MAC("v87", "v83") \
+    "s_waitcnt lgkmcnt(8)\n" \
+    MAC("v92", "v88") \
+    MAC("v93", "v89") \
+    MAC("v94", "v90") \
+    MAC("v95", "v91") \
+    "s_waitcnt lgkmcnt(6)\n" \
+    MAC("v100", "v96") \
+    MAC("v101", "v97") \
+    MAC("v102", "v98") \
+    MAC("v103", "v99") \
+    "s_waitcnt lgkmcnt(4)\n" \
+    MAC("v108", "v104") \
+    MAC("v109", "v105") \
+    MAC("v110", "v106") \
+    MAC("v111", "v107") \
+    "s_waitcnt lgkmcnt(2)\n" \
+    MAC("v68", "v64") \
+    MAC("v69", "v65") \
+    MAC("v70", "v66") \
+    MAC("v71", "v67") \
+    "s_waitcnt lgkmcnt(0)\n" \
+    MAC("v76", "v72") \
+    MAC("v77", "v73") \
+    MAC("v78", "v74") \
+    MAC("v79", "v75")
+// fused step: acc = fma(x, w, acc) (the reference's contracted bf16 chain)
+#define UOCR_RMAC_FMA(X, W) "v_fmac_f32 %[acc], " X ", " W "\n"
+// unfused step: acc = acc + round(x * w) (the reference's f32 matmul_t, whose
+// build does not contract the loop; src/kernels/cpu_ops.cpp:11-24)
+#define UOCR_RMAC_SEP(X, W) "v_mul_f32 v112, " X ", " W "\nv_add_f32 %[acc], %[acc], v112\n"
+
 // One token's routing by one 256-thread workgroup: rsmem = RING chunks of the
 // router matrix, then the token row as f32 (H floats), then H + 32 floats of
 // scratch for the RMSNorm. Waves 1..3 return after
@@ -483,9 +717,11 @@ __device__ __forceinline__ void router_token(const DecodeArgs& a, int t, unsigne
             *reinterpret_cast<f16x8*>(a.x16 + (size_t)t * H + c) = h;
         }
 
-    // logits: lane e of wave 0 runs the reference's sequential fmaf chain,
-    // columns ascending (src/kernels/cpu_ops.cpp:26-39, contracted by the
-    // -march=native build). Waves 1..3 keep the ring filled; wave 0 only
+    // logits: lane e of wave 0 runs the reference's sequential chain, columns
+    // ascending: fmaf steps for a bf16 router (matmul_t_bf16,
+    // src/kernels/cpu_ops.cpp:26-39, contracted by the -march=native build),
+    // acc + round(x * w) for an f32 router (matmul_t, cpu_ops.cpp:11-24, whose
+    // build leaves the loop uncontracted; H % 4 == 0 here, so no fused tail). Waves 1..3 keep the ring filled; wave 0 only
     // computes.
     float acc = 0.0f;
     const int my_loads = wave == 0 ? 0 : router_loads_of(wave);
@@ -502,235 +738,17 @@ __device__ __forceinline__ void router_token(const DecodeArgs& a, int t, unsigne
             // schedule waits for every read pair)
             const uint32_t w_addr = lds_addr(ring + (size_t)(ch % RING) * kRChunkBytes) + lane * 16;
             const uint32_t x_addr = lds_addr(xs + ch * kRChunkCols);
-            asm volatile(
-                "s_waitcnt lgkmcnt(0)\n"
-                "ds_read_b128 v[64:67], %[w] offset:0\n"
-                "ds_read_b128 v[68:71], %[x] offset:0\n"
-                "ds_read_b128 v[72:75], %[w] offset:1024\n"
-                "ds_read_b128 v[76:79], %[x] offset:16\n"
-                "ds_read_b128 v[80:83], %[w] offset:2048\n"
-                "ds_read_b128 v[84:87], %[x] offset:32\n"
-                "ds_read_b128 v[88:91], %[w] offset:3072\n"
-                "ds_read_b128 v[92:95], %[x] offset:48\n"
-                "ds_read_b128 v[96:99], %[w] offset:4096\n"
-                "ds_read_b128 v[100:103], %[x] offset:64\n"
-                "ds_read_b128 v[104:107], %[w] offset:5120\n"
-                "ds_read_b128 v[108:111], %[x] offset:80\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v68, v64\n"
-                "v_fmac_f32 %[acc], v69, v65\n"
-                "v_fmac_f32 %[acc], v70, v66\n"
-                "v_fmac_f32 %[acc], v71, v67\n"
-                "ds_read_b128 v[64:67], %[w] offset:6144\n"
-                "ds_read_b128 v[68:71], %[x] offset:96\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v76, v72\n"
-                "v_fmac_f32 %[acc], v77, v73\n"
-                "v_fmac_f32 %[acc], v78, v74\n"
-                "v_fmac_f32 %[acc], v79, v75\n"
-                "ds_read_b128 v[72:75], %[w] offset:7168\n"
-                "ds_read_b128 v[76:79], %[x] offset:112\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v84, v80\n"
-                "v_fmac_f32 %[acc], v85, v81\n"
-                "v_fmac_f32 %[acc], v86, v82\n"
-                "v_fmac_f32 %[acc], v87, v83\n"
-                "ds_read_b128 v[80:83], %[w] offset:8192\n"
-                "ds_read_b128 v[84:87], %[x] offset:128\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v92, v88\n"
-                "v_fmac_f32 %[acc], v93, v89\n"
-                "v_fmac_f32 %[acc], v94, v90\n"
-                "v_fmac_f32 %[acc], v95, v91\n"
-                "ds_read_b128 v[88:91], %[w] offset:9216\n"
-                "ds_read_b128 v[92:95], %[x] offset:144\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v100, v96\n"
-                "v_fmac_f32 %[acc], v101, v97\n"
-                "v_fmac_f32 %[acc], v102, v98\n"
-                "v_fmac_f32 %[acc], v103, v99\n"
-                "ds_read_b128 v[96:99], %[w] offset:10240\n"
-                "ds_read_b128 v[100:103], %[x] offset:160\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v108, v104\n"
-                "v_fmac_f32 %[acc], v109, v105\n"
-                "v_fmac_f32 %[acc], v110, v106\n"
-                "v_fmac_f32 %[acc], v111, v107\n"
-                "ds_read_b128 v[104:107], %[w] offset:11264\n"
-                "ds_read_b128 v[108:111], %[x] offset:176\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v68, v64\n"
-                "v_fmac_f32 %[acc], v69, v65\n"
-                "v_fmac_f32 %[acc], v70, v66\n"
-                "v_fmac_f32 %[acc], v71, v67\n"
-                "ds_read_b128 v[64:67], %[w] offset:12288\n"
-                "ds_read_b128 v[68:71], %[x] offset:192\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v76, v72\n"
-                "v_fmac_f32 %[acc], v77, v73\n"
-                "v_fmac_f32 %[acc], v78, v74\n"
-                "v_fmac_f32 %[acc], v79, v75\n"
-                "ds_read_b128 v[72:75], %[w] offset:13312\n"
-                "ds_read_b128 v[76:79], %[x] offset:208\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v84, v80\n"
-                "v_fmac_f32 %[acc], v85, v81\n"
-                "v_fmac_f32 %[acc], v86, v82\n"
-                "v_fmac_f32 %[acc], v87, v83\n"
-                "ds_read_b128 v[80:83], %[w] offset:14336\n"
-                "ds_read_b128 v[84:87], %[x] offset:224\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v92, v88\n"
-                "v_fmac_f32 %[acc], v93, v89\n"
-                "v_fmac_f32 %[acc], v94, v90\n"
-                "v_fmac_f32 %[acc], v95, v91\n"
-                "ds_read_b128 v[88:91], %[w] offset:15360\n"
-                "ds_read_b128 v[92:95], %[x] offset:240\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v100, v96\n"
-                "v_fmac_f32 %[acc], v101, v97\n"
-                "v_fmac_f32 %[acc], v102, v98\n"
-                "v_fmac_f32 %[acc], v103, v99\n"
-                "ds_read_b128 v[96:99], %[w] offset:16384\n"
-                "ds_read_b128 v[100:103], %[x] offset:256\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v108, v104\n"
-                "v_fmac_f32 %[acc], v109, v105\n"
-                "v_fmac_f32 %[acc], v110, v106\n"
-                "v_fmac_f32 %[acc], v111, v107\n"
-                "ds_read_b128 v[104:107], %[w] offset:17408\n"
-                "ds_read_b128 v[108:111], %[x] offset:272\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v68, v64\n"
-                "v_fmac_f32 %[acc], v69, v65\n"
-                "v_fmac_f32 %[acc], v70, v66\n"
-                "v_fmac_f32 %[acc], v71, v67\n"
-                "ds_read_b128 v[64:67], %[w] offset:18432\n"
-                "ds_read_b128 v[68:71], %[x] offset:288\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v76, v72\n"
-                "v_fmac_f32 %[acc], v77, v73\n"
-                "v_fmac_f32 %[acc], v78, v74\n"
-                "v_fmac_f32 %[acc], v79, v75\n"
-                "ds_read_b128 v[72:75], %[w] offset:19456\n"
-                "ds_read_b128 v[76:79], %[x] offset:304\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v84, v80\n"
-                "v_fmac_f32 %[acc], v85, v81\n"
-                "v_fmac_f32 %[acc], v86, v82\n"
-                "v_fmac_f32 %[acc], v87, v83\n"
-                "ds_read_b128 v[80:83], %[w] offset:20480\n"
-                "ds_read_b128 v[84:87], %[x] offset:320\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v92, v88\n"
-                "v_fmac_f32 %[acc], v93, v89\n"
-                "v_fmac_f32 %[acc], v94, v90\n"
-                "v_fmac_f32 %[acc], v95, v91\n"
-                "ds_read_b128 v[88:91], %[w] offset:21504\n"
-                "ds_read_b128 v[92:95], %[x] offset:336\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v100, v96\n"
-                "v_fmac_f32 %[acc], v101, v97\n"
-                "v_fmac_f32 %[acc], v102, v98\n"
-                "v_fmac_f32 %[acc], v103, v99\n"
-                "ds_read_b128 v[96:99], %[w] offset:22528\n"
-                "ds_read_b128 v[100:103], %[x] offset:352\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v108, v104\n"
-                "v_fmac_f32 %[acc], v109, v105\n"
-                "v_fmac_f32 %[acc], v110, v106\n"
-                "v_fmac_f32 %[acc], v111, v107\n"
-                "ds_read_b128 v[104:107], %[w] offset:23552\n"
-                "ds_read_b128 v[108:111], %[x] offset:368\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v68, v64\n"
-                "v_fmac_f32 %[acc], v69, v65\n"
-                "v_fmac_f32 %[acc], v70, v66\n"
-                "v_fmac_f32 %[acc], v71, v67\n"
-                "ds_read_b128 v[64:67], %[w] offset:24576\n"
-                "ds_read_b128 v[68:71], %[x] offset:384\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v76, v72\n"
-                "v_fmac_f32 %[acc], v77, v73\n"
-                "v_fmac_f32 %[acc], v78, v74\n"
-                "v_fmac_f32 %[acc], v79, v75\n"
-                "ds_read_b128 v[72:75], %[w] offset:25600\n"
-                "ds_read_b128 v[76:79], %[x] offset:400\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v84, v80\n"
-                "v_fmac_f32 %[acc], v85, v81\n"
-                "v_fmac_f32 %[acc], v86, v82\n"
-                "v_fmac_f32 %[acc], v87, v83\n"
-                "ds_read_b128 v[80:83], %[w] offset:26624\n"
-                "ds_read_b128 v[84:87], %[x] offset:416\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v92, v88\n"
-                "v_fmac_f32 %[acc], v93, v89\n"
-                "v_fmac_f32 %[acc], v94, v90\n"
-                "v_fmac_f32 %[acc], v95, v91\n"
-                "ds_read_b128 v[88:91], %[w] offset:27648\n"
-                "ds_read_b128 v[92:95], %[x] offset:432\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v100, v96\n"
-                "v_fmac_f32 %[acc], v101, v97\n"
-                "v_fmac_f32 %[acc], v102, v98\n"
-                "v_fmac_f32 %[acc], v103, v99\n"
-                "ds_read_b128 v[96:99], %[w] offset:28672\n"
-                "ds_read_b128 v[100:103], %[x] offset:448\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v108, v104\n"
-                "v_fmac_f32 %[acc], v109, v105\n"
-                "v_fmac_f32 %[acc], v110, v106\n"
-                "v_fmac_f32 %[acc], v111, v107\n"
-                "ds_read_b128 v[104:107], %[w] offset:29696\n"
-                "ds_read_b128 v[108:111], %[x] offset:464\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v68, v64\n"
-                "v_fmac_f32 %[acc], v69, v65\n"
-                "v_fmac_f32 %[acc], v70, v66\n"
-                "v_fmac_f32 %[acc], v71, v67\n"
-                "ds_read_b128 v[64:67], %[w] offset:30720\n"
-                "ds_read_b128 v[68:71], %[x] offset:480\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v76, v72\n"
-                "v_fmac_f32 %[acc], v77, v73\n"
-                "v_fmac_f32 %[acc], v78, v74\n"
-                "v_fmac_f32 %[acc], v79, v75\n"
-                "ds_read_b128 v[72:75], %[w] offset:31744\n"
-                "ds_read_b128 v[76:79], %[x] offset:496\n"
-                "s_waitcnt lgkmcnt(10)\n"
-                "v_fmac_f32 %[acc], v84, v80\n"
-                "v_fmac_f32 %[acc], v85, v81\n"
-                "v_fmac_f32 %[acc], v86, v82\n"
-                "v_fmac_f32 %[acc], v87, v83\n"
-                "s_waitcnt lgkmcnt(8)\n"
-                "v_fmac_f32 %[acc], v92, v88\n"
-                "v_fmac_f32 %[acc], v93, v89\n"
-                "v_fmac_f32 %[acc], v94, v90\n"
-                "v_fmac_f32 %[acc], v95, v91\n"
-                "s_waitcnt lgkmcnt(6)\n"
-                "v_fmac_f32 %[acc], v100, v96\n"
-                "v_fmac_f32 %[acc], v101, v97\n"
-                "v_fmac_f32 %[acc], v102, v98\n"
-                "v_fmac_f32 %[acc], v103, v99\n"
-                "s_waitcnt lgkmcnt(4)\n"
-                "v_fmac_f32 %[acc], v108, v104\n"
-                "v_fmac_f32 %[acc], v109, v105\n"
-                "v_fmac_f32 %[acc], v110, v106\n"
-                "v_fmac_f32 %[acc], v111, v107\n"
-                "s_waitcnt lgkmcnt(2)\n"
-                "v_fmac_f32 %[acc], v68, v64\n"
-                "v_fmac_f32 %[acc], v69, v65\n"
-                "v_fmac_f32 %[acc], v70, v66\n"
-                "v_fmac_f32 %[acc], v71, v67\n"
-                "s_waitcnt lgkmcnt(0)\n"
-                "v_fmac_f32 %[acc], v76, v72\n"
-                "v_fmac_f32 %[acc], v77, v73\n"
-                "v_fmac_f32 %[acc], v78, v74\n"
-                "v_fmac_f32 %[acc], v79, v75\n"
+            if (a.router_unfused) {
+                asm volatile(UOCR_RCHUNK(UOCR_RMAC_SEP)
+                : [acc] "+v"(acc)
+                : [w] "v"(w_addr), [x] "v"(x_addr)
+                : "v64", "v65", "v66", "v67", "v68", "v69", "v70", "v71", "v72", "v73", "v74", "v75", "v76", "v77", "v78", "v79", "v80", "v81", "v82", "v83", "v84", "v85", "v86", "v87", "v88", "v89", "v90", "v91", "v92", "v93", "v94", "v95", "v96", "v97", "v98", "v99", "v100", "v101", "v102", "v103", "v104", "v105", "v106", "v107", "v108", "v109", "v110", "v111", "v112", "memory");
+            } else {
+                asm volatile(UOCR_RCHUNK(UOCR_RMAC_FMA)
                 : [acc] "+v"(acc)
                 : [w] "v"(w_addr), [x] "v"(x_addr)
                 : "v64", "v65", "v66", "v67", "v68", "v69", "v70", "v71", "v72", "v73", "v74", "v75", "v76", "v77", "v78", "v79", "v80", "v81", "v82", "v83", "v84", "v85", "v86", "v87", "v88", "v89", "v90", "v91", "v92", "v93", "v94", "v95", "v96", "v97", "v98", "v99", "v100", "v101", "v102", "v103", "v104", "v105", "v106", "v107", "v108", "v109", "v110", "v111", "memory");
+            }
         }
     }
     // scoring and top-k by wave 0 alone

@@ -133,6 +133,8 @@ struct DecodeArgs {
     const float* rms_weight;   // optional [hidden]; also selects out = x + moe
     float rms_eps;
     const float* router_f32;   // [hidden/4][64][4], experts padded to 64
+    int router_unfused;        // 1: chain steps acc + round(x * w) (an f32 router, matmul_t);
+                               // 0: fma(x, w, acc) (a bf16 router, matmul_t_bf16)
     const uint16_t* router_t;  // [hidden/8][n_experts][8] bf16 (fused decode kernel)
     int norm_topk_prob, scoring_sigmoid;
     float scaling;

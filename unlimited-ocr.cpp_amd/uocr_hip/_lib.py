@@ -40,7 +40,7 @@ class LayerDescC(C.Structure):
                 ("up", C.POINTER(QMatrixC)), ("down", C.POINTER(QMatrixC)),
                 ("shared_gate", C.POINTER(QMatrixC)), ("shared_up", C.POINTER(QMatrixC)),
                 ("shared_down", C.POINTER(QMatrixC)), ("rms_weight", C.c_void_p),
-                ("rms_eps", C.c_float)]
+                ("rms_eps", C.c_float), ("router_f32", C.c_void_p)]
 
 
 def lib_path():
@@ -59,6 +59,17 @@ SIGNATURES = {
     "uocr_hip_moe_layer_status": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_int)]),
     "uocr_hip_moe_layer_status_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
     "uocr_hip_moe_router_overflow": (C.c_int, [C.c_int, C.POINTER(C.c_int)]),
+    "uocr_hip_st_open": (C.c_int, [C.c_char_p, C.POINTER(C.c_void_p)]),
+    "uocr_hip_st_close": (C.c_int, [C.c_void_p]),
+    "uocr_hip_st_contains": (C.c_int, [C.c_void_p, C.c_char_p]),
+    "uocr_hip_st_numel": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_size_t)]),
+    "uocr_hip_st_read_f32": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_size_t]),
+    "uocr_hip_st_read_u8": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p, C.c_size_t]),
+    "uocr_hip_st_metadata": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_char_p)]),
+    "uocr_hip_gptq_group": (C.c_int, [C.c_void_p, C.c_int]),
+    "uocr_hip_gptq_qmatrix": (C.c_int, [C.c_void_p, C.c_char_p, C.c_int, C.c_int, C.c_int, C.POINTER(QMatrixC)]),
+    "uocr_hip_fold_expert_input_scale": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]),
+    "uocr_hip_scale_columns_f32": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
     "uocr_hip_fused_schedule_check": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int), C.c_int]),
     "uocr_hip_moe_layer_forward": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
                                               C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,

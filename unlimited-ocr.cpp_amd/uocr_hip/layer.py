@@ -50,10 +50,14 @@ class MoELayerInt4:
         if L.rms_weight is not None:
             rms = np.ascontiguousarray(L.rms_weight, np.float32)
             keep.append(rms)
+        rf = getattr(L, "router_f32", None)
+        if rf is not None:
+            rf = np.ascontiguousarray(rf, np.float32)
+            keep.append(rf)
         d = LayerDescC(L.hidden, L.inter, L.n_experts, L.top_k, L.n_shared, L.norm_topk_prob,
                        L.routed_scaling_factor, L.scoring_sigmoid, router.ctypes.data,
                        gate, up, down, sg, su, sd, rms.ctypes.data if rms is not None else None,
-                       L.rms_eps)
+                       L.rms_eps, rf.ctypes.data if rf is not None else None)
         h = C.c_void_p()
         check(lib.uocr_hip_moe_layer_create(C.byref(d), C.byref(h)))
         self.handle = h

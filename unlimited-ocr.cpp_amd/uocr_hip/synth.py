@@ -76,6 +76,7 @@ class Layer:
     norm_topk_prob: int = 0
     routed_scaling_factor: float = 1.0
     scoring_sigmoid: int = 0
+    router_f32: Optional[np.ndarray] = None  # f32 [E, H]; replaces router_bf16 (AWQ-folded router)
     _keep: list = field(default_factory=list, repr=False)
 
 
