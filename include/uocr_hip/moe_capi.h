@@ -324,6 +324,61 @@ int uocr_hip_fold_expert_input_scale(const float* s, int hidden, float* rms_weig
 /* scale_columns (weights.cpp:185-197): out[r, c] = w[r, c] * s[c]. */
 int uocr_hip_scale_columns_f32(const float* w, int rows, int cols, const float* s, float* out);
 
+/* ---- R-SWA attention and KV cache (src/kernels/cuda/rswa_attention.cu;
+ * host semantics src/scheduler/kv_cache.cpp) ----
+ * Mirrors of uocr::cuda::rswa_* (include/uocr/cuda_ops.h:59-124) with the same
+ * parameter lists (`bool causal` becomes int, `cudaStream_t` void*, `void`
+ * int). Caches are f32 [capacity, kv_heads, head_dim] per request (batched:
+ * request slot s at base + s * batch_cap * kv_heads * head_dim); q/out f32.
+ * Requirements: heads a multiple of kv_heads, head_dim a multiple of 4 up to
+ * 256 (the reference takes any head_dim <= 256), 16-byte aligned q, caches
+ * and out. Attention uses scale 1/sqrt(head_dim) and an online softmax over
+ * the rows in any order (the reference kernel walks them in order with
+ * __expf); results match the CPU RSWACache::attention within 1e-4 abs.
+ * Decode over the first kv_len rows: q/out [heads, head_dim]
+ * (cuda_ops.h:59-63). */
+int uocr_hip_rswa_attention_decode(const float* q, const float* kcache, const float* vcache, int kv_len, int heads,
+                                   int kv_heads, int head_dim, float* out, void* stream);
+/* Query block (cuda_ops.h:65-72): q/out [seq, heads, head_dim]; causal: query s
+ * attends rows [0, min(kv_len, q_start + s + 1)), else [0, kv_len). */
+int uocr_hip_rswa_attention(const float* q, const float* kcache, const float* vcache, int kv_len, int seq,
+                            int q_start, int heads, int kv_heads, int head_dim, int causal, float* out,
+                            void* stream);
+/* The same with kv_len read from device memory at run time (cuda_ops.h:74-80),
+ * so a captured graph stays valid as the cache grows. The reference kernel
+ * handles seq == 1 only (it indexes heads by block for seq > 1); this one
+ * applies the documented [seq, heads, head_dim] layout and causal mask. */
+int uocr_hip_rswa_attention_devlen(const float* q, const float* kcache, const float* vcache, const int* d_len,
+                                   int seq, int q_start, int heads, int kv_heads, int head_dim, int causal,
+                                   float* out, void* stream);
+/* Append one decoded token's K/V [kv_heads, head_dim] (cuda_ops.h:82-86):
+ * rows grow to prefill_len + window, then row prefill_len + *d_ring_pos is
+ * overwritten circularly; *d_len / *d_ring_pos advance on the device. */
+int uocr_hip_rswa_append_decode(const float* k, const float* v, float* kcache, float* vcache, int* d_len,
+                                int* d_ring_pos, int prefill_len, int window, int kv_heads, int head_dim,
+                                void* stream);
+/* Batched append (cuda_ops.h:88-99): row b of k/v [batch, kv_heads, head_dim]
+ * into request d_slots[b], its state d_len / d_ring_pos / d_prefill_len
+ * indexed by the slot. */
+int uocr_hip_rswa_append_decode_batch(const float* k, const float* v, float* kcache_base, float* vcache_base,
+                                      int* d_len, int* d_ring_pos, const int* d_prefill_len, const int* d_slots,
+                                      int batch, int batch_cap, int window, int kv_heads, int head_dim,
+                                      void* stream);
+/* Batched decode attention (cuda_ops.h:101-107): row b of q/out
+ * [batch, heads, head_dim] over request d_slots[b]'s first d_len[slot] rows. */
+int uocr_hip_rswa_attention_batch(const float* q, const float* kcache_base, const float* vcache_base,
+                                  const int* d_len, const int* d_slots, int batch, int batch_cap, int heads,
+                                  int kv_heads, int head_dim, float* out, void* stream);
+/* Ragged multi-request prefill (cuda_ops.h:109-124): row t's K/V into request
+ * d_slots[t] at row d_pos[t]; attention of row t over its request's rows
+ * [0, d_pos[t]]. */
+int uocr_hip_rswa_write_prefill_ragged(const float* k, const float* v, float* kcache_base, float* vcache_base,
+                                       const int* d_slots, const int* d_pos, int total, int batch_cap, int kv_heads,
+                                       int head_dim, void* stream);
+int uocr_hip_rswa_attention_ragged(const float* q, const float* kcache_base, const float* vcache_base,
+                                   const int* d_slots, const int* d_pos, int total, int batch_cap, int heads,
+                                   int kv_heads, int head_dim, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

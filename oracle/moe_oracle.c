@@ -309,6 +309,71 @@ void orc_fold_expert_input_scale(const float* s, int hidden, float* rms_weight,
             router_f32[(size_t)e * hidden + c] = orc_bf16_to_f32(router_bf16[(size_t)e * hidden + c]) * s[c];
 }
 
+/* src/scheduler/kv_cache.cpp:84-130, as the reference build computes it: the
+ * score loop like matmul_t (products rounded, added in order; only the scalar
+ * tail of head_dim % 4 terms fused), the accumulator update as
+ * fma(acc, alpha, round(beta * v)), l * alpha + beta as fma(l, alpha, beta);
+ * exp is glibc's expf (std::exp on floats). Pinned bit-exact against
+ * oracle/_ref (tests/test_oracle_rswa.py). */
+void orc_rswa_attention(const float* q, const float* kcache, const float* vcache, int kv_len, int seq,
+                        int q_start, int heads, int kv_heads, int head_dim, int causal, float* out) {
+    const int hd = head_dim, group = heads / kv_heads;
+    const float scale = 1.0f / sqrtf((float)hd);
+    float* acc = (float*)malloc(sizeof(float) * (size_t)hd);
+    for (int s = 0; s < seq; ++s) {
+        const int qpos = q_start + s;
+        for (int h = 0; h < heads; ++h) {
+            const float* qh = q + ((size_t)s * heads + h) * hd;
+            const int kvh = h / group;
+            const int limit = causal ? (kv_len < qpos + 1 ? kv_len : qpos + 1) : kv_len;
+            float m = -INFINITY, l = 0.0f;
+            for (int d = 0; d < hd; ++d) acc[d] = 0.0f;
+            for (int t = 0; t < limit; ++t) {
+                const float* kt = kcache + ((size_t)t * kv_heads + kvh) * hd;
+                const float* vt = vcache + ((size_t)t * kv_heads + kvh) * hd;
+                float dot = 0.0f;
+                const int hd4 = hd & ~3;
+                for (int d = 0; d < hd4; ++d) dot = dot + qh[d] * kt[d];
+                for (int d = hd4; d < hd; ++d) dot = fmaf(qh[d], kt[d], dot);
+                dot = dot * scale;
+                const float m_new = m > dot ? m : dot;
+                const float alpha = expf(m - m_new);
+                const float beta = expf(dot - m_new);
+                l = fmaf(l, alpha, beta);
+                for (int d = 0; d < hd; ++d) acc[d] = fmaf(acc[d], alpha, beta * vt[d]);
+                m = m_new;
+            }
+            float* oh = out + ((size_t)s * heads + h) * hd;
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+            for (int d = 0; d < hd; ++d) oh[d] = acc[d] * inv;
+        }
+    }
+    free(acc);
+}
+
+/* src/scheduler/kv_cache.cpp:54-82 */
+void orc_rswa_append(float* kcache, float* vcache, int* len, int* ring_pos, int* ring_started,
+                     int prefill_len, int window, int stride, const float* k, const float* v) {
+    int row;
+    if (*len < prefill_len + window) {
+        row = *len;
+        *len = *len + 1;
+        if (*len >= prefill_len + window) {
+            *ring_started = 1;
+            *ring_pos = 0;
+        }
+    } else {
+        if (!*ring_started) {
+            *ring_started = 1;
+            *ring_pos = 0;
+        }
+        row = prefill_len + *ring_pos;
+        *ring_pos = (*ring_pos + 1) % window;
+    }
+    memcpy(kcache + (size_t)row * stride, k, sizeof(float) * (size_t)stride);
+    memcpy(vcache + (size_t)row * stride, v, sizeof(float) * (size_t)stride);
+}
+
 /* src/engine/gpu_decoder.cu:602-609: for t, for j: e_tokens[ids[t,j]].push_back(t)
  * -- a stable counting sort of the (t, j) entries by expert. */
 void orc_stable_group(const int* ids, int seq, int top_k, int n_experts, int* counts,

@@ -89,6 +89,19 @@ void orc_fold_expert_input_scale(const float* s, int hidden, float* rms_weight,
 /* weights.cpp:185-197: out[r, c] = w[r, c] * s[c] (w already materialised as f32). */
 void orc_scale_columns(const float* w, int rows, int cols, const float* s, float* out);
 
+/* R-SWA KV cache of one layer, src/scheduler/kv_cache.cpp. Cache layout
+ * [capacity, kv_heads, head_dim] f32 (capacity = prefill_len + window).
+ * attention (kv_cache.cpp:84-130): q/out [seq, heads, head_dim]; query s attends
+ * rows [0, causal ? min(kv_len, q_start + s + 1) : kv_len) of kv head
+ * h / (heads / kv_heads), online softmax in row order. */
+void orc_rswa_attention(const float* q, const float* kcache, const float* vcache, int kv_len, int seq,
+                        int q_start, int heads, int kv_heads, int head_dim, int causal, float* out);
+/* append_decode (kv_cache.cpp:54-82) with the cache's state (len, ring_pos,
+ * ring_started) passed in and updated: grow to prefill_len + window, then
+ * overwrite row prefill_len + ring_pos circularly. stride = kv_heads * head_dim. */
+void orc_rswa_append(float* kcache, float* vcache, int* len, int* ring_pos, int* ring_started,
+                     int prefill_len, int window, int stride, const float* k, const float* v);
+
 void orc_stable_group(const int* ids, int seq, int top_k, int n_experts, int* counts,
                       int* offsets, int* perm_token, int* perm_j);
 

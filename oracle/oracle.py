@@ -68,6 +68,9 @@ def lib():
                                    C.c_float, C.c_int, i32p, f32p]
         L.orc_moe_gate_f32router.argtypes = [f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int,
                                              C.c_int, C.c_float, C.c_int, i32p, f32p]
+        L.orc_rswa_attention.argtypes = [f32p, f32p, f32p] + [C.c_int] * 7 + [f32p]
+        L.orc_rswa_append.argtypes = [f32p, f32p, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int),
+                                      C.c_int, C.c_int, C.c_int, f32p, f32p]
         L.orc_stable_group.argtypes = [i32p, C.c_int, C.c_int, C.c_int, i32p, i32p, i32p, C.c_void_p]
         L.orc_moe_layer.argtypes = [C.POINTER(LayerC), f32p, C.c_int, C.c_void_p, C.c_int, C.c_int,
                                     i32p, f32p, f32p]
@@ -94,6 +97,16 @@ def ref():
         R.ref_f32_to_bf16.argtypes = [C.c_float]
         R.ref_bf16_to_f32.restype = C.c_float
         R.ref_bf16_to_f32.argtypes = [C.c_uint16]
+        R.ref_rswa_new.restype = C.c_void_p
+        R.ref_rswa_new.argtypes = [C.c_int, C.c_int, C.c_int]
+        R.ref_rswa_free.argtypes = [C.c_void_p]
+        R.ref_rswa_reset.argtypes = [C.c_void_p, C.c_int]
+        R.ref_rswa_write_prefill.argtypes = [C.c_void_p, f32p, f32p, C.c_int]
+        R.ref_rswa_append.argtypes = [C.c_void_p, f32p, f32p]
+        for n in ("ref_rswa_len", "ref_rswa_ring_pos", "ref_rswa_capacity"):
+            getattr(R, n).argtypes = [C.c_void_p]
+        R.ref_rswa_copy_kv.argtypes = [C.c_void_p, f32p, f32p]
+        R.ref_rswa_attention.argtypes = [C.c_void_p, f32p, C.c_int, C.c_int, f32p, C.c_int, C.c_int]
         _ref = R
     return _ref
 
@@ -157,6 +170,48 @@ def stable_group(ids, n_experts):
     perm = np.empty(seq * k, np.int32)
     lib().orc_stable_group(ids, seq, k, n_experts, counts, offs, perm, None)
     return counts, offs, perm
+
+
+def rswa_attention(q, kcache, vcache, kv_len, q_start, heads, kv_heads, head_dim, causal):
+    """RSWACache::attention (kv_cache.cpp:84-130) on an explicit cache
+    [capacity, kv_heads, head_dim]; q [seq, heads, head_dim] -> out (same shape)."""
+    q = np.ascontiguousarray(q, np.float32)
+    seq = q.size // (heads * head_dim)
+    out = np.empty_like(q)
+    lib().orc_rswa_attention(q, np.ascontiguousarray(kcache, np.float32), np.ascontiguousarray(vcache, np.float32),
+                             kv_len, seq, q_start, heads, kv_heads, head_dim, 1 if causal else 0, out)
+    return out
+
+
+class RswaCache:
+    """One layer's R-SWA cache with the reference's host semantics
+    (kv_cache.cpp:29-82): reset(P), write_prefill, append_decode."""
+
+    def __init__(self, kv_heads, head_dim, window):
+        self.kv_heads, self.head_dim, self.window = kv_heads, head_dim, window
+        self.stride = kv_heads * head_dim
+
+    def reset(self, prefill_len):
+        self.prefill_len = prefill_len
+        self.capacity = prefill_len + self.window
+        self.k = np.zeros(self.capacity * self.stride, np.float32)
+        self.v = np.zeros(self.capacity * self.stride, np.float32)
+        self.len, self.ring_pos, self.ring_started = C.c_int(prefill_len), C.c_int(0), C.c_int(0)
+
+    def write_prefill(self, k, v, seq):
+        n = seq * self.stride
+        self.k[:n] = np.asarray(k, np.float32).ravel()[:n]
+        self.v[:n] = np.asarray(v, np.float32).ravel()[:n]
+        self.len.value = seq
+        self.prefill_len = seq
+
+    def append(self, k, v):
+        lib().orc_rswa_append(self.k, self.v, C.byref(self.len), C.byref(self.ring_pos), C.byref(self.ring_started),
+                              self.prefill_len, self.window, self.stride,
+                              np.ascontiguousarray(k, np.float32).ravel(), np.ascontiguousarray(v, np.float32).ravel())
+
+    def attention(self, q, q_start, heads, causal):
+        return rswa_attention(q, self.k, self.v, self.len.value, q_start, heads, self.kv_heads, self.head_dim, causal)
 
 
 def fold_expert_input_scale(s, rms_weight, router_bf16):

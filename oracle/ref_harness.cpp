@@ -1,10 +1,12 @@
 // extern "C" entry points onto the reference's own CPU code, compiled from the
-// reference sources where they lie (src/runtime/quant.cpp, src/kernels/cpu_ops.cpp).
+// reference sources where they lie (src/runtime/quant.cpp, src/kernels/cpu_ops.cpp,
+// src/scheduler/kv_cache.cpp).
 // TEST INFRASTRUCTURE ONLY: loaded by tests/ to pin the oracle restatement and
 // to write golden vectors; never part of the product.
 #include <cstring>
 #include <vector>
 
+#include "uocr/kv_cache.h"
 #include "uocr/ops.h"
 #include "uocr/quant.h"
 
@@ -77,4 +79,25 @@ void ref_rmsnorm(const float* x, const float* w, float* out, int rows, int cols,
 
 unsigned short ref_f32_to_bf16(float f) { return uocr::f32_to_bf16(f); }
 float ref_bf16_to_f32(unsigned short h) { return uocr::bf16_to_f32(h); }
+
+// R-SWA cache of one layer (src/scheduler/kv_cache.cpp)
+void* ref_rswa_new(int kv_heads, int head_dim, int window) { return new uocr::RSWACache(1, kv_heads, head_dim, window); }
+void ref_rswa_free(void* c) { delete static_cast<uocr::RSWACache*>(c); }
+void ref_rswa_reset(void* c, int prefill_len) { static_cast<uocr::RSWACache*>(c)->reset(prefill_len); }
+void ref_rswa_write_prefill(void* c, const float* k, const float* v, int seq) {
+    static_cast<uocr::RSWACache*>(c)->write_prefill(0, k, v, seq);
+}
+void ref_rswa_append(void* c, const float* k, const float* v) { static_cast<uocr::RSWACache*>(c)->append_decode(0, k, v); }
+int ref_rswa_len(void* c) { return static_cast<uocr::RSWACache*>(c)->length(0); }
+int ref_rswa_ring_pos(void* c) { return static_cast<uocr::RSWACache*>(c)->ring_pos(0); }
+int ref_rswa_capacity(void* c) { return static_cast<uocr::RSWACache*>(c)->capacity(); }
+void ref_rswa_copy_kv(void* c, float* k, float* v) {
+    auto* r = static_cast<uocr::RSWACache*>(c);
+    const std::size_t n = static_cast<std::size_t>(r->capacity()) * r->kv_heads() * r->head_dim();
+    std::memcpy(k, r->keys(0), n * sizeof(float));
+    std::memcpy(v, r->values(0), n * sizeof(float));
+}
+void ref_rswa_attention(void* c, const float* q, int seq, int q_start, float* out, int heads, int causal) {
+    static_cast<uocr::RSWACache*>(c)->attention(0, q, seq, q_start, out, heads, causal != 0);
+}
 }

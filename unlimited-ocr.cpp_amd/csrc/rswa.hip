@@ -1,0 +1,368 @@
+// R-SWA attention and KV-cache writes (the step after the MoE path):
+// counterparts of src/kernels/cuda/rswa_attention.cu and the host cache
+// semantics of src/scheduler/kv_cache.cpp. Cache layout as the reference's:
+// [capacity, kv_heads, head_dim] f32 per request (a batch of requests: slot s
+// at base + s * batch_cap * kv_heads * head_dim); rows 0..P-1 hold the first
+// prefill ("reference tokens"), rows P..P+W-1 a ring of the last W decoded
+// tokens.
+//
+// Attention: one workgroup per (query row, head), 8 waves splitting the keys.
+// A wave takes groups of 8 consecutive keys (groups w, w + 8, ...): lane
+// (j, p) = (lane / 8, lane % 8) holds key j's dims [p*D, (p+1)*D) of K and V
+// (D = HDP / 8; a key row is one contiguous 16-byte-per-lane read by 8 lanes),
+// with the next group's K and V loads issued before the current group is
+// used. Scores reduce over the 8 lanes of a key, the online softmax runs per
+// wave (max, rescale, sum over the group's keys), and each lane accumulates
+// p * V for its own key slot; the 8 key slots and then the 8 waves are
+// combined at the end (flash-decoding). Decode is HBM-bound: every (row, head)
+// streams kv_len * head_dim * 8 bytes of K and V.
+#include <hip/hip_runtime.h>
+
+#include <initializer_list>
+#include <string>
+
+#include "common.hpp"
+#include "launch.hpp"
+#include "uocr_hip/moe_capi.h"
+
+namespace uocr_hip {
+namespace {
+
+constexpr int kRswaWaves = 8;
+
+struct RswaArgs {
+    const float* q;
+    const float* kc;
+    const float* vc;
+    float* out;
+    int heads, kv_heads, head_dim;
+    float scale;
+    int mode;  // 0: one cache, kv_len (causal: q_start); 1: same, kv_len = *d_len;
+               // 2: batch (slot d_slots[b], length d_len[slot]); 3: ragged (slot d_slots[t], rows 0..d_pos[t])
+    int kv_len, q_start, causal;
+    const int* d_len;
+    const int* d_slots;
+    const int* d_pos;
+    int batch_cap;
+};
+
+template <int HDP>
+__global__ __launch_bounds__(kRswaWaves * 64) void rswa_kernel(RswaArgs a) {
+    constexpr int D = HDP / 8;  // dims per lane
+    constexpr int NV = D / 4;   // float4 per lane per row
+    const int row = blockIdx.x, head = blockIdx.y;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int j = lane >> 3, p = lane & 7;
+    const int hd = a.head_dim, stride = a.kv_heads * hd;
+    const int kvh = head / (a.heads / a.kv_heads);
+    const float* kc = a.kc;
+    const float* vc = a.vc;
+    int limit;
+    if (a.mode <= 1) {
+        const int kv_len = a.mode == 1 ? *a.d_len : a.kv_len;
+        limit = a.causal ? min(kv_len, a.q_start + row + 1) : kv_len;
+    } else {
+        const int slot = a.d_slots[row];
+        limit = a.mode == 2 ? a.d_len[slot] : a.d_pos[row] + 1;
+        kc += (size_t)slot * a.batch_cap * stride;
+        vc += (size_t)slot * a.batch_cap * stride;
+    }
+    const size_t qoff = ((size_t)row * a.heads + head) * hd;
+    kc += (size_t)kvh * hd;
+    vc += (size_t)kvh * hd;
+    const int d0 = p * D;
+
+    f32x4 qv[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+        qv[i] = d0 + 4 * i < hd ? *reinterpret_cast<const f32x4*>(a.q + qoff + d0 + 4 * i) : f32x4{0.f, 0.f, 0.f, 0.f};
+
+    float m = -INFINITY, l = 0.0f;
+    f32x4 acc[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int n_groups = (limit + 7) / 8;
+    auto load = [&](int g, f32x4 (&kv)[NV], f32x4 (&vv)[NV]) {
+        const int t = g * 8 + j;
+        const bool ok = g < n_groups && t < limit;
+        const float* kr = kc + (size_t)t * stride + d0;
+        const float* vr = vc + (size_t)t * stride + d0;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const bool in = ok && d0 + 4 * i < hd;
+            kv[i] = in ? *reinterpret_cast<const f32x4*>(kr + 4 * i) : f32x4{0.f, 0.f, 0.f, 0.f};
+            vv[i] = in ? *reinterpret_cast<const f32x4*>(vr + 4 * i) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    f32x4 k0[NV], v0[NV], k1[NV], v1[NV];
+    constexpr float kLog2e = 1.4426950408889634f;
+    auto step = [&](int g, const f32x4 (&kv)[NV], const f32x4 (&vv)[NV]) {
+        float part = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) part = fmaf(qv[i][c], kv[i][c], part);
+        part += __shfl_xor(part, 1, 64);
+        part += __shfl_xor(part, 2, 64);
+        part += __shfl_xor(part, 4, 64);
+        const bool valid = g * 8 + j < limit;
+        const float s = valid ? part * a.scale : -INFINITY;
+        float mg = fmaxf(s, __shfl_xor(s, 8, 64));
+        mg = fmaxf(mg, __shfl_xor(mg, 16, 64));
+        mg = fmaxf(mg, __shfl_xor(mg, 32, 64));
+        const float m_new = fmaxf(m, mg);  // finite: key 0 of the group is valid
+        const float alpha = __builtin_amdgcn_exp2f((m - m_new) * kLog2e);
+        const float beta = valid ? __builtin_amdgcn_exp2f((s - m_new) * kLog2e) : 0.0f;
+        float bs = beta + __shfl_xor(beta, 8, 64);
+        bs += __shfl_xor(bs, 16, 64);
+        bs += __shfl_xor(bs, 32, 64);
+        l = fmaf(l, alpha, bs);
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[i][c] = fmaf(acc[i][c], alpha, beta * vv[i][c]);
+        m = m_new;
+    };
+    // groups wave, wave + 8, ...; one group's loads in flight beyond the one in use
+    int g = wave;
+    if (g < n_groups) load(g, k0, v0);
+    while (g < n_groups) {
+        load(g + kRswaWaves, k1, v1);
+        step(g, k0, v0);
+        g += kRswaWaves;
+        if (g >= n_groups) break;
+        load(g + kRswaWaves, k0, v0);
+        step(g, k1, v1);
+        g += kRswaWaves;
+    }
+    // sum the 8 key slots of the wave (same m within the wave)
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            float x = acc[i][c];
+            x += __shfl_xor(x, 8, 64);
+            x += __shfl_xor(x, 16, 64);
+            x += __shfl_xor(x, 32, 64);
+            acc[i][c] = x;
+        }
+    __shared__ float wm[kRswaWaves], wl[kRswaWaves];
+    __shared__ __attribute__((aligned(16))) float wacc[kRswaWaves][HDP];
+    if (lane < 8) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) *reinterpret_cast<f32x4*>(&wacc[wave][d0 + 4 * i]) = acc[i];
+    }
+    if (lane == 0) {
+        wm[wave] = m;
+        wl[wave] = l;
+    }
+    __syncthreads();
+    // combine the waves (a wave without keys has m = -inf and weight 0)
+    for (int d = tid; d < hd; d += kRswaWaves * 64) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kRswaWaves; ++w) M = fmaxf(M, wm[w]);
+        float L = 0.0f, o = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < kRswaWaves; ++w) {
+                const float f = wm[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((wm[w] - M) * kLog2e);
+                L = fmaf(wl[w], f, L);
+                o = fmaf(wacc[w][d], f, o);
+            }
+        }
+        a.out[qoff + d] = L > 0.0f ? o / L : 0.0f;
+    }
+}
+
+// Row copy of one token's K and V (stride floats each) into a cache row.
+__device__ __forceinline__ void copy_row(const float* k, const float* v, float* kd, float* vd, int stride) {
+    for (int i = threadIdx.x * 4; i < stride; i += blockDim.x * 4) {
+        *reinterpret_cast<f32x4*>(kd + i) = *reinterpret_cast<const f32x4*>(k + i);
+        *reinterpret_cast<f32x4*>(vd + i) = *reinterpret_cast<const f32x4*>(v + i);
+    }
+}
+
+// The cache row an append writes, with the ring state advanced: grow until
+// prefill_len + window, then overwrite prefill_len + ring_pos circularly
+// (kv_cache.cpp:54-82; rswa_attention.cu:409-420). One thread updates the
+// state; the row reaches the others through LDS.
+__device__ __forceinline__ int append_row(int* d_len, int* d_ring_pos, int prefill_len, int window) {
+    __shared__ int row_s;
+    if (threadIdx.x == 0) {
+        const int len = *d_len;
+        int row;
+        if (len < prefill_len + window) {
+            row = len;
+            *d_len = len + 1;
+            if (len + 1 >= prefill_len + window) *d_ring_pos = 0;
+        } else {
+            const int rp = *d_ring_pos;
+            row = prefill_len + rp;
+            *d_ring_pos = (rp + 1) % window;
+        }
+        row_s = row;
+    }
+    __syncthreads();
+    return row_s;
+}
+
+__global__ __launch_bounds__(256) void rswa_append_kernel(const float* k, const float* v, float* kc, float* vc,
+                                                          int* d_len, int* d_ring_pos, int prefill_len, int window,
+                                                          int stride) {
+    const int row = append_row(d_len, d_ring_pos, prefill_len, window);
+    copy_row(k, v, kc + (size_t)row * stride, vc + (size_t)row * stride, stride);
+}
+
+__global__ __launch_bounds__(256) void rswa_append_batch_kernel(const float* k, const float* v, float* kc, float* vc,
+                                                                int* d_len, int* d_ring_pos, const int* d_prefill_len,
+                                                                const int* d_slots, int batch_cap, int window,
+                                                                int stride) {
+    const int b = blockIdx.x, slot = d_slots[b];
+    const int row = append_row(d_len + slot, d_ring_pos + slot, d_prefill_len[slot], window);
+    const size_t dst = ((size_t)slot * batch_cap + row) * stride;
+    copy_row(k + (size_t)b * stride, v + (size_t)b * stride, kc + dst, vc + dst, stride);
+}
+
+__global__ __launch_bounds__(256) void rswa_write_ragged_kernel(const float* k, const float* v, float* kc, float* vc,
+                                                                const int* d_slots, const int* d_pos, int batch_cap,
+                                                                int stride) {
+    const int t = blockIdx.x;
+    const size_t dst = ((size_t)d_slots[t] * batch_cap + d_pos[t]) * stride;
+    copy_row(k + (size_t)t * stride, v + (size_t)t * stride, kc + dst, vc + dst, stride);
+}
+
+int check_shape(int heads, int kv_heads, int head_dim) {
+    if (heads <= 0 || kv_heads <= 0 || heads % kv_heads)
+        return set_error(UOCR_HIP_EINVAL, "heads must be a positive multiple of kv_heads");
+    if (head_dim <= 0 || head_dim > 256 || head_dim % 4)
+        return set_error(UOCR_HIP_EUNSUPPORTED, "head_dim must be a multiple of 4 in [4, 256]");
+    return UOCR_HIP_OK;
+}
+
+int check_ptrs(std::initializer_list<const void*> ps) {
+    for (const void* p : ps) {
+        if (!p) return set_error(UOCR_HIP_EINVAL, "null pointer");
+        if ((uintptr_t)p % 16) return set_error(UOCR_HIP_EINVAL, "q, k/v caches and out must be 16-byte aligned");
+    }
+    return UOCR_HIP_OK;
+}
+
+int launch_attention(RswaArgs a, int rows, hipStream_t st) {
+    if (rows <= 0) return UOCR_HIP_OK;
+    a.scale = 1.0f / sqrtf((float)a.head_dim);
+    const dim3 grid(rows, a.heads), block(kRswaWaves * 64);
+    if (a.head_dim <= 64) launch_k(rswa_kernel<64>, grid, block, 0, st, a);
+    else if (a.head_dim <= 128) launch_k(rswa_kernel<128>, grid, block, 0, st, a);
+    else launch_k(rswa_kernel<256>, grid, block, 0, st, a);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? UOCR_HIP_OK : set_error(UOCR_HIP_EHIP, std::string("rswa launch: ") + hipGetErrorString(e));
+}
+
+int launch_done(const char* what) {
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? UOCR_HIP_OK : set_error(UOCR_HIP_EHIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+}  // namespace
+}  // namespace uocr_hip
+
+using namespace uocr_hip;
+
+extern "C" {
+
+int uocr_hip_rswa_attention_decode(const float* q, const float* kcache, const float* vcache, int kv_len, int heads,
+                                   int kv_heads, int head_dim, float* out, void* stream) {
+    if (int rc = check_shape(heads, kv_heads, head_dim)) return rc;
+    if (int rc = check_ptrs({q, kcache, vcache, out})) return rc;
+    if (kv_len < 0) return set_error(UOCR_HIP_EINVAL, "kv_len must be >= 0");
+    RswaArgs a{q, kcache, vcache, out, heads, kv_heads, head_dim, 0.f, 0, kv_len, 0, 0, nullptr, nullptr, nullptr, 0};
+    return launch_attention(a, 1, (hipStream_t)stream);
+}
+
+int uocr_hip_rswa_attention(const float* q, const float* kcache, const float* vcache, int kv_len, int seq,
+                            int q_start, int heads, int kv_heads, int head_dim, int causal, float* out,
+                            void* stream) {
+    if (int rc = check_shape(heads, kv_heads, head_dim)) return rc;
+    if (int rc = check_ptrs({q, kcache, vcache, out})) return rc;
+    if (kv_len < 0 || seq < 0) return set_error(UOCR_HIP_EINVAL, "kv_len and seq must be >= 0");
+    RswaArgs a{q, kcache, vcache, out, heads, kv_heads, head_dim, 0.f, 0, kv_len, q_start, causal != 0,
+               nullptr, nullptr, nullptr, 0};
+    return launch_attention(a, seq, (hipStream_t)stream);
+}
+
+int uocr_hip_rswa_attention_devlen(const float* q, const float* kcache, const float* vcache, const int* d_len,
+                                   int seq, int q_start, int heads, int kv_heads, int head_dim, int causal,
+                                   float* out, void* stream) {
+    if (int rc = check_shape(heads, kv_heads, head_dim)) return rc;
+    if (int rc = check_ptrs({q, kcache, vcache, out})) return rc;
+    if (!d_len || seq < 0) return set_error(UOCR_HIP_EINVAL, "null d_len or negative seq");
+    RswaArgs a{q, kcache, vcache, out, heads, kv_heads, head_dim, 0.f, 1, 0, q_start, causal != 0,
+               d_len, nullptr, nullptr, 0};
+    return launch_attention(a, seq, (hipStream_t)stream);
+}
+
+int uocr_hip_rswa_attention_batch(const float* q, const float* kcache_base, const float* vcache_base,
+                                  const int* d_len, const int* d_slots, int batch, int batch_cap, int heads,
+                                  int kv_heads, int head_dim, float* out, void* stream) {
+    if (batch <= 0) return UOCR_HIP_OK;  // as the reference: nothing to do
+    if (int rc = check_shape(heads, kv_heads, head_dim)) return rc;
+    if (int rc = check_ptrs({q, kcache_base, vcache_base, out})) return rc;
+    if (!d_len || !d_slots || batch_cap <= 0) return set_error(UOCR_HIP_EINVAL, "null d_len/d_slots or batch_cap <= 0");
+    RswaArgs a{q, kcache_base, vcache_base, out, heads, kv_heads, head_dim, 0.f, 2, 0, 0, 0,
+               d_len, d_slots, nullptr, batch_cap};
+    return launch_attention(a, batch, (hipStream_t)stream);
+}
+
+int uocr_hip_rswa_attention_ragged(const float* q, const float* kcache_base, const float* vcache_base,
+                                   const int* d_slots, const int* d_pos, int total, int batch_cap, int heads,
+                                   int kv_heads, int head_dim, float* out, void* stream) {
+    if (total <= 0) return UOCR_HIP_OK;
+    if (int rc = check_shape(heads, kv_heads, head_dim)) return rc;
+    if (int rc = check_ptrs({q, kcache_base, vcache_base, out})) return rc;
+    if (!d_slots || !d_pos || batch_cap <= 0) return set_error(UOCR_HIP_EINVAL, "null d_slots/d_pos or batch_cap <= 0");
+    RswaArgs a{q, kcache_base, vcache_base, out, heads, kv_heads, head_dim, 0.f, 3, 0, 0, 0,
+               nullptr, d_slots, d_pos, batch_cap};
+    return launch_attention(a, total, (hipStream_t)stream);
+}
+
+int uocr_hip_rswa_append_decode(const float* k, const float* v, float* kcache, float* vcache, int* d_len,
+                                int* d_ring_pos, int prefill_len, int window, int kv_heads, int head_dim,
+                                void* stream) {
+    if (int rc = check_shape(kv_heads, kv_heads, head_dim)) return rc;
+    if (int rc = check_ptrs({k, v, kcache, vcache})) return rc;
+    if (!d_len || !d_ring_pos || window <= 0 || prefill_len < 0)
+        return set_error(UOCR_HIP_EINVAL, "null state or window <= 0");
+    launch_k(rswa_append_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, k, v, kcache, vcache, d_len, d_ring_pos,
+             prefill_len, window, kv_heads * head_dim);
+    return launch_done("rswa append");
+}
+
+int uocr_hip_rswa_append_decode_batch(const float* k, const float* v, float* kcache_base, float* vcache_base,
+                                      int* d_len, int* d_ring_pos, const int* d_prefill_len, const int* d_slots,
+                                      int batch, int batch_cap, int window, int kv_heads, int head_dim,
+                                      void* stream) {
+    if (batch <= 0) return UOCR_HIP_OK;
+    if (int rc = check_shape(kv_heads, kv_heads, head_dim)) return rc;
+    if (int rc = check_ptrs({k, v, kcache_base, vcache_base})) return rc;
+    if (!d_len || !d_ring_pos || !d_prefill_len || !d_slots || window <= 0 || batch_cap <= 0)
+        return set_error(UOCR_HIP_EINVAL, "null state arrays, window <= 0 or batch_cap <= 0");
+    launch_k(rswa_append_batch_kernel, dim3(batch), dim3(256), 0, (hipStream_t)stream, k, v, kcache_base, vcache_base,
+             d_len, d_ring_pos, d_prefill_len, d_slots, batch_cap, window, kv_heads * head_dim);
+    return launch_done("rswa batch append");
+}
+
+int uocr_hip_rswa_write_prefill_ragged(const float* k, const float* v, float* kcache_base, float* vcache_base,
+                                       const int* d_slots, const int* d_pos, int total, int batch_cap, int kv_heads,
+                                       int head_dim, void* stream) {
+    if (total <= 0) return UOCR_HIP_OK;
+    if (int rc = check_shape(kv_heads, kv_heads, head_dim)) return rc;
+    if (int rc = check_ptrs({k, v, kcache_base, vcache_base})) return rc;
+    if (!d_slots || !d_pos || batch_cap <= 0) return set_error(UOCR_HIP_EINVAL, "null d_slots/d_pos or batch_cap <= 0");
+    launch_k(rswa_write_ragged_kernel, dim3(total), dim3(256), 0, (hipStream_t)stream, k, v, kcache_base, vcache_base,
+             d_slots, d_pos, batch_cap, kv_heads * head_dim);
+    return launch_done("rswa ragged write");
+}
+
+}  // extern "C"
