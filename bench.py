@@ -259,13 +259,59 @@ def copy_probe(nbytes, reps=5):
     print(json.dumps({"copy_probe_bytes": nbytes, "reps": reps}))
 
 
+def run_rswa(steps, warmup, batch=16, prefill=1000, window=128, heads=10, kv_heads=10, head_dim=128, replicas=2):
+    """R-SWA decode attention (uocr_hip_rswa_attention_batch) at the decoder's
+    shapes: `batch` requests with full caches (prefill + window rows), one
+    query row each. HBM-bound: every (request, head) streams its K and V rows.
+    `replicas` cache copies (alternating) keep the caches out of the 256 MB
+    Infinity Cache."""
+    import ctypes as C
+    import torch
+    from uocr_hip import _lib
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    cap = prefill + window
+    stride = kv_heads * head_dim
+    g = torch.Generator(device=dev).manual_seed(5)
+    caches = [(torch.randn(batch * cap * stride, device=dev, generator=g),
+               torch.randn(batch * cap * stride, device=dev, generator=g)) for _ in range(replicas)]
+    q = torch.randn(batch * heads * head_dim, device=dev, generator=g)
+    out = torch.empty_like(q)
+    d_len = torch.full((batch,), cap, dtype=torch.int32, device=dev)
+    slots = torch.arange(batch, dtype=torch.int32, device=dev)
+    P = lambda t: C.c_void_p(t.data_ptr())
+
+    def call(i):
+        kc, vc = caches[i % replicas]
+        rc = lib.uocr_hip_rswa_attention_batch(P(q), P(kc), P(vc), P(d_len), P(slots), batch, cap, heads, kv_heads,
+                                               head_dim, P(out), None)
+        if rc:
+            raise RuntimeError(lib.uocr_hip_last_error().decode())
+    for i in range(warmup):
+        call(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        call(i)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    nbytes = batch * heads * cap * head_dim * 4 * 2 + 2 * batch * heads * head_dim * 4
+    return {"workload": f"rswa_decode_batch{batch}_kv{cap}_h{heads}_d{head_dim}", "ms_per_step": ms,
+            "kernel": "rswa_kernel<128> (uocr_hip_rswa_attention_batch)", "bytes": nbytes,
+            "gbs": nbytes / ms / 1e6, "hbm_frac": nbytes / ms / 1e6 / HBM_PEAK_GBS,
+            "note": "hipEvent-timed on torch's current stream (the library launches on the default stream)"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--replicas", type=int, default=6)
-    ap.add_argument("--extra", default="0,2,3,4", help="extra configs to report ('' = none)")
+    ap.add_argument("--extra", default="0,2,3,4,rswa",
+                    help="extra configs to report: 0,2,3,4 and rswa (R-SWA decode attention); '' = none")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run a plain copy of BYTES bytes (counter calibration)")
@@ -280,7 +326,11 @@ def main():
 
     main_res = run_config(1, args.steps, args.warmup, args.replicas)
     extras = {}
-    for c in [int(v) for v in args.extra.split(",") if v.strip()]:
+    for c in [v.strip() for v in args.extra.split(",") if v.strip()]:
+        if c == "rswa":
+            extras["rswa"] = run_rswa(max(args.steps // 2, 20), 5)
+            continue
+        c = int(c)
         if c == 4:
             for g in (32, 128):
                 r = run_config(4, max(args.steps // 10, 5), 3, 1, group=g, graph=True)

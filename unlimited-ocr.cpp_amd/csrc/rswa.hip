@@ -10,8 +10,8 @@
 // A wave takes groups of 8 consecutive keys (groups w, w + 8, ...): lane
 // (j, p) = (lane / 8, lane % 8) holds key j's dims [p*D, (p+1)*D) of K and V
 // (D = HDP / 8; a key row is one contiguous 16-byte-per-lane read by 8 lanes),
-// with the next group's K and V loads issued before the current group is
-// used. Scores reduce over the 8 lanes of a key, the online softmax runs per
+// with the next two groups' K and V loads (one for head_dim > 128) issued
+// before the current group is used. Scores reduce over the 8 lanes of a key, the online softmax runs per
 // wave (max, rescale, sum over the group's keys), and each lane accumulates
 // p * V for its own key slot; the 8 key slots and then the 8 waves are
 // combined at the end (flash-decoding). Decode is HBM-bound: every (row, head)
@@ -83,19 +83,23 @@ __global__ __launch_bounds__(kRswaWaves * 64) void rswa_kernel(RswaArgs a) {
     for (int i = 0; i < NV; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int n_groups = (limit + 7) / 8;
+    // Unpredicated loads (a lane-predicated load makes the compiler wait for
+    // every outstanding load before the first use, defeating the prefetch):
+    // keys past the limit re-read the last valid row (their weight is 0),
+    // dims past head_dim re-read the last 4 (their q is 0 and they are never
+    // stored). Called only with limit >= 1.
     auto load = [&](int g, f32x4 (&kv)[NV], f32x4 (&vv)[NV]) {
-        const int t = g * 8 + j;
-        const bool ok = g < n_groups && t < limit;
-        const float* kr = kc + (size_t)t * stride + d0;
-        const float* vr = vc + (size_t)t * stride + d0;
+        const int t = min(g * 8 + j, limit - 1);
+        const float* kr = kc + (size_t)t * stride;
+        const float* vr = vc + (size_t)t * stride;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const bool in = ok && d0 + 4 * i < hd;
-            kv[i] = in ? *reinterpret_cast<const f32x4*>(kr + 4 * i) : f32x4{0.f, 0.f, 0.f, 0.f};
-            vv[i] = in ? *reinterpret_cast<const f32x4*>(vr + 4 * i) : f32x4{0.f, 0.f, 0.f, 0.f};
+            const int d = min(d0 + 4 * i, hd - 4);
+            kv[i] = *reinterpret_cast<const f32x4*>(kr + d);
+            vv[i] = *reinterpret_cast<const f32x4*>(vr + d);
         }
     };
-    f32x4 k0[NV], v0[NV], k1[NV], v1[NV];
+    f32x4 k0[NV], v0[NV], k1[NV], v1[NV], k2[NV], v2[NV];
     constexpr float kLog2e = 1.4426950408889634f;
     auto step = [&](int g, const f32x4 (&kv)[NV], const f32x4 (&vv)[NV]) {
         float part = 0.0f;
@@ -124,17 +128,39 @@ __global__ __launch_bounds__(kRswaWaves * 64) void rswa_kernel(RswaArgs a) {
             for (int c = 0; c < 4; ++c) acc[i][c] = fmaf(acc[i][c], alpha, beta * vv[i][c]);
         m = m_new;
     };
-    // groups wave, wave + 8, ...; one group's loads in flight beyond the one in use
+    // groups wave, wave + 8, ...; two groups' loads in flight beyond the one in
+    // use (three register buffers in rotation), one for head_dim > 128
+    constexpr int GS = kRswaWaves;
     int g = wave;
-    if (g < n_groups) load(g, k0, v0);
-    while (g < n_groups) {
-        load(g + kRswaWaves, k1, v1);
-        step(g, k0, v0);
-        g += kRswaWaves;
-        if (g >= n_groups) break;
-        load(g + kRswaWaves, k0, v0);
-        step(g, k1, v1);
-        g += kRswaWaves;
+    if constexpr (HDP <= 128) {
+        if (g < n_groups) {
+            load(g, k0, v0);
+            load(g + GS, k1, v1);
+        }
+        while (g < n_groups) {
+            load(g + 2 * GS, k2, v2);
+            step(g, k0, v0);
+            g += GS;
+            if (g >= n_groups) break;
+            load(g + 2 * GS, k0, v0);
+            step(g, k1, v1);
+            g += GS;
+            if (g >= n_groups) break;
+            load(g + 2 * GS, k1, v1);
+            step(g, k2, v2);
+            g += GS;
+        }
+    } else {
+        if (g < n_groups) load(g, k0, v0);
+        while (g < n_groups) {
+            load(g + GS, k1, v1);
+            step(g, k0, v0);
+            g += GS;
+            if (g >= n_groups) break;
+            load(g + GS, k0, v0);
+            step(g, k1, v1);
+            g += GS;
+        }
     }
     // sum the 8 key slots of the wave (same m within the wave)
 #pragma unroll
