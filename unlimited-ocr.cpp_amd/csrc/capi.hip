@@ -739,7 +739,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     dn.n_rows = L->hidden;
     dn.k = L->inter;
     dn.act_out = nullptr;
-    dn.y_out = (float*)(ws + p.y);
+    dn.y_out = (f16*)(ws + p.y);
     HIP_TRY(launch_experts_prefill(dn, false, p.max_tiles, st),
             "down launch");
     stage(4);

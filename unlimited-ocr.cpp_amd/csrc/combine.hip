@@ -7,7 +7,13 @@
 namespace uocr_hip {
 
 // out[t] = residual[t] + (sum_j fma(w[t,j], y[pos[t,j]]) in j order) + shared(t)
-// (src/engine/moe_decoder.cpp:88-97,111-112,179).
+// (src/engine/moe_decoder.cpp:88-97,111-112,179); the y rows are f16, widened
+// exactly, and every sum is in f32.
+__device__ __forceinline__ f32x4 load_y4(const f16* p) {
+    const f16x4 h = *reinterpret_cast<const f16x4*>(p);
+    return f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+}
+
 __global__ __launch_bounds__(1024) void combine_kernel(CombineArgs c) {
     const int t = blockIdx.x;
     const int H = c.hidden;
@@ -16,15 +22,14 @@ __global__ __launch_bounds__(1024) void combine_kernel(CombineArgs c) {
         for (int j = 0; j < c.top_k; ++j) {
             const int slot = c.pos[(size_t)t * c.top_k + j];
             const float w = c.weights[(size_t)t * c.top_k + j];
-            const f32x4 yv = *reinterpret_cast<const f32x4*>(c.y + (size_t)slot * H + col);
+            const f32x4 yv = load_y4(c.y + (size_t)slot * H + col);
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[i] = fmaf(w, yv[i], acc[i]);
         }
         if (c.n_virtual > 0) {
-            f32x4 sh = *reinterpret_cast<const f32x4*>(c.y + (size_t)(c.offsets[c.n_experts] + t) * H + col);
+            f32x4 sh = load_y4(c.y + (size_t)(c.offsets[c.n_experts] + t) * H + col);
             for (int v = 1; v < c.n_virtual; ++v) {
-                const f32x4 yv =
-                    *reinterpret_cast<const f32x4*>(c.y + (size_t)(c.offsets[c.n_experts + v] + t) * H + col);
+                const f32x4 yv = load_y4(c.y + (size_t)(c.offsets[c.n_experts + v] + t) * H + col);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) sh[i] += yv[i];
             }

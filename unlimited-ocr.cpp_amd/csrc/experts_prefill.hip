@@ -215,7 +215,7 @@ __global__ __launch_bounds__(256) void experts_prefill_kernel(ExpertArgs a) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int col = ntile * kPreBN + wn * 64 + j * 16 + (lane & 15);
-                    a.y_out[orow + col] = acc[i][j][r];
+                    a.y_out[orow + col] = (f16)acc[i][j][r];
                 }
             }
         }
@@ -502,9 +502,11 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
                 for (int i = 0; i < 8 * JN; ++i) {
                     const int m = wave * 32 * JN + i * 4 + er;
                     const f32x4 v = *reinterpret_cast<const f32x4*>(ep + (i * 4 + er) * kEpStride + ec);
+                    // f16 rows (8 bytes per lane, 128 contiguous bytes per row)
+                    const f16x4 h = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
                     if (m < rows)
-                        *reinterpret_cast<f32x4*>(a.y_out + (size_t)(slot0 + m) * a.n_rows + ntile * kBigBN + pass * 64 +
-                                                  ec / 4) = v;
+                        *reinterpret_cast<f16x4*>(a.y_out + (size_t)(slot0 + m) * a.n_rows + ntile * kBigBN + pass * 64 +
+                                                  ec / 4) = h;
                 }
             }
         }

@@ -95,11 +95,11 @@ struct ExpertArgs {
     const int* tile_info;    // [max tiles][4]: e, m0, rows, first slot
     const int* n_tiles;
     f16* act_out;            // gate/up: [slots, n_rows] f16
-    float* y_out;            // down: [slots, n_rows] f32
+    f16* y_out;              // down: [slots, n_rows] f16 (summed in f32 by the combine)
 };
 
 struct CombineArgs {
-    const float* y;        // [slots, hidden]
+    const f16* y;          // [slots, hidden] f16 down outputs
     const int* pos;        // [seq, top_k]
     const float* weights;  // [seq, top_k]
     const int* offsets;    // virtual groups start at offsets[n_experts + v]
