@@ -204,33 +204,41 @@ def _cpu_model():
     return None
 
 
-def cpu_baseline(seconds=10.0):
+def cpu_baseline(seconds=10.0, par_seconds=4.0):
     """Oracle (port of the reference CPU path) on config 1's 16 tokens, repeated
-    for ~`seconds`. Threads: the box's CPU share for one GPU (16, or fewer if the
-    host has fewer), one token per thread at a time. The reference itself runs a
-    token's routed experts serially and uses OpenMP only inside the router and
-    shared-expert GEMMs (src/runtime/weights.cpp:51-72, src/kernels/cpu_ops.cpp:11-39);
-    the per-token parallelism here is a stated deviation that favours the CPU."""
+    for ~`seconds`, with the reference's threading: one thread runs the tokens
+    and each token's routed experts in order (src/engine/moe_decoder.cpp:76-113,
+    src/runtime/weights.cpp:51-72 serial INT4 matvecs; the INT4 shared expert is
+    serial too, and the router GEMM's OpenMP split moves well under 1% of the
+    work). A second, shorter run with one token per thread over the box's CPU
+    share is reported beside it as a deviation from the reference's threading."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     from uocr_hip import synth
 
     wl = synth.make_config(1)
     nproc = os.cpu_count() or 1
+
+    def timed(threads, budget):
+        n = 0
+        t0 = time.perf_counter()
+        while True:
+            O.moe_layer(wl.layers[0], wl.x, threads=threads)
+            n += 1
+            if time.perf_counter() - t0 > budget:
+                break
+        dt = time.perf_counter() - t0
+        return n, dt
+
+    n, dt = timed(1, seconds)
     threads = min(16, nproc)
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        O.moe_layer(wl.layers[0], wl.x, threads=threads)
-        n += 1
-        if time.perf_counter() - t0 > seconds:
-            break
-    dt = time.perf_counter() - t0
-    return {"value": n * wl.seq / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+    pn, pdt = timed(threads, par_seconds)
+    return {"value": n * wl.seq / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
             "nproc": nproc, "cpu_model": _cpu_model(), "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
-            "threading": "tokens in parallel, one thread per token (reference: routed experts serial per "
-                         "token, OpenMP only in router/shared GEMMs)",
+            "threading": "reference: tokens and routed experts in order on one thread",
             "sample": f"config 1 layer (16 tokens, all routed+shared experts) x{n} runs, {dt:.1f}s",
+            "token_parallel": {"value": pn * wl.seq / pdt, "cores": threads,
+                               "sample": f"x{pn} runs, {pdt:.1f}s, one token per thread (not the reference's threading)"},
             "note": "reported baseline, not the target"}
 
 
