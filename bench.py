@@ -320,6 +320,9 @@ def main():
     ap.add_argument("--replicas", type=int, default=6)
     ap.add_argument("--extra", default="0,2,3,4,rswa",
                     help="extra configs to report: 0,2,3,4 and rswa (R-SWA decode attention); '' = none")
+    ap.add_argument("--graph", default="",
+                    help="decode configs (0, 1) replayed from a hipGraph, as a decode engine runs its step; "
+                         "their eager rate is reported beside it (config 4 always runs as a graph)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run a plain copy of BYTES bytes (counter calibration)")
@@ -332,7 +335,8 @@ def main():
               "single MI355X; multi-GPU expert parallelism is design-only)", file=sys.stderr)
         sys.exit(2)
 
-    main_res = run_config(1, args.steps, args.warmup, args.replicas)
+    graph_cfgs = {v.strip() for v in args.graph.split(",") if v.strip()}
+    main_res = run_config(1, args.steps, args.warmup, args.replicas, graph="1" in graph_cfgs)
     extras = {}
     for c in [v.strip() for v in args.extra.split(",") if v.strip()]:
         if c == "rswa":
@@ -345,7 +349,8 @@ def main():
                 extras[f"4_g{g}"] = r
         else:
             extras[str(c)] = run_config(c, max(args.steps // (10 if c >= 2 else 1), 10),
-                                        max(args.warmup // 4, 3), 3 if c >= 2 else args.replicas)
+                                        max(args.warmup // 4, 3), 3 if c >= 2 else args.replicas,
+                                        graph=str(c) in graph_cfgs)
     cpu = None if args.no_cpu else cpu_baseline()
     dom = main_res["dominant"]
     line = {
