@@ -335,6 +335,10 @@ int uocr_hip_scale_columns_f32(const float* w, int rows, int cols, const float* 
  * and out. Attention uses scale 1/sqrt(head_dim) and an online softmax over
  * the rows in any order (the reference kernel walks them in order with
  * __expf); results match the CPU RSWACache::attention within 1e-4 abs.
+ * When the (row, head) count cannot fill the GPU (decode), the keys are split
+ * over up to 8 workgroups whose partial results go through a 4 MiB
+ * library-owned device buffer and a second kernel merges them: such calls on
+ * different streams of one device must not overlap.
  * Decode over the first kv_len rows: q/out [heads, head_dim]
  * (cuda_ops.h:59-63). */
 int uocr_hip_rswa_attention_decode(const float* q, const float* kcache, const float* vcache, int kv_len, int heads,

@@ -214,3 +214,45 @@ def test_rejects_unsupported_head_dim(dev):
     x = torch.zeros(64, dtype=torch.float32, device=dev)
     with pytest.raises(HipError, match="head_dim"):
         ok(lib().uocr_hip_rswa_attention_decode(ptr(x), ptr(x), ptr(x), 1, 1, 1, 6, ptr(x), None))
+
+
+@pytest.mark.parametrize("kv_heads,heads,hd,kv_len", [(10, 10, 128, 1128), (3, 6, 256, 1000), (2, 8, 64, 700)])
+def test_long_cache_key_split(dev, kv_heads, heads, hd, kv_len):
+    """Decode rows over long caches: few (row, head) workgroups, so the keys
+    are split over several workgroups and merged (flash-decoding); the
+    single-cache, device-length and batched entry points against the oracle."""
+    torch = _t()
+    rng = np.random.default_rng(kv_len + hd)
+    print(f"[rswa] key split kv_heads={kv_heads} heads={heads} hd={hd} kv_len={kv_len}", flush=True)
+    K, V = rand(rng, kv_len, kv_heads, hd), rand(rng, kv_len, kv_heads, hd)
+    kc, vc = dev_f32(K, dev), dev_f32(V, dev)
+    q = rand(rng, 1, heads, hd)
+    want = O.rswa_attention(q, K, V, kv_len, 0, heads, kv_heads, hd, False).ravel()
+    out = torch.empty(heads * hd, dtype=torch.float32, device=dev)
+    ok(lib().uocr_hip_rswa_attention_decode(ptr(dev_f32(q, dev)), ptr(kc), ptr(vc), kv_len, heads, kv_heads, hd,
+                                            ptr(out), None))
+    torch.cuda.synchronize()
+    assert np.abs(out.cpu().numpy() - want).max() <= TOL
+    out.zero_()
+    ok(lib().uocr_hip_rswa_attention_devlen(ptr(dev_f32(q, dev)), ptr(kc), ptr(vc), ptr(dev_i32([kv_len], dev)),
+                                            1, kv_len - 1, heads, kv_heads, hd, 1, ptr(out), None))
+    torch.cuda.synchronize()
+    assert np.abs(out.cpu().numpy() - want).max() <= TOL
+    # batched: slots of one cache array with lengths from 1 to the capacity
+    lens = [kv_len, 1, kv_len // 3, kv_len - 5]
+    n, st = len(lens), kv_heads * hd
+    kb = rand(rng, n, kv_len, st)
+    vb = rand(rng, n, kv_len, st)
+    slots = np.array([2, 0, 3, 1, 0], np.int32)
+    qb = rand(rng, len(slots), heads, hd)
+    outb = torch.empty(qb.size, dtype=torch.float32, device=dev)
+    ok(lib().uocr_hip_rswa_attention_batch(ptr(dev_f32(qb, dev)), ptr(dev_f32(kb, dev)), ptr(dev_f32(vb, dev)),
+                                           ptr(dev_i32(lens, dev)), ptr(dev_i32(slots, dev)), len(slots), kv_len,
+                                           heads, kv_heads, hd, ptr(outb), None))
+    torch.cuda.synchronize()
+    got = outb.cpu().numpy().reshape(len(slots), heads * hd)
+    for b, s in enumerate(slots):
+        Ks = kb[s].reshape(kv_len, kv_heads, hd)
+        Vs = vb[s].reshape(kv_len, kv_heads, hd)
+        wb = O.rswa_attention(qb[b:b + 1], Ks, Vs, lens[s], 0, heads, kv_heads, hd, False).ravel()
+        assert np.abs(got[b] - wb).max() <= TOL, (b, s)

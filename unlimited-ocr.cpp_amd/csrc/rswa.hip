@@ -8,8 +8,8 @@
 //
 // Attention: one workgroup per (query row, head), 8 waves splitting the keys.
 // A wave takes groups of 8 consecutive keys (groups w, w + 8, ...): lane
-// (j, p) = (lane / 8, lane % 8) holds key j's dims [p*D, (p+1)*D) of K and V
-// (D = HDP / 8; a key row is one contiguous 16-byte-per-lane read by 8 lanes),
+// (j, p) = (lane / 8, lane % 8) holds key j's dims 4p + 32i .. + 3 (i < HDP / 32)
+// of K and V (each load: the 8 lanes of a key read one contiguous 128-byte run),
 // with the next two groups' K and V loads (one for head_dim > 128) issued
 // before the current group is used. Scores reduce over the 8 lanes of a key, the online softmax runs per
 // wave (max, rescale, sum over the group's keys), and each lane accumulates
@@ -18,7 +18,9 @@
 // streams kv_len * head_dim * 8 bytes of K and V.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <initializer_list>
+#include <mutex>
 #include <string>
 
 #include "common.hpp"
@@ -44,7 +46,12 @@ struct RswaArgs {
     const int* d_slots;
     const int* d_pos;
     int batch_cap;
+    int n_chunks;  // > 1: keys split over blockIdx.z, partial (m, l, o) records to part
+    float* part;   // [rows][heads][n_chunks][kRswaRec]
 };
+
+// one partial record: m, l, (pad), then o[head_dim]
+constexpr int kRswaRec = 256 + 4;
 
 template <int HDP>
 __global__ __launch_bounds__(kRswaWaves * 64) void rswa_kernel(RswaArgs a) {
@@ -70,31 +77,41 @@ __global__ __launch_bounds__(kRswaWaves * 64) void rswa_kernel(RswaArgs a) {
     const size_t qoff = ((size_t)row * a.heads + head) * hd;
     kc += (size_t)kvh * hd;
     vc += (size_t)kvh * hd;
-    const int d0 = p * D;
+    // lane p's dims: 4 at 4p + 32i (i < NV), so the 8 lanes of a key read one
+    // contiguous 128-byte run per load
+    auto dim_of = [&](int i) { return 4 * p + 32 * i; };
 
     f32x4 qv[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i)
-        qv[i] = d0 + 4 * i < hd ? *reinterpret_cast<const f32x4*>(a.q + qoff + d0 + 4 * i) : f32x4{0.f, 0.f, 0.f, 0.f};
+        qv[i] = dim_of(i) < hd ? *reinterpret_cast<const f32x4*>(a.q + qoff + dim_of(i)) : f32x4{0.f, 0.f, 0.f, 0.f};
 
     float m = -INFINITY, l = 0.0f;
     f32x4 acc[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int n_groups = (limit + 7) / 8;
+    // this workgroup's keys [kbeg, kend): chunk blockIdx.z of n_chunks (chunks
+    // of whole 8-key groups; a chunk past the limit has no keys)
+    int kbeg = 0, kend = limit;
+    if (a.n_chunks > 1) {
+        const int cs = ((limit + a.n_chunks - 1) / a.n_chunks + 7) & ~7;
+        kbeg = min(limit, (int)blockIdx.z * cs);
+        kend = min(limit, kbeg + cs);
+    }
+    const int n_groups = (kend - kbeg + 7) / 8;
     // Unpredicated loads (a lane-predicated load makes the compiler wait for
     // every outstanding load before the first use, defeating the prefetch):
     // keys past the limit re-read the last valid row (their weight is 0),
     // dims past head_dim re-read the last 4 (their q is 0 and they are never
     // stored). Called only with limit >= 1.
     auto load = [&](int g, f32x4 (&kv)[NV], f32x4 (&vv)[NV]) {
-        const int t = min(g * 8 + j, limit - 1);
+        const int t = min(kbeg + g * 8 + j, kend - 1);
         const float* kr = kc + (size_t)t * stride;
         const float* vr = vc + (size_t)t * stride;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const int d = min(d0 + 4 * i, hd - 4);
+            const int d = min(dim_of(i), hd - 4);
             kv[i] = *reinterpret_cast<const f32x4*>(kr + d);
             vv[i] = *reinterpret_cast<const f32x4*>(vr + d);
         }
@@ -110,7 +127,7 @@ __global__ __launch_bounds__(kRswaWaves * 64) void rswa_kernel(RswaArgs a) {
         part += __shfl_xor(part, 1, 64);
         part += __shfl_xor(part, 2, 64);
         part += __shfl_xor(part, 4, 64);
-        const bool valid = g * 8 + j < limit;
+        const bool valid = kbeg + g * 8 + j < kend;
         const float s = valid ? part * a.scale : -INFINITY;
         float mg = fmaxf(s, __shfl_xor(s, 8, 64));
         mg = fmaxf(mg, __shfl_xor(mg, 16, 64));
@@ -177,7 +194,7 @@ __global__ __launch_bounds__(kRswaWaves * 64) void rswa_kernel(RswaArgs a) {
     __shared__ __attribute__((aligned(16))) float wacc[kRswaWaves][HDP];
     if (lane < 8) {
 #pragma unroll
-        for (int i = 0; i < NV; ++i) *reinterpret_cast<f32x4*>(&wacc[wave][d0 + 4 * i]) = acc[i];
+        for (int i = 0; i < NV; ++i) *reinterpret_cast<f32x4*>(&wacc[wave][dim_of(i)]) = acc[i];
     }
     if (lane == 0) {
         wm[wave] = m;
@@ -185,6 +202,20 @@ __global__ __launch_bounds__(kRswaWaves * 64) void rswa_kernel(RswaArgs a) {
     }
     __syncthreads();
     // combine the waves (a wave without keys has m = -inf and weight 0)
+    float* rec = a.n_chunks > 1 ? a.part + (((size_t)row * a.heads + head) * a.n_chunks + blockIdx.z) * kRswaRec
+                                : nullptr;
+    if (rec && tid == 0) {
+        float M = -INFINITY, L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kRswaWaves; ++w) M = fmaxf(M, wm[w]);
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < kRswaWaves; ++w)
+                L = fmaf(wl[w], wm[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((wm[w] - M) * kLog2e), L);
+        }
+        rec[0] = M;
+        rec[1] = L;
+    }
     for (int d = tid; d < hd; d += kRswaWaves * 64) {
         float M = -INFINITY;
 #pragma unroll
@@ -198,7 +229,33 @@ __global__ __launch_bounds__(kRswaWaves * 64) void rswa_kernel(RswaArgs a) {
                 o = fmaf(wacc[w][d], f, o);
             }
         }
-        a.out[qoff + d] = L > 0.0f ? o / L : 0.0f;
+        if (rec)
+            rec[4 + d] = o;  // unnormalised, relative to this chunk's max
+        else
+            a.out[qoff + d] = L > 0.0f ? o / L : 0.0f;
+    }
+}
+
+// Merge of the n_chunks partial records of each (row, head): the
+// flash-decoding combine, chunks in key order.
+__global__ __launch_bounds__(256) void rswa_merge_kernel(const float* part, float* out, int heads, int head_dim,
+                                                         int n_chunks) {
+    constexpr float kLog2e = 1.4426950408889634f;
+    const int row = blockIdx.x, head = blockIdx.y;
+    const float* rec = part + ((size_t)row * heads + head) * n_chunks * kRswaRec;
+    float M = -INFINITY;
+    for (int c = 0; c < n_chunks; ++c) M = fmaxf(M, rec[(size_t)c * kRswaRec]);
+    for (int d = threadIdx.x; d < head_dim; d += blockDim.x) {
+        float L = 0.0f, o = 0.0f;
+        if (M != -INFINITY) {
+            for (int c = 0; c < n_chunks; ++c) {
+                const float m = rec[(size_t)c * kRswaRec];
+                const float f = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m - M) * kLog2e);
+                L = fmaf(rec[(size_t)c * kRswaRec + 1], f, L);
+                o = fmaf(rec[(size_t)c * kRswaRec + 4 + d], f, o);
+            }
+        }
+        out[((size_t)row * heads + head) * head_dim + d] = L > 0.0f ? o / L : 0.0f;
     }
 }
 
@@ -275,13 +332,61 @@ int check_ptrs(std::initializer_list<const void*> ps) {
     return UOCR_HIP_OK;
 }
 
-int launch_attention(RswaArgs a, int rows, hipStream_t st) {
+// Partial records of the key-split attention: a library-owned device buffer
+// (the reference's attention signatures carry no workspace). Calls that split
+// on one device share it, so split calls on different streams of one device
+// must not overlap; a call whose records would not fit runs unsplit.
+constexpr int kRswaPartRecs = 4096;
+__device__ float g_rswa_part[(size_t)kRswaPartRecs * kRswaRec];
+std::mutex g_rswa_mu;
+float* g_rswa_part_ptr[64] = {};
+int g_rswa_cus[64] = {};
+
+// device address of g_rswa_part and the CU count of the current device
+int rswa_device(float** part, int* cus) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= 64) return -1;
+    std::lock_guard<std::mutex> lock(g_rswa_mu);
+    if (!g_rswa_part_ptr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_rswa_part)) != hipSuccess) return -1;
+        if (hipDeviceGetAttribute(&g_rswa_cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
+        g_rswa_part_ptr[dev] = static_cast<float*>(p);
+    }
+    *part = g_rswa_part_ptr[dev];
+    *cus = g_rswa_cus[dev];
+    return 0;
+}
+
+// max_len: an upper bound of any row's key count (0: unknown). When rows x
+// heads workgroups cannot fill the chip (decode), the keys of each (row, head)
+// are split into chunks of at least 128 keys over up to 8 workgroups, then
+// merged by a second kernel.
+int launch_attention(RswaArgs a, int rows, hipStream_t st, int max_len) {
     if (rows <= 0) return UOCR_HIP_OK;
     a.scale = 1.0f / sqrtf((float)a.head_dim);
-    const dim3 grid(rows, a.heads), block(kRswaWaves * 64);
+    a.n_chunks = 1;
+    float* part = nullptr;
+    int cus = 0;
+    const long long wgs = (long long)rows * a.heads;
+    if (wgs < 512 && rswa_device(&part, &cus) == 0) {
+        int n = (int)((2LL * cus + wgs - 1) / wgs);
+        if (max_len > 0) n = std::min(n, max_len / 128);
+        n = std::min(n, 8);
+        while (n > 1 && wgs * n > kRswaPartRecs) --n;
+        if (n > 1) {
+            a.n_chunks = n;
+            a.part = part;
+        }
+    }
+    const dim3 grid(rows, a.heads, a.n_chunks), block(kRswaWaves * 64);
     if (a.head_dim <= 64) launch_k(rswa_kernel<64>, grid, block, 0, st, a);
     else if (a.head_dim <= 128) launch_k(rswa_kernel<128>, grid, block, 0, st, a);
     else launch_k(rswa_kernel<256>, grid, block, 0, st, a);
+    if (a.n_chunks > 1)
+        launch_k(rswa_merge_kernel, dim3(rows, a.heads), dim3(std::min(256, (a.head_dim + 63) / 64 * 64)), 0, st,
+                 (const float*)a.part, a.out, a.heads, a.head_dim, a.n_chunks);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? UOCR_HIP_OK : set_error(UOCR_HIP_EHIP, std::string("rswa launch: ") + hipGetErrorString(e));
 }
@@ -304,7 +409,7 @@ int uocr_hip_rswa_attention_decode(const float* q, const float* kcache, const fl
     if (int rc = check_ptrs({q, kcache, vcache, out})) return rc;
     if (kv_len < 0) return set_error(UOCR_HIP_EINVAL, "kv_len must be >= 0");
     RswaArgs a{q, kcache, vcache, out, heads, kv_heads, head_dim, 0.f, 0, kv_len, 0, 0, nullptr, nullptr, nullptr, 0};
-    return launch_attention(a, 1, (hipStream_t)stream);
+    return launch_attention(a, 1, (hipStream_t)stream, kv_len);
 }
 
 int uocr_hip_rswa_attention(const float* q, const float* kcache, const float* vcache, int kv_len, int seq,
@@ -315,7 +420,7 @@ int uocr_hip_rswa_attention(const float* q, const float* kcache, const float* vc
     if (kv_len < 0 || seq < 0) return set_error(UOCR_HIP_EINVAL, "kv_len and seq must be >= 0");
     RswaArgs a{q, kcache, vcache, out, heads, kv_heads, head_dim, 0.f, 0, kv_len, q_start, causal != 0,
                nullptr, nullptr, nullptr, 0};
-    return launch_attention(a, seq, (hipStream_t)stream);
+    return launch_attention(a, seq, (hipStream_t)stream, kv_len);
 }
 
 int uocr_hip_rswa_attention_devlen(const float* q, const float* kcache, const float* vcache, const int* d_len,
@@ -326,7 +431,7 @@ int uocr_hip_rswa_attention_devlen(const float* q, const float* kcache, const fl
     if (!d_len || seq < 0) return set_error(UOCR_HIP_EINVAL, "null d_len or negative seq");
     RswaArgs a{q, kcache, vcache, out, heads, kv_heads, head_dim, 0.f, 1, 0, q_start, causal != 0,
                d_len, nullptr, nullptr, 0};
-    return launch_attention(a, seq, (hipStream_t)stream);
+    return launch_attention(a, seq, (hipStream_t)stream, 0);
 }
 
 int uocr_hip_rswa_attention_batch(const float* q, const float* kcache_base, const float* vcache_base,
@@ -338,7 +443,7 @@ int uocr_hip_rswa_attention_batch(const float* q, const float* kcache_base, cons
     if (!d_len || !d_slots || batch_cap <= 0) return set_error(UOCR_HIP_EINVAL, "null d_len/d_slots or batch_cap <= 0");
     RswaArgs a{q, kcache_base, vcache_base, out, heads, kv_heads, head_dim, 0.f, 2, 0, 0, 0,
                d_len, d_slots, nullptr, batch_cap};
-    return launch_attention(a, batch, (hipStream_t)stream);
+    return launch_attention(a, batch, (hipStream_t)stream, batch_cap);
 }
 
 int uocr_hip_rswa_attention_ragged(const float* q, const float* kcache_base, const float* vcache_base,
@@ -350,7 +455,7 @@ int uocr_hip_rswa_attention_ragged(const float* q, const float* kcache_base, con
     if (!d_slots || !d_pos || batch_cap <= 0) return set_error(UOCR_HIP_EINVAL, "null d_slots/d_pos or batch_cap <= 0");
     RswaArgs a{q, kcache_base, vcache_base, out, heads, kv_heads, head_dim, 0.f, 3, 0, 0, 0,
                nullptr, d_slots, d_pos, batch_cap};
-    return launch_attention(a, total, (hipStream_t)stream);
+    return launch_attention(a, total, (hipStream_t)stream, batch_cap);
 }
 
 int uocr_hip_rswa_append_decode(const float* k, const float* v, float* kcache, float* vcache, int* d_len,
