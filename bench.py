@@ -348,7 +348,7 @@ def main():
                 r = run_config(4, max(args.steps // 10, 5), 3, 1, group=g, graph=True)
                 extras[f"4_g{g}"] = r
         else:
-            extras[str(c)] = run_config(c, max(args.steps // (10 if c >= 2 else 1), 10),
+            extras[str(c)] = run_config(c, max(args.steps // (5 if c >= 2 else 1), 20),
                                         max(args.warmup // 4, 3), 3 if c >= 2 else args.replicas,
                                         graph=str(c) in graph_cfgs)
     cpu = None if args.no_cpu else cpu_baseline()
