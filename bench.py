@@ -189,6 +189,16 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False):
                 res["dominant"] = {"kernel": "expert_decode_kernel<4, 10, true> (gate+up)", "ms": stage["gate_up"],
                                    "bytes": avg["gate_up"], "gbs": res["gate_up_gbs"],
                                    "traffic_file": "expert_gate_up_decode_config1_traffic.md"}
+    # the fused decode kernel's sticky status (bit 0: a bounded cross-workgroup
+    # wait timed out, bit 1: an exact pick outside the candidates): any set bit
+    # means some timed call returned NaN rows, so the measurement is void
+    flags = 0
+    for lay in layers:
+        flags |= lay.status(clear=True)
+    res["status_flags"] = flags
+    if flags:
+        print(f"bench.py: config {cfg}: layer status flags {flags:#x} (a fused call timed out or "
+              "picked outside its candidates; its outputs were NaN)", file=sys.stderr)
     for lay in layers:
         lay.close()
     return res
@@ -378,6 +388,7 @@ def main():
         "cpu_baseline": cpu,
         "configs": extras,
     }
+    line["status_flags"] = main_res.get("status_flags")
     print(json.dumps(line))
 
 
