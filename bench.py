@@ -168,12 +168,13 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False):
                    gate_up_bytes=avg["gate_up"], gate_up_flops=fl_gu)
         if stage and "fused" in stage:
             # one kernel for the whole layer: its algorithmic bytes are the
-            # layer's (touched experts only, although the dense gate/up pass
-            # reads every expert by design)
+            # layer's (touched experts only, although from 12 tokens the dense
+            # gate/up pass reads every expert by design)
             fu = stage["fused"] * 1e-3
             res["dominant"] = {"kernel": "decode_fused_kernel<4, 10, 7> (router + experts + combine)",
                                "ms": stage["fused"], "bytes": avg["total"],
-                               "gbs": avg["total"] / fu / 1e9, "traffic_file": "decode_fused_config1_traffic.md"}
+                               "gbs": avg["total"] / fu / 1e9,
+                               "traffic_file": "decode_fused_config1_traffic.md" if cfg == 1 else None}
         elif stage:
             gu = stage["gate_up"] * 1e-3
             res["gate_up_gbs"] = avg["gate_up"] / gu / 1e9

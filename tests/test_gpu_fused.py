@@ -46,9 +46,9 @@ def _status_clear(layer, label):
 @pytest.mark.parametrize("group", [32, 64, 128])
 def test_fused_batch_sizes_one_layer(dev, group):
     """One layer object, the batch size changing between calls: 12..16 tokens
-    run the single-kernel path, 1..11 tokens the four-launch decode path, so
-    the fused kernel's progress words must stay consistent across calls that
-    skip it."""
+    run the single kernel with dense gate/up, 1..11 tokens the same kernel with
+    gate/up over the candidate groups only, so the progress words and the
+    schedule must stay consistent across calls that switch modes."""
     from uocr_hip import MoELayerInt4, synth
     L = synth.random_layer(4100 + group, group=group)
     layer = MoELayerInt4(L)

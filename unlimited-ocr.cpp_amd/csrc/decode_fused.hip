@@ -658,13 +658,20 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
         publish();
     }
 
-    // ---- 2. gate/up (workers T .. P-1): every group for all tokens
-    const int ngu_total = G * RBG;
+    // ---- 2. gate/up (workers T .. P-1). Dense (kFusedDenseMinSeq tokens and
+    // more): every group for all tokens, no wait for the routing. Sparse (fewer
+    // tokens): the live groups only, after the candidate summary -- a few
+    // tokens touch few groups, so reading every group would cost more than
+    // waiting for the candidates.
+    const bool sparse = T < kFusedDenseMinSeq;
+    if (sparse) need_summary();
+    const int n_gu_groups = sparse ? n_live : G;
+    const int ngu_total = n_gu_groups * RBG;
     if (b >= T) {
         for (int i = b - T;; i += PW) {
             fresh_indices();
             if (i >= ngu_total) break;
-            gate_up_item(i / RBG, i % RBG, i + PW >= ngu_total);
+            gate_up_item(sparse ? live[i / RBG] : i / RBG, i % RBG, !sparse && i + PW >= ngu_total);
             pend = true;
         }
     }
@@ -676,10 +683,10 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
     // the live groups only (the routing summary first).
     need_summary();
     const int n_dn_groups = n_live;
-    const FusedSchedule sch(T, P, G, RBG, RBD, n_live);  // identical in every workgroup
+    const FusedSchedule sch(T, P, n_gu_groups, RBG, RBD, n_live);  // identical in every workgroup
     const int ndn_total = sch.ndn_total;
     // position of gate/up item r of the group at down position gpos
-    auto gu_index = [&](int gpos, int r_) { return live[gpos] * RBG + r_; };
+    auto gu_index = [&](int gpos, int r_) { return (sparse ? gpos : live[gpos]) * RBG + r_; };
     const int my_slot = sch.slot_of(b);
     for (int j = my_slot; j < ndn_total; j += P) {
         fresh_indices();

@@ -112,6 +112,7 @@ struct CombineArgs {
 // at creation): workgroup b publishes the number of steps it has finished this
 // call as base + steps, and leaves every call at base + kFusedSteps.
 constexpr int kFusedMaxSeq = 16;
+constexpr int kFusedDenseMinSeq = 12;  // fewer tokens: gate/up over the candidate groups only
 constexpr int kFusedMaxGrid = 4096;
 struct FusedSync {
     int progress[kFusedMaxGrid];
