@@ -142,14 +142,19 @@ def test_fused_tied_router_rows(dev, ulps):
     if ulps:
         L.router_bf16[20, 100] = L.router_bf16[9, 100] + np.uint16(ulps)
     layer = MoELayerInt4(L)
-    # small channels 1.. keep the bias order: five leaders, then the pair
-    x = synth.bf16_normal(np.random.default_rng(13), (16, L.hidden), 0.01)
-    x[:, 0] = 1.0
-    got = _forward(layer, x, dev)
-    _check(L, x, got, f"tied-{ulps}")
-    if ulps == 0:
-        assert (got[0] == 9).any(axis=1).all() and not (got[0] == 20).any(), "equal scores: lower index"
-    _status_clear(layer, f"tied-{ulps}")
+    # every candidate source: 16 tokens (dense, the routers' candidates), 7
+    # (sparse, the routers' candidates), 3 and 1 (sparse, the per-expert
+    # estimate workgroups)
+    for seq in (16, 7, 3, 1):
+        print(f"[fused] tied ulps={ulps} seq={seq}", flush=True)
+        # small channels 1.. keep the bias order: five leaders, then the pair
+        x = synth.bf16_normal(np.random.default_rng(13), (seq, L.hidden), 0.01)
+        x[:, 0] = 1.0
+        got = _forward(layer, x, dev)
+        _check(L, x, got, f"tied-{ulps}-t{seq}")
+        if ulps == 0:
+            assert (got[0] == 9).any(axis=1).all() and not (got[0] == 20).any(), "equal scores: lower index"
+        _status_clear(layer, f"tied-{ulps}-t{seq}")
     layer.close()
 
 

@@ -144,6 +144,105 @@ __device__ __forceinline__ void convert_own_rows(f16* As, int wave, int lane) {
 // 16-byte reads one 8-column block ahead, so a column costs the weight's
 // widening and the fmac. The router waves run at raised issue priority (the
 // other workgroup on the CU dequantises expert weights meanwhile).
+// Every expert that can be among the token's top_k after the exact chain,
+// from an estimate S of its logit and SA = sum |x w| (lane e: expert e, the
+// whole wave calls). The chain's rounding error is at most 2^-24 * H * SA
+// (recursive fma summation) and the estimate's at most 2^-24 * n_est * SA
+// with n_est the estimate's terms per partial sum plus its merge depth;
+// NTERMS = H + n_est + 64 bounds both with slack. Softmax: a candidate when
+// its upper bound reaches the top_k-th largest lower bound, less the logit
+// distance over which two probabilities can still round equal (equal scores go
+// to the lower index). Sigmoid: the same in score space. Non-finite input: all.
+__device__ __forceinline__ uint64_t candidate_mask(const DecodeArgs& a, float S, float SA, float nterms) {
+    const int lane = threadIdx.x & 63;
+    const int E = a.n_experts;
+    const bool valid = lane < E;
+    bool cand;
+    if (__ballot(valid && !(__builtin_isfinite(S) && __builtin_isfinite(SA)))) {
+        cand = valid;
+    } else {
+        const float B = nterms * 0x1p-24f * 1.02f * SA + 0x1p-22f * fabsf(S) + 1e-30f;
+        float lo = S - B, hi = S + B;
+        if (a.scoring_sigmoid) {
+            lo = (1.0f - 1e-5f) / (1.0f + __expf(-lo));
+            hi = (1.0f + 1e-5f) / (1.0f + __expf(-hi));
+        }
+        float rem = valid ? lo : -INFINITY, kth = -INFINITY;
+        for (int j = 0; j < a.top_k && j < E; ++j) {
+            kth = wave_max64(rem);
+            const uint64_t tie = __ballot(rem == kth);
+            if (lane == (int)__builtin_ctzll(tie)) rem = -INFINITY;
+        }
+        float slack = 0.0f;
+        if (!a.scoring_sigmoid) {
+            const float mx = wave_max64(valid ? fabsf(hi) : 0.0f);
+            slack = 0x1p-21f * (2.0f + fabsf(kth) + mx);
+        }
+        cand = valid && hi + slack >= kth;
+    }
+    return __ballot(cand);
+}
+
+// Logit estimates of expert e for the T tokens (one workgroup, up to
+// kFusedEstMaxSeq tokens): thread i takes columns 8i .. 8i + 7 (an fma chain
+// of 8 terms per token), the 256 partials then summed in a tree (8 levels);
+// published as tagged words est[t][e][0..1] (estimate, sum of |x w|).
+template <int KT>
+__device__ __forceinline__ void estimate_expert(const DecodeArgs& a, int e, unsigned rtag, float* red) {
+    constexpr int H = KT * 128;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int T = a.seq, E = a.n_experts;
+    float s[kFusedEstMaxSeq], sa[kFusedEstMaxSeq];
+#pragma unroll
+    for (int t = 0; t < kFusedEstMaxSeq; ++t) s[t] = sa[t] = 0.0f;
+    if (tid < H / 8) {
+        const u32x4 wv = *reinterpret_cast<const u32x4*>(a.router_t + ((size_t)tid * E + e) * 8);
+        float w[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            w[2 * i] = __uint_as_float(wv[i] << 16);
+            w[2 * i + 1] = __uint_as_float(wv[i] & 0xffff0000u);
+        }
+        const uint16_t* xb = static_cast<const uint16_t*>(a.x);
+#pragma unroll
+        for (int t = 0; t < kFusedEstMaxSeq; ++t) {
+            if (t < T) {
+                const u32x4 xv = *reinterpret_cast<const u32x4*>(xb + (size_t)t * H + tid * 8);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float x0 = __uint_as_float(xv[i] << 16), x1 = __uint_as_float(xv[i] & 0xffff0000u);
+                    s[t] = fmaf(x0, w[2 * i], s[t]);
+                    s[t] = fmaf(x1, w[2 * i + 1], s[t]);
+                    sa[t] = fmaf(fabsf(x0), fabsf(w[2 * i]), sa[t]);
+                    sa[t] = fmaf(fabsf(x1), fabsf(w[2 * i + 1]), sa[t]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < kFusedEstMaxSeq; ++t) {
+        if (t >= T) break;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            s[t] += __shfl_xor(s[t], o, 64);
+            sa[t] += __shfl_xor(sa[t], o, 64);
+        }
+        if (lane == 0) {
+            red[(wave * kFusedEstMaxSeq + t) * 2] = s[t];
+            red[(wave * kFusedEstMaxSeq + t) * 2 + 1] = sa[t];
+        }
+    }
+    __syncthreads();
+    if (tid < 2 * T) {
+        const int t = tid >> 1, k = tid & 1;
+        const float v = (red[(0 * kFusedEstMaxSeq + t) * 2 + k] + red[(1 * kFusedEstMaxSeq + t) * 2 + k]) +
+                        (red[(2 * kFusedEstMaxSeq + t) * 2 + k] + red[(3 * kFusedEstMaxSeq + t) * 2 + k]);
+        const uint64_t word = ((uint64_t)rtag << 32) | __float_as_uint(v);
+        __hip_atomic_store(a.sync->est + ((size_t)t * 64 + e) * 2 + k, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+}
+
 template <int KT>
 __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, float* hand, float* sc, float* topv,
                                                   uint64_t* etab, float* xs, float* part, unsigned rtag) {
@@ -201,42 +300,12 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
         part[wave * 128 + lane] = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
         part[wave * 128 + 64 + lane] = sa;
     };
-    // Every expert that can be among the token's top_k after the exact chain.
-    // The chain's rounding error is at most 2^-24 * H * sum|x w| (recursive
-    // fma summation), the blocked estimate's at most 2^-24 * (SEG / 8 + 6) *
-    // sum|x w|; both with slack. Softmax: candidate when its upper bound
-    // reaches the top_k-th largest lower bound, less the logit distance over
-    // which two probabilities can still round equal (equal scores go to the
-    // lower index). Sigmoid: the same in score space. Published as two tagged
-    // 32-bit halves of the expert mask.
+    // the candidates: an expert whose logit interval can reach the top_k
+    // (candidate_mask), published as two tagged 32-bit halves of the mask
     auto early_finish = [&]() {
-        const bool valid = lane < E;
         const float S = ((part[lane] + part[128 + lane]) + part[256 + lane]) + part[384 + lane];
         const float SA = ((part[64 + lane] + part[192 + lane]) + part[320 + lane]) + part[448 + lane];
-        bool cand;
-        if (__ballot(valid && !(__builtin_isfinite(S) && __builtin_isfinite(SA)))) {
-            cand = valid;
-        } else {
-            const float B = (float)(H + SEG / 8 + 64) * 0x1p-24f * 1.02f * SA + 0x1p-22f * fabsf(S) + 1e-30f;
-            float lo = S - B, hi = S + B;
-            if (a.scoring_sigmoid) {
-                lo = (1.0f - 1e-5f) / (1.0f + __expf(-lo));
-                hi = (1.0f + 1e-5f) / (1.0f + __expf(-hi));
-            }
-            float rem = valid ? lo : -INFINITY, kth = -INFINITY;
-            for (int j = 0; j < a.top_k && j < E; ++j) {
-                kth = wave_max64(rem);
-                const uint64_t tie = __ballot(rem == kth);
-                if (lane == (int)__builtin_ctzll(tie)) rem = -INFINITY;
-            }
-            float slack = 0.0f;
-            if (!a.scoring_sigmoid) {
-                const float mx = wave_max64(valid ? fabsf(hi) : 0.0f);
-                slack = 0x1p-21f * (2.0f + fabsf(kth) + mx);
-            }
-            cand = valid && hi + slack >= kth;
-        }
-        const uint64_t m = __ballot(cand);
+        const uint64_t m = candidate_mask(a, S, SA, (float)(H + SEG / 8 + 64));
         if (lane < 2) {
             const uint64_t w = ((uint64_t)rtag << 32) | (uint32_t)(lane == 0 ? m : (m >> 32));
             __hip_atomic_store(a.sync->cand + 2 * t + lane, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -397,18 +466,66 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
     };
     auto need_summary = [&]() {
         if (have_summary) return;
-        if (wave == 0) {
-            if (!have_cw) cand_prefetch();
+        if (T <= kFusedEstMaxSeq) {
+            // few tokens: the candidates from the per-expert estimates, wave w
+            // taking tokens w, w + 4, ... (each token's words requested
+            // before any is checked)
+            constexpr int TPW = (kFusedEstMaxSeq + 3) / 4;
+            const bool want = lane < E;
+            uint64_t w0[TPW], w1[TPW];
             int it = 0;
-            while (__ballot((uint32_t)(cw >> 32) != rtag)) {
+            while (true) {
+                bool stale = false;
+#pragma unroll
+                for (int u = 0; u < TPW; ++u) {
+                    const int t = wave + 4 * u;
+                    if (t < T && want) {
+                        w0[u] = __hip_atomic_load(sy->est + ((size_t)t * 64 + lane) * 2, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+                        w1[u] = __hip_atomic_load(sy->est + ((size_t)t * 64 + lane) * 2 + 1, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+                    } else {
+                        w0[u] = w1[u] = 0;
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < TPW; ++u)
+                    if (wave + 4 * u < T && want)
+                        stale |= (uint32_t)(w0[u] >> 32) != rtag || (uint32_t)(w1[u] >> 32) != rtag;
+                if (!__ballot(stale)) break;
                 if (++it > kSpinLimit) {
                     if (lane == 0) report_timeout(sy, rtag);
                     break;
                 }
                 __builtin_amdgcn_s_sleep(1);
-                if (lane < 2 * T) cw = __hip_atomic_load(sy->cand + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            if (lane < 2 * T) cm32[lane] = (uint32_t)cw;
+#pragma unroll
+            for (int u = 0; u < TPW; ++u) {
+                const int t = wave + 4 * u;
+                if (t >= T) break;
+                const uint64_t m = candidate_mask(a, __uint_as_float((uint32_t)w0[u]), __uint_as_float((uint32_t)w1[u]),
+                                                  (float)(H + 16 + 64));
+                if (lane == 0) {
+                    cm32[2 * t] = (uint32_t)m;
+                    cm32[2 * t + 1] = (uint32_t)(m >> 32);
+                }
+            }
+            __syncthreads();
+        }
+        if (wave == 0) {
+            if (T > kFusedEstMaxSeq) {
+                if (!have_cw) cand_prefetch();
+                int it = 0;
+                while (__ballot((uint32_t)(cw >> 32) != rtag)) {
+                    if (++it > kSpinLimit) {
+                        if (lane == 0) report_timeout(sy, rtag);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                    if (lane < 2 * T) cw = __hip_atomic_load(sy->cand + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                if (lane < 2 * T) cm32[lane] = (uint32_t)cw;
+            }
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
             // lane e: the tokens whose candidates hold expert e
             int tm = 0;
@@ -664,6 +781,11 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
     // tokens touch few groups, so reading every group would cost more than
     // waiting for the candidates.
     const bool sparse = T < kFusedDenseMinSeq;
+    // up to kFusedEstMaxSeq tokens: workgroups T .. T + E - 1 first estimate
+    // one expert's logits each (a router's own estimate waits for the whole
+    // router matrix; beyond a few tokens every workgroup's candidate
+    // computation over the tokens costs more than that wait)
+    if (T <= kFusedEstMaxSeq && b >= T && b < T + E) estimate_expert<KTG>(a, b - T, rtag, Cs);
     if (sparse) need_summary();
     const int n_gu_groups = sparse ? n_live : G;
     const int ngu_total = n_gu_groups * RBG;
@@ -743,6 +865,8 @@ static hipError_t launch_fused(const DecodeArgs& a, hipStream_t st) {
     // and fully resident (workgroups wait for one another)
     const int grid = std::min(resident, kFusedMaxGrid);
     if (grid <= a.seq) return hipErrorInvalidConfiguration;
+    // up to kFusedEstMaxSeq tokens every expert needs its estimating workgroup
+    if (a.seq <= kFusedEstMaxSeq && grid < a.seq + a.n_experts) return hipErrorInvalidConfiguration;
     // Plain launch: a cooperative launch (which refuses a grid that cannot be
     // resident at once) measured 53.6 us per call against 36.6 us on MI355X. The
     // grid is sized from the occupancy query; if other work keeps workgroups

@@ -113,6 +113,7 @@ struct CombineArgs {
 // call as base + steps, and leaves every call at base + kFusedSteps.
 constexpr int kFusedMaxSeq = 16;
 constexpr int kFusedDenseMinSeq = 12;  // fewer tokens: gate/up over the candidate groups only
+constexpr int kFusedEstMaxSeq = 4;     // up to this many: candidates from per-expert estimate workgroups
 constexpr int kFusedMaxGrid = 4096;
 struct FusedSync {
     int progress[kFusedMaxGrid];
@@ -123,6 +124,10 @@ struct FusedSync {
     // at 2t + 1; tag = (base >> 12) + 1 (24 bits): a reader validates each word
     // by its tag, with no separate wait for the router
     unsigned long long cand[2 * kFusedMaxSeq];
+    // up to kFusedEstMaxSeq tokens: logit estimates of (token t, expert e),
+    // one workgroup per expert, as (tag << 32) | float bits: [t][e][2] =
+    // estimate, sum of |x w|
+    unsigned long long est[kFusedEstMaxSeq * 64 * 2];
 };
 
 // Decode-sized layer (seq < 256): router_decode / expert passes / combine with
