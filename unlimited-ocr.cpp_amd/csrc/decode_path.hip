@@ -43,7 +43,10 @@ constexpr int kDecBM = 16;
 constexpr int kDecodeMaxEntries = 256 * kMaxTopK;  // seq < 256
 
 template <int GPT, int KT, bool GU, bool ZP>
-__global__ __launch_bounds__(256) void expert_decode_kernel(DecodeArgs a) {
+// three workgroups per CU (the routing ids are read from global memory, not
+// staged, so the LDS fits three), except the gate/up pass at g32 or with zero
+// points, which would spill at the register budget of three
+__global__ __launch_bounds__(256, (GU && (GPT == 4 || ZP)) ? 2 : 3) void expert_decode_kernel(DecodeArgs a) {
     constexpr int K = KT * kTileK;
     constexpr int NG = scale_row_stride(K, kTileK / GPT);
     constexpr int SROW = kTileRows * NG;
@@ -53,7 +56,6 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(DecodeArgs a) {
     __shared__ __attribute__((aligned(16))) f16 Ss[4][ZP ? 2 * NM : NM][SROW];
     constexpr int ZOFF = NM * SROW * 2;  // bytes from a scale row to its zero-offset row
     __shared__ int ent[256];
-    __shared__ int ids_s[kDecodeMaxEntries];
     __shared__ int hist[kMaxExperts], offs[kMaxExperts], live[kMaxExperts];
     __shared__ int n_live_s;
     __shared__ int ipre[kMaxExperts + 1];  // first item of live group i
@@ -67,9 +69,8 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(DecodeArgs a) {
     // (the shared-expert groups first -- every token, so the longest items --
     // then the routed experts with tokens).
     for (int e = tid; e < kMaxExperts; e += 256) hist[e] = 0;
-    for (int i = tid; i < N; i += 256) ids_s[i] = a.ids[i];
     __syncthreads();
-    for (int i = tid; i < N; i += 256) atomicAdd(&hist[ids_s[i]], 1);
+    for (int i = tid; i < N; i += 256) atomicAdd(&hist[a.ids[i]], 1);
     __syncthreads();
     if (wave == 0) {
         int run_off = 0, run_live = a.n_virtual;
@@ -146,7 +147,7 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(DecodeArgs a) {
             int run = 0;
             for (int base = 0; base < N; base += 64) {
                 const int i = base + lane;
-                const bool hit = i < N && ids_s[i] == g;
+                const bool hit = i < N && a.ids[i] == g;
                 const uint64_t m = __ballot(hit);
                 if (hit) ent[run + __popcll(m & below)] = i;
                 run += __popcll(m);
