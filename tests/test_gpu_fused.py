@@ -160,7 +160,7 @@ def test_fused_tied_router_rows(dev, ulps):
 
 def test_fused_status_async_and_path(dev):
     """The stream-ordered status copy reads the same (clear) flags as the
-    synchronising query, and 12..16-token bf16 calls take the decode path."""
+    synchronising query, and 16-token bf16 calls take the decode path."""
     import torch
     from uocr_hip import MoELayerInt4, synth
     L = synth.random_layer(4600)

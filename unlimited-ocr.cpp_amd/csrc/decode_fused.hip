@@ -1,6 +1,9 @@
-// Fused decode layer (12..16 tokens, bf16 input, no fused RMSNorm): router,
+// Fused decode layer (1..16 tokens, bf16 input, no fused RMSNorm): router,
 // gate/up, down and combine in ONE persistent launch (two workgroups per CU,
-// the grid fully resident and the same on every call).
+// the grid fully resident and the same on every call). The description below
+// is the dense form (12..16 tokens); with fewer tokens the gate/up items cover
+// only the candidate groups, after the candidate summary (up to 4 tokens the
+// candidates come from per-expert estimate workgroups instead of the routers).
 //
 // The stand-alone decode path (decode_path.hip) runs four kernels in order. At
 // 16 tokens the router is latency-bound (the reference's sequential fmaf chain
