@@ -56,6 +56,19 @@ typedef struct {
     int group_size;
 } uocr_hip_qmatrix;
 
+/* Unquantised host matrix [rows, cols], row-major: the reference's
+ * WeightMatrix in its BF16_EXT form (a bf16 checkpoint view) or its F32
+ * forms (F32_EXT / F32_OWNED, e.g. the AWQ-folded shared gate/up that
+ * scale_columns materialises), include/uocr/weights.h:18-46,
+ * src/runtime/weights.cpp:101-112,185-197. dtype is UOCR_HIP_DTYPE_BF16
+ * (uint16 bf16 bits) or UOCR_HIP_DTYPE_F32. */
+typedef struct {
+    const void* data;
+    int dtype;
+    int rows;
+    int cols;
+} uocr_hip_dense_matrix;
+
 /* One MoE layer (host pointers). Field names follow uocr::ModelConfig
  * (include/uocr/config.h:18-33) and uocr::LayerWeights (include/uocr/weights.h).
  * The shared MLP has width n_shared * inter (src/runtime/weights.cpp:352). */
@@ -82,6 +95,25 @@ typedef struct {
                                    weights.cpp:199-207, is f32). Such a layer routes
                                    with the f32-weight router kernel on every path
                                    and never takes the fused decode kernel. */
+    /* The shared MLP unquantised, as the reference loads it (load_linear with
+     * quantize = false, src/runtime/weights.cpp:289-292: BF16_EXT views of the
+     * checkpoint, F32 gate/up after the AWQ fold, weights.cpp:199-207) and runs
+     * it (three bf16 linear_forward calls, src/engine/gpu_decoder.cu:647-652).
+     * Non-NULL: [n_shared*inter, hidden] / [n_shared*inter, hidden] /
+     * [hidden, n_shared*inter], each bf16 or f32 on its own, and the INT4
+     * shared_gate/up/down must be NULL. */
+    const uocr_hip_dense_matrix* shared_gate_w;
+    const uocr_hip_dense_matrix* shared_up_w;
+    const uocr_hip_dense_matrix* shared_down_w;
+    /* Unquantised routed experts (the reference's default expert format,
+     * include/uocr/config.h:111; grouped by moe_grouped_gate_up_bf16 /
+     * _down_bf16, src/kernels/cuda/moe_gemm_bf16.cu:122-353). Non-NULL: arrays
+     * [n_experts] of [inter, hidden] / [inter, hidden] / [hidden, inter]
+     * matrices, the INT4 gate/up/down must be NULL, and the shared MLP must be
+     * unquantised too (or absent). */
+    const uocr_hip_dense_matrix* gate_w;
+    const uocr_hip_dense_matrix* up_w;
+    const uocr_hip_dense_matrix* down_w;
 } uocr_hip_layer_desc;
 
 typedef struct uocr_hip_moe_layer uocr_hip_moe_layer;
@@ -96,7 +128,12 @@ typedef struct uocr_hip_moe_layer uocr_hip_moe_layer;
  * zeros are all 8 takes the zero-free fast path); |15 * scale| (all-8 zeros:
  * |8 * scale|) within the f16 range. Scales are stored as f16 (round to
  * nearest: relative error <= 2^-11 per scale in f16's normal range; exact for
- * bf16-valued scales there), zeros exactly. Anything else is
+ * bf16-valued scales there), zeros exactly. Scales below f16's normal range
+ * (2^-14) are held as f16 subnormals (absolute error <= 2^-25) and scales below
+ * 2^-25 become 0 (the reference quantizer's 1e-8 floor, quant.cpp:62, is such
+ * a scale). Unquantised matrices (uocr_hip_dense_matrix) are stored as f16:
+ * exact for bf16 values in f16's normal range, relative error <= 2^-11 for f32
+ * values there; every |value| must be <= 65504 (f16's range). Anything else is
  * UOCR_HIP_EUNSUPPORTED with the reason in uocr_hip_last_error(). Allocates
  * device memory; not for the per-call path. */
 int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* desc, uocr_hip_moe_layer** out);
@@ -189,9 +226,13 @@ int uocr_hip_moe_router_topk(const float* router_logits, int seq, int n_experts,
  * and zeros [n_experts][rows][ng] (expert stride *_sstride floats, row stride
  * ng); value = (q - zero) * scale. Assignment tables [n_experts, cap] and
  * count[n_experts] as moe_router_topk writes them (entries past
- * min(count, cap) are ignored). Activations f32. Weights are dequantised to
- * bf16 and multiplied with bf16 activations, f32 accumulation (the
- * reference's tensor-core numerics). `bn` / `bm` are accepted and ignored.
+ * min(count, cap) are ignored). Activations f32. INT4 weights are
+ * dequantised in f32 ((q - zero) * scale) and rounded once to f16, bf16
+ * weights are converted to f16, and both multiply f16-rounded activations
+ * with f32 accumulation (the reference stages bf16 operands for its tensor
+ * cores, moe_gemm_int4.cu:456-473; f16 carries 3 more significand bits, and
+ * values beyond f16's range, |v| > 65504, become infinite rather than
+ * silently wrong). `bn` / `bm` are accepted and ignored.
  * This build requires hidden and inter multiples of 64 and group % 32 == 0
  * (else UOCR_HIP_EUNSUPPORTED). The down projections ADD w * y into `out`
  * with f32 atomics (the caller zeroes `out`, as in the reference); the order

@@ -17,6 +17,8 @@
  *                                      composition of _ref matmul_t_bf16 + _ref softmax,
  *                                      stable-argsort brute force for the greedy top-k
  *   orc_stable_group                   equals a stable sort of (expert, token) pairs
+ *   orc_dense_matmul / orc_mlp_dense   bit-exact vs the composition of oracle/_ref's
+ *                                      matmul_t(_bf16) + silu_mul, and a float64 bound
  *   orc_moe_layer                      float64 brute force from dequantized weights
  * The reference's weights.cpp (INT4 matvec) and moe_decoder.cpp (moe_gate) cannot be
  * linked here: weights.cpp needs nlohmann/json, which this image lacks.
@@ -409,9 +411,37 @@ void orc_mlp(const orc_qmatrix* gate, const orc_qmatrix* up, const orc_qmatrix* 
     free(a);
 }
 
+/* src/runtime/weights.cpp:51-60 (WeightMatrix::matmul, F32 and BF16_EXT branches) */
+void orc_dense_matmul(const orc_dense* w, const float* x, float* y, int m) {
+    if (w->dtype == 1)
+        orc_matmul_t_bf16(x, (const uint16_t*)w->data, NULL, y, m, w->rows, w->cols);
+    else
+        orc_matmul_t(x, (const float*)w->data, NULL, y, m, w->rows, w->cols);
+}
+
+/* src/engine/moe_decoder.cpp:45-60 (mlp_forward) and :62-74 (routed_expert)
+ * with unquantised matrices */
+void orc_mlp_dense(const orc_dense* gate, const orc_dense* up, const orc_dense* down, const float* x,
+                   float* out, int m) {
+    const int inter = gate->rows;
+    float* g = (float*)malloc(sizeof(float) * (size_t)m * inter);
+    float* u = (float*)malloc(sizeof(float) * (size_t)m * inter);
+    float* a = (float*)malloc(sizeof(float) * (size_t)m * inter);
+    orc_dense_matmul(gate, x, g, m);
+    orc_dense_matmul(up, x, u, m);
+    orc_silu_mul(g, u, a, (long long)m * inter);
+    orc_dense_matmul(down, a, out, m);
+    free(g);
+    free(u);
+    free(a);
+}
+
 /* src/engine/moe_decoder.cpp:62-74 */
 void orc_routed_expert(const orc_layer* L, const float* x, float* out, int e) {
-    orc_mlp(&L->gate[e], &L->up[e], &L->down[e], x, out, 1);
+    if (L->gate_w)
+        orc_mlp_dense(&L->gate_w[e], &L->up_w[e], &L->down_w[e], x, out, 1);
+    else
+        orc_mlp(&L->gate[e], &L->up[e], &L->down[e], x, out, 1);
 }
 
 /* One token of src/engine/moe_decoder.cpp:76-113 (+ residual, :166-179). */
@@ -426,7 +456,10 @@ static void layer_token(const orc_layer* L, const float* x, const float* h, cons
         for (int d = 0; d < H; ++d) moe[d] = fmaf(w[j], acc[d], moe[d]);
     }
     if (L->shared_inter > 0) { /* add_rows(out, shared) (moe_decoder.cpp:110-112) */
-        orc_mlp(&L->shared_gate, &L->shared_up, &L->shared_down, x, sh, 1);
+        if (L->shared_gate_w.data)
+            orc_mlp_dense(&L->shared_gate_w, &L->shared_up_w, &L->shared_down_w, x, sh, 1);
+        else
+            orc_mlp(&L->shared_gate, &L->shared_up, &L->shared_down, x, sh, 1);
         for (int d = 0; d < H; ++d) moe[d] += sh[d];
     }
     if (h)

@@ -33,6 +33,15 @@ typedef struct {
     int group_size;
 } orc_qmatrix;
 
+/* Unquantised matrix [rows, cols] row-major: WeightMatrix's F32 forms
+ * (dtype 0) and BF16_EXT (dtype 1, uint16 bf16 bits), include/uocr/weights.h:18-46. */
+typedef struct {
+    const void* data;
+    int dtype;
+    int rows;
+    int cols;
+} orc_dense;
+
 /* One MoE layer's weights, as the reference's LayerWeights holds them
  * (include/uocr/weights.h; moe_decoder.cpp:76-113). */
 typedef struct {
@@ -53,6 +62,13 @@ typedef struct {
     float rms_eps;
     const float* router_f32;         /* optional f32 router [n_experts, hidden] (an AWQ-folded
                                         router, weights.cpp:185-207); replaces router_bf16 */
+    /* unquantised shared MLP (weights.cpp:289-292, the reference's own form); used when
+       shared_gate_w.data is non-NULL, in place of the INT4 shared_* */
+    orc_dense shared_gate_w, shared_up_w, shared_down_w;
+    /* unquantised routed experts [n_experts] (config.h:111); used when non-NULL */
+    const orc_dense* gate_w;
+    const orc_dense* up_w;
+    const orc_dense* down_w;
 } orc_layer;
 
 float orc_bf16_to_f32(uint16_t h);
@@ -105,6 +121,12 @@ void orc_rswa_append(float* kcache, float* vcache, int* len, int* ring_pos, int*
 void orc_stable_group(const int* ids, int seq, int top_k, int n_experts, int* counts,
                       int* offsets, int* perm_token, int* perm_j);
 
+/* WeightMatrix::matmul, src/runtime/weights.cpp:51-60: F32 -> matmul_t,
+ * BF16_EXT -> matmul_t_bf16 (y [m, rows] = x [m, cols] . W^T). */
+void orc_dense_matmul(const orc_dense* w, const float* x, float* y, int m);
+/* mlp_forward (moe_decoder.cpp:45-60) on unquantised gate/up/down. */
+void orc_mlp_dense(const orc_dense* gate, const orc_dense* up, const orc_dense* down, const float* x,
+                   float* out, int m);
 void orc_routed_expert(const orc_layer* L, const float* x, float* out, int e);
 void orc_mlp(const orc_qmatrix* gate, const orc_qmatrix* up, const orc_qmatrix* down,
              const float* x, float* out, int m);

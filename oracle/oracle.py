@@ -27,6 +27,10 @@ class QMatC(C.Structure):
                 ("rows", C.c_int), ("cols", C.c_int), ("group_size", C.c_int)]
 
 
+class DenseC(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("dtype", C.c_int), ("rows", C.c_int), ("cols", C.c_int)]
+
+
 class LayerC(C.Structure):
     _fields_ = [("hidden", C.c_int), ("inter", C.c_int), ("shared_inter", C.c_int),
                 ("n_experts", C.c_int), ("top_k", C.c_int), ("norm_topk_prob", C.c_int),
@@ -34,7 +38,9 @@ class LayerC(C.Structure):
                 ("router_bf16", C.c_void_p), ("gate", C.POINTER(QMatC)), ("up", C.POINTER(QMatC)),
                 ("down", C.POINTER(QMatC)), ("shared_gate", QMatC), ("shared_up", QMatC),
                 ("shared_down", QMatC), ("rms_weight", C.c_void_p), ("rms_eps", C.c_float),
-                ("router_f32", C.c_void_p)]
+                ("router_f32", C.c_void_p), ("shared_gate_w", DenseC), ("shared_up_w", DenseC),
+                ("shared_down_w", DenseC), ("gate_w", C.POINTER(DenseC)), ("up_w", C.POINTER(DenseC)),
+                ("down_w", C.POINTER(DenseC))]
 
 
 def build():
@@ -72,6 +78,8 @@ def lib():
         L.orc_rswa_append.argtypes = [f32p, f32p, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int),
                                       C.c_int, C.c_int, C.c_int, f32p, f32p]
         L.orc_stable_group.argtypes = [i32p, C.c_int, C.c_int, C.c_int, i32p, i32p, i32p, C.c_void_p]
+        L.orc_dense_matmul.argtypes = [C.POINTER(DenseC), f32p, f32p, C.c_int]
+        L.orc_mlp_dense.argtypes = [C.POINTER(DenseC)] * 3 + [f32p, f32p, C.c_int]
         L.orc_moe_layer.argtypes = [C.POINTER(LayerC), f32p, C.c_int, C.c_void_p, C.c_int, C.c_int,
                                     i32p, f32p, f32p]
         _lib = L
@@ -239,18 +247,59 @@ def rmsnorm(x, w, eps):
     return out
 
 
+def _dc(d, keep):
+    """orc_dense view of a synth.Dense (f32 or bf16-bits array)."""
+    a = np.ascontiguousarray(d.data)
+    keep.append(a)
+    return DenseC(a.ctypes.data, 1 if a.dtype == np.uint16 else 0, a.shape[0], a.shape[1])
+
+
+def dense_matmul(d, x):
+    """WeightMatrix::matmul on an unquantised matrix (weights.cpp:51-60)."""
+    keep = []
+    dc = _dc(d, keep)
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty((x.shape[0], d.data.shape[0]), np.float32)
+    lib().orc_dense_matmul(C.byref(dc), x, y, x.shape[0])
+    return y
+
+
+def mlp_dense(g, u, d, x):
+    """mlp_forward (moe_decoder.cpp:45-60) on unquantised matrices."""
+    keep = []
+    gc, uc, dc = _dc(g, keep), _dc(u, keep), _dc(d, keep)
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty((x.shape[0], d.data.shape[0]), np.float32)
+    lib().orc_mlp_dense(C.byref(gc), C.byref(uc), C.byref(dc), x, y, x.shape[0])
+    return y
+
+
 def layer_c(L):
     """orc_layer view of a synth.Layer (and the arrays it points into)."""
     keep = []
     E = L.n_experts
-    gate = (QMatC * E)(*[_qc(q, keep) for q in L.gate])
-    up = (QMatC * E)(*[_qc(q, keep) for q in L.up])
-    down = (QMatC * E)(*[_qc(q, keep) for q in L.down])
-    keep += [gate, up, down]
+    dense_experts = getattr(L, "gate_w", None) is not None
+    if dense_experts:
+        gate = up = down = None
+        gw = (DenseC * E)(*[_dc(m, keep) for m in L.gate_w])
+        uw = (DenseC * E)(*[_dc(m, keep) for m in L.up_w])
+        dw = (DenseC * E)(*[_dc(m, keep) for m in L.down_w])
+        keep += [gw, uw, dw]
+    else:
+        gw = uw = dw = None
+        gate = (QMatC * E)(*[_qc(q, keep) for q in L.gate])
+        up = (QMatC * E)(*[_qc(q, keep) for q in L.up])
+        down = (QMatC * E)(*[_qc(q, keep) for q in L.down])
+        keep += [gate, up, down]
     empty = QMatC(None, None, None, 0, 0, 1)
-    sg = _qc(L.shared_gate, keep) if L.n_shared else empty
-    su = _qc(L.shared_up, keep) if L.n_shared else empty
-    sd = _qc(L.shared_down, keep) if L.n_shared else empty
+    dempty = DenseC(None, 0, 0, 0)
+    dense_shared = getattr(L, "shared_gate_w", None) is not None
+    sg = _qc(L.shared_gate, keep) if L.n_shared and not dense_shared else empty
+    su = _qc(L.shared_up, keep) if L.n_shared and not dense_shared else empty
+    sd = _qc(L.shared_down, keep) if L.n_shared and not dense_shared else empty
+    sgw = _dc(L.shared_gate_w, keep) if L.n_shared and dense_shared else dempty
+    suw = _dc(L.shared_up_w, keep) if L.n_shared and dense_shared else dempty
+    sdw = _dc(L.shared_down_w, keep) if L.n_shared and dense_shared else dempty
     router = np.ascontiguousarray(L.router_bf16, np.uint16)
     keep.append(router)
     rms = None
@@ -264,7 +313,7 @@ def layer_c(L):
     lc = LayerC(L.hidden, L.inter, L.n_shared * L.inter, E, L.top_k, L.norm_topk_prob,
                 L.routed_scaling_factor, L.scoring_sigmoid, router.ctypes.data, gate, up, down,
                 sg, su, sd, rms.ctypes.data if rms is not None else None, L.rms_eps,
-                rf.ctypes.data if rf is not None else None)
+                rf.ctypes.data if rf is not None else None, sgw, suw, sdw, gw, uw, dw)
     return lc, keep
 
 

@@ -17,6 +17,10 @@ Vectors (reference file:line of the function that produced each output):
   smx_*     src/kernels/cpu_ops.cpp:93-106  softmax (router logits, large/small/equal rows)
   silu_*    src/kernels/cpu_ops.cpp:108-113 silu_mul
   rms_*     src/kernels/cpu_ops.cpp:58-67   rmsnorm (eps 1e-6)
+  mlpd_*    src/engine/moe_decoder.cpp:45-60 mlp_forward on unquantised matrices: a bf16 gate
+            (matmul_t_bf16), an f32 up (matmul_t: the AWQ-folded form, weights.cpp:185-207),
+            silu_mul, a bf16 down -- the reference's own functions composed as
+            WeightMatrix::matmul dispatches them (weights.cpp:51-60)
 """
 import os
 import sys
@@ -115,6 +119,19 @@ def main():
     o = np.empty_like(x)
     R.ref_rmsnorm(x, wr, o, 4, 1280, 1e-6)
     v.update(rms_x=x, rms_w=wr, rms_out=o)
+
+    m, H, I = 3, 128, 96
+    x = rng.standard_normal((m, H)).astype(np.float32)
+    gb = f32_to_bf16_bits(rng.standard_normal((I, H)).astype(np.float32) * np.float32(0.05))
+    uf = rng.standard_normal((I, H)).astype(np.float32) * np.float32(0.05)
+    db = f32_to_bf16_bits(rng.standard_normal((H, I)).astype(np.float32) * np.float32(0.05))
+    gy, uy, act, out = (np.empty((m, I), np.float32), np.empty((m, I), np.float32),
+                        np.empty((m, I), np.float32), np.empty((m, H), np.float32))
+    R.ref_matmul_t_bf16(x, gb, None, gy, m, I, H)
+    R.ref_matmul_t(x, uf, None, uy, m, I, H)
+    R.ref_silu_mul(gy, uy, act, m * I)
+    R.ref_matmul_t_bf16(act, db, None, out, m, H, I)
+    v.update(mlpd_x=x, mlpd_gate=gb, mlpd_up=uf, mlpd_down=db, mlpd_out=out)
 
     path = os.path.join(HERE, "ref_vectors.npz")
     np.savez_compressed(path, **v)

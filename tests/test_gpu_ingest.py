@@ -54,6 +54,24 @@ def test_gptq_file_with_awq_fold(dev, tmp_path, group, seq):
     check_parity(L, x, dev, sample=32 if seq > 64 else None, dtype="f32", label=f"gptq-awq-g{group}-t{seq}")
 
 
+@pytest.mark.parametrize("seq", [16, 600])
+def test_gptq_file_fold_into_bf16_shared_mlp(dev, tmp_path, seq):
+    """The reference's real layer form: GPTQ INT4 routed experts from the file,
+    a bf16 shared MLP from the checkpoint; the file's expert_in_scale turns the
+    shared gate/up into F32 matrices (scale_columns, weights.cpp:185-207) and
+    the router into f32, and the layer takes them as they are."""
+    from uocr_hip import synth
+    base = synth.with_bf16_shared(awq_layer(4500, group=32, n_experts=64), 4501)
+    rng = np.random.default_rng(seq)
+    base.rms_weight = rng.uniform(0.5, 2.0, base.hidden).astype(np.float32)
+    s = rng.uniform(1 / 16, 16, base.hidden).astype(np.float32)
+    L = gptq_round_trip(tmp_path, base, 3, s)
+    assert L.shared_gate_w.data.dtype == np.float32 and L.shared_down_w.data.dtype == np.uint16
+    np.testing.assert_array_equal(L.shared_gate_w.data, base.shared_gate_w.to_f32() * s[None, :])
+    x = synth.bf16_normal(np.random.default_rng(seq + 3), (seq, L.hidden), 1.0)
+    check_parity(L, x, dev, sample=32 if seq > 64 else None, dtype="f32", label=f"gptq-awq-bf16shared-t{seq}")
+
+
 @pytest.mark.parametrize("seq", [16, 300])
 def test_f32_router_bf16_input_skips_fused_kernel(dev, seq):
     """An f32 router with bf16 input and no norm: 16 tokens would take the fused

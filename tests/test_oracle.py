@@ -112,6 +112,43 @@ def test_rmsnorm_golden(gv):
     assert same_bits(O.rmsnorm(gv["rms_x"], gv["rms_w"], 1e-6), gv["rms_out"])
 
 
+def test_mlp_dense_golden(gv):
+    """Unquantised shared MLP (bf16 gate, f32 up, bf16 down): the reference's
+    own matmul_t_bf16 / matmul_t / silu_mul composed (mlpd_* golden vectors)."""
+    g, u, d = synth.Dense(gv["mlpd_gate"]), synth.Dense(gv["mlpd_up"]), synth.Dense(gv["mlpd_down"])
+    assert same_bits(O.mlp_dense(g, u, d, gv["mlpd_x"]), gv["mlpd_out"])
+    # each matrix dispatches on its own dtype (weights.cpp:51-60)
+    assert same_bits(O.dense_matmul(g, gv["mlpd_x"]), O.matmul_t_bf16(gv["mlpd_x"], gv["mlpd_gate"]))
+    assert same_bits(O.dense_matmul(u, gv["mlpd_x"]), O.matmul_t(gv["mlpd_x"], gv["mlpd_up"]))
+    # and the whole chain against float64
+    x = gv["mlpd_x"].astype(np.float64)
+    a = x @ g.to_f32().astype(np.float64).T
+    b = x @ u.to_f32().astype(np.float64).T
+    ref = (a / (1 + np.exp(-a)) * b) @ d.to_f32().astype(np.float64).T
+    assert np.max(np.abs(O.mlp_dense(g, u, d, gv["mlpd_x"]) - ref)) < 1e-5
+
+
+def test_moe_layer_dense_float64_brute_force():
+    """bf16 routed experts + bf16 shared MLP (the reference's default layer)
+    against float64 arithmetic on the same matrices."""
+    L = synth.random_layer_bf16(34, hidden=256, inter=128, n_experts=16, top_k=4, n_shared=2)
+    x = synth.bf16_normal(np.random.default_rng(5), (4, 256), 1.0)
+    ids, w, out = O.moe_layer(L, x)
+
+    def mlp(g, u, d, v):
+        a = v @ g.to_f32().astype(np.float64).T
+        b = v @ u.to_f32().astype(np.float64).T
+        return (a / (1 + np.exp(-a)) * b) @ d.to_f32().astype(np.float64).T
+
+    xd = x.astype(np.float64)
+    ref = mlp(L.shared_gate_w, L.shared_up_w, L.shared_down_w, xd)
+    for t in range(4):
+        for j in range(4):
+            e = ids[t, j]
+            ref[t] += w[t, j] * mlp(L.gate_w[e], L.up_w[e], L.down_w[e], xd[t:t + 1])[0]
+    assert np.linalg.norm(out - ref) / np.linalg.norm(ref) < 1e-5
+
+
 def test_against_ref_library_when_built():
     R = O.ref()
     if R is None:

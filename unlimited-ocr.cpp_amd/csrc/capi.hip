@@ -157,7 +157,7 @@ int scratch_ptr(int device, void** out) {
 }
 }  // namespace
 
-constexpr int kStages = 6;  // router, group, gate_up, down, combine, fused
+constexpr int kStages = 7;  // router, group, gate_up, down, combine, fused, shared
 
 struct uocr_hip_moe_layer {
     int hidden = 0, inter = 0, n_experts = 0, top_k = 0, n_virtual = 0, group = 0;
@@ -177,6 +177,17 @@ struct uocr_hip_moe_layer {
     uint16_t* up_z = nullptr;
     uint16_t* down_z = nullptr;
     long long gu_wstride = 0, gu_sstride = 0, dn_wstride = 0, dn_sstride = 0;
+    // unquantised matrices as f16 row-major (dense.hip): the shared MLP
+    // [s_inter][hidden] / [hidden][s_inter] and the routed experts
+    // [E][inter][hidden] / [E][hidden][inter]
+    bool shared_dense = false, experts_dense = false;
+    int s_inter = 0;
+    f16* sgate = nullptr;
+    f16* sup = nullptr;
+    f16* sdown = nullptr;
+    f16* egate = nullptr;
+    f16* eup = nullptr;
+    f16* edown = nullptr;
     size_t device_bytes = 0;
     bool timing = false;
     hipEvent_t ev[2 * kStages] = {};  // start/stop per stage
@@ -192,7 +203,8 @@ namespace {
 void free_layer(uocr_hip_moe_layer* L) {
     if (!L) return;
     void* ptrs[] = {L->router_t, L->router_f32, L->rms_weight, L->gate,   L->up,   L->down, L->gate_s,
-                    L->up_s,     L->down_s,     L->gate_z,     L->up_z,   L->down_z, L->sync};
+                    L->up_s,     L->down_s,     L->gate_z,     L->up_z,   L->down_z, L->sync,
+                    L->sgate,    L->sup,        L->sdown,      L->egate,  L->eup,    L->edown};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     for (auto& e : L->ev)
@@ -212,9 +224,43 @@ int check_qm(const uocr_hip_qmatrix* q, int rows, int cols, int group, const cha
     return UOCR_HIP_OK;
 }
 
+int check_dense(const uocr_hip_dense_matrix* m, int rows, int cols, const char* what) {
+    if (!m || !m->data) return fail(UOCR_HIP_EINVAL, std::string(what) + ": null matrix pointer");
+    if (m->dtype != UOCR_HIP_DTYPE_BF16 && m->dtype != UOCR_HIP_DTYPE_F32)
+        return fail(UOCR_HIP_EINVAL, std::string(what) + ": dtype must be UOCR_HIP_DTYPE_BF16 or _F32");
+    if (m->rows != rows || m->cols != cols)
+        return fail(UOCR_HIP_EINVAL, std::string(what) + ": shape " + std::to_string(m->rows) + "x" +
+                                         std::to_string(m->cols) + ", expected " + std::to_string(rows) +
+                                         "x" + std::to_string(cols));
+    return UOCR_HIP_OK;
+}
+
+// f16 copy of an unquantised host matrix (round to nearest; exact for bf16
+// values in f16's normal range); values beyond f16's range are refused
+int dense_to_f16(const uocr_hip_dense_matrix& m, uint16_t* dst, std::string* err) {
+    const size_t n = (size_t)m.rows * m.cols;
+    for (size_t i = 0; i < n; ++i) {
+        float v;
+        if (m.dtype == UOCR_HIP_DTYPE_BF16) {
+            const uint32_t bits = (uint32_t) static_cast<const uint16_t*>(m.data)[i] << 16;
+            std::memcpy(&v, &bits, 4);
+        } else {
+            v = static_cast<const float*>(m.data)[i];
+        }
+        if (!std::isfinite(v) || std::fabs(v) > 65504.0f) {
+            *err = "value " + std::to_string(v) + " at row " + std::to_string(i / m.cols) +
+                   " outside the f16 range";
+            return UOCR_HIP_EUNSUPPORTED;
+        }
+        dst[i] = f16_bits(v);
+    }
+    return UOCR_HIP_OK;
+}
+
 struct WsPlan {
     size_t x16, ids, wts, counts, offsets, ntiles, slot_tok, slot_w, pos, tile_e, tile_m0, tile_info, act, y, total;
     size_t lrank, chunk_count, chunk_base;
+    size_t sact, sy;  // unquantised shared MLP: act [seq, s_inter] f16, y [seq, hidden] f32
     int slots, max_tiles, bm;
 };
 
@@ -243,18 +289,38 @@ bool use_prefill(const uocr_hip_moe_layer* L, int seq) {
 constexpr int kFusedMinSeq = 1;
 
 bool use_fused(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
-    return L->sync && L->router_t && seq >= kFusedMinSeq && seq <= kFusedMaxSeq && x_dtype == UOCR_HIP_DTYPE_BF16 &&
+    return L->sync && !L->experts_dense && L->router_t && seq >= kFusedMinSeq && seq <= kFusedMaxSeq && x_dtype == UOCR_HIP_DTYPE_BF16 &&
            !L->rms_weight &&
            decode_fused_ok(L->hidden, L->inter, L->group) && L->n_experts + L->n_virtual <= kMaxExperts;
 }
 
 
+// Tile rows of the unquantised expert kernels: decode-sized tiles below the
+// prefill threshold, 128-slot MFMA tiles from there (when the shapes allow)
+int dense_experts_bm(const uocr_hip_moe_layer* L, int seq) {
+    return (seq >= kPrefillMinSeq && dense_shapes_ok(L->hidden, L->inter, true, kDenseTiledBM) &&
+            dense_shapes_ok(L->inter, L->hidden, false, kDenseTiledBM))
+               ? kDenseTiledBM
+               : kDenseSkinnyBM;
+}
+// ... and of the unquantised shared MLP (every token: a plain GEMM)
+int dense_shared_bm(const uocr_hip_moe_layer* L, int seq) {
+    return (seq >= 128 && dense_shapes_ok(L->hidden, L->s_inter, true, kDenseTiledBM) &&
+            dense_shapes_ok(L->s_inter, L->hidden, false, kDenseTiledBM))
+               ? kDenseTiledBM
+               : kDenseSkinnyBM;
+}
+// the layer runs the grouping kernels (prefill path, or unquantised experts)
+bool uses_grouping(const uocr_hip_moe_layer* L, int seq) { return L->experts_dense || use_prefill(L, seq); }
+
 WsPlan plan(const uocr_hip_moe_layer* L, int seq) {
     WsPlan p{};
     const int Ev = L->n_experts + L->n_virtual;
     p.slots = seq * (L->top_k + L->n_virtual);
-    p.bm = !use_prefill(L, seq) ? kDecodeTileRows
-                                : (prefill_big_ok(L->hidden, L->inter) ? kPrefillBigTileRows : kPrefillTileRows);
+    p.bm = L->experts_dense ? dense_experts_bm(L, seq)
+           : !use_prefill(L, seq)
+               ? kDecodeTileRows
+               : (prefill_big_ok(L->hidden, L->inter) ? kPrefillBigTileRows : kPrefillTileRows);
     p.max_tiles = (seq * L->top_k) / p.bm + L->n_experts + L->n_virtual * ((seq + p.bm - 1) / p.bm) + 1;
     size_t o = 0;
     auto take = [&](size_t bytes) {
@@ -276,7 +342,8 @@ WsPlan plan(const uocr_hip_moe_layer* L, int seq) {
     p.tile_info = take((size_t)p.max_tiles * 16);
     // act / y: one row per slot (y: per entry), or per (group, token) when the
     // fused decode kernel may run (seq <= kFusedMaxSeq, any input dtype)
-    const bool fused_rows = seq <= kFusedMaxSeq && L->sync && decode_fused_ok(L->hidden, L->inter, L->group);
+    const bool fused_rows =
+        seq <= kFusedMaxSeq && L->sync && !L->experts_dense && decode_fused_ok(L->hidden, L->inter, L->group);
     const size_t rows = fused_rows ? (size_t)std::max(p.slots, Ev * seq) : (size_t)p.slots;
     p.act = take(rows * L->inter * 2);
     p.y = take(rows * L->hidden * 4);
@@ -284,6 +351,10 @@ WsPlan plan(const uocr_hip_moe_layer* L, int seq) {
     p.lrank = take((size_t)seq * L->top_k * 4);
     p.chunk_count = take((size_t)chunks * L->n_experts * 4);
     p.chunk_base = take((size_t)chunks * L->n_experts * 4);
+    if (L->shared_dense) {
+        p.sact = take((size_t)seq * L->s_inter * 2);
+        p.sy = take((size_t)seq * L->hidden * 4);
+    }
     p.total = o;
     return p;
 }
@@ -308,29 +379,62 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
     if (d->top_k <= 0 || d->top_k > kMaxTopK || d->top_k > E)
         return fail(UOCR_HIP_EINVAL, "top_k must be in [1, min(8, n_experts)]");
     if (d->n_shared < 0 || E + d->n_shared > kMaxExperts) return fail(UOCR_HIP_EINVAL, "bad n_shared");
-    if ((!d->router_bf16 && !d->router_f32) || !d->gate || !d->up || !d->down)
+    if (!d->router_bf16 && !d->router_f32) return fail(UOCR_HIP_EINVAL, "null router pointer");
+    const bool edense = d->gate_w || d->up_w || d->down_w;
+    const int S = d->n_shared;
+    const bool sdense = S > 0 && (d->shared_gate_w || d->shared_up_w || d->shared_down_w);
+    if (edense) {
+        if (d->gate || d->up || d->down)
+            return fail(UOCR_HIP_EINVAL, "routed experts given both as INT4 and unquantised matrices");
+        if (!d->gate_w || !d->up_w || !d->down_w) return fail(UOCR_HIP_EINVAL, "null expert weight pointer");
+        if (S > 0 && !sdense)
+            return fail(UOCR_HIP_EUNSUPPORTED, "unquantised routed experts need an unquantised shared MLP");
+    } else if (!d->gate || !d->up || !d->down) {
         return fail(UOCR_HIP_EINVAL, "null weight pointer");
-    const int G = d->gate[0].group_size;
+    }
+    if (sdense && (d->shared_gate || d->shared_up || d->shared_down))
+        return fail(UOCR_HIP_EINVAL, "shared MLP given both as INT4 and unquantised matrices");
+    // group size of the INT4 matrices (unused when none is INT4)
+    const int G = !edense ? d->gate[0].group_size : (S > 0 && !sdense ? d->shared_gate->group_size : 32);
     if (G != 32 && G != 64 && G != 128) return fail(UOCR_HIP_EUNSUPPORTED, "group_size must be 32, 64 or 128");
     int rc;
     for (int e = 0; e < E; ++e) {
-        if ((rc = check_qm(&d->gate[e], I, H, G, "gate"))) return rc;
-        if ((rc = check_qm(&d->up[e], I, H, G, "up"))) return rc;
-        if ((rc = check_qm(&d->down[e], H, I, G, "down"))) return rc;
+        if (edense) {
+            if ((rc = check_dense(&d->gate_w[e], I, H, "gate"))) return rc;
+            if ((rc = check_dense(&d->up_w[e], I, H, "up"))) return rc;
+            if ((rc = check_dense(&d->down_w[e], H, I, "down"))) return rc;
+        } else {
+            if ((rc = check_qm(&d->gate[e], I, H, G, "gate"))) return rc;
+            if ((rc = check_qm(&d->up[e], I, H, G, "up"))) return rc;
+            if ((rc = check_qm(&d->down[e], H, I, G, "down"))) return rc;
+        }
     }
-    const int S = d->n_shared;
     if (S > 0) {
-        if ((rc = check_qm(d->shared_gate, S * I, H, G, "shared_gate"))) return rc;
-        if ((rc = check_qm(d->shared_up, S * I, H, G, "shared_up"))) return rc;
-        if ((rc = check_qm(d->shared_down, H, S * I, G, "shared_down"))) return rc;
+        if (sdense) {
+            if ((rc = check_dense(d->shared_gate_w, S * I, H, "shared_gate"))) return rc;
+            if ((rc = check_dense(d->shared_up_w, S * I, H, "shared_up"))) return rc;
+            if ((rc = check_dense(d->shared_down_w, H, S * I, "shared_down"))) return rc;
+        } else {
+            if ((rc = check_qm(d->shared_gate, S * I, H, G, "shared_gate"))) return rc;
+            if ((rc = check_qm(d->shared_up, S * I, H, G, "shared_up"))) return rc;
+            if ((rc = check_qm(d->shared_down, H, S * I, G, "shared_down"))) return rc;
+        }
     }
+    // the unquantised kernels' decode tiles (every layer shape that passed the
+    // checks above satisfies them; the prefill tiles fall back to these)
+    if ((edense && !(dense_shapes_ok(H, I, true, kDenseSkinnyBM) && dense_shapes_ok(I, H, false, kDenseSkinnyBM))) ||
+        (sdense && !(dense_shapes_ok(H, S * I, true, kDenseSkinnyBM) && dense_shapes_ok(S * I, H, false, kDenseSkinnyBM))))
+        return fail(UOCR_HIP_EUNSUPPORTED, "unquantised matrix shapes not supported by this build");
 
     auto* L = new uocr_hip_moe_layer();
     L->hidden = H;
     L->inter = I;
     L->n_experts = E;
     L->top_k = d->top_k;
-    L->n_virtual = S;
+    L->n_virtual = sdense ? 0 : S;  // an INT4 shared MLP runs as virtual expert groups
+    L->shared_dense = sdense;
+    L->experts_dense = edense;
+    L->s_inter = S * I;
     L->group = G;
     L->norm_topk_prob = d->norm_topk_prob;
     L->scoring_sigmoid = d->scoring_sigmoid;
@@ -338,7 +442,7 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
     L->rms_eps = d->rms_eps;
     (void)hipGetDevice(&L->device);
 
-    const int Ev = E + S;
+    const int Ev = edense ? 0 : E + L->n_virtual;  // INT4 groups to repack
     L->gu_wstride = (long long)I * H / 2;
     L->gu_sstride = (long long)I * scale_row_stride(H, G);
     L->dn_wstride = (long long)H * I / 2;
@@ -356,12 +460,12 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
             sym = sym && s1;
             return UOCR_HIP_OK;
         };
-        for (int e = 0; e < E; ++e)
+        for (int e = 0; e < (edense ? 0 : E); ++e)
             if ((rc = scan(d->gate[e], "gate")) || (rc = scan(d->up[e], "up")) || (rc = scan(d->down[e], "down"))) {
                 delete L;
                 return rc;
             }
-        if (S > 0 && ((rc = scan(*d->shared_gate, "shared_gate")) || (rc = scan(*d->shared_up, "shared_up")) ||
+        if (L->n_virtual > 0 && ((rc = scan(*d->shared_gate, "shared_gate")) || (rc = scan(*d->shared_up, "shared_up")) ||
                       (rc = scan(*d->shared_down, "shared_down")))) {
             delete L;
             return rc;
@@ -408,6 +512,40 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
             return fail(codes[e], m);
         }
 
+    // unquantised matrices -> f16 row-major
+    std::vector<uint16_t> dsg, dsu, dsd, deg, deu, ded;
+    {
+        std::string err;
+        auto conv = [&](const uocr_hip_dense_matrix& m, std::vector<uint16_t>& v, size_t off, const std::string& what) {
+            const int c = dense_to_f16(m, v.data() + off, &err);
+            if (c) fail(c, what + ": " + err);
+            return c;
+        };
+        if (sdense) {
+            dsg.resize((size_t)S * I * H);
+            dsu.resize(dsg.size());
+            dsd.resize(dsg.size());
+            if ((rc = conv(*d->shared_gate_w, dsg, 0, "shared_gate")) || (rc = conv(*d->shared_up_w, dsu, 0, "shared_up")) ||
+                (rc = conv(*d->shared_down_w, dsd, 0, "shared_down"))) {
+                free_layer(L);
+                return rc;
+            }
+        }
+        if (edense) {
+            const size_t n = (size_t)I * H;
+            deg.resize((size_t)E * n);
+            deu.resize(deg.size());
+            ded.resize(deg.size());
+            for (int e = 0; e < E; ++e)
+                if ((rc = conv(d->gate_w[e], deg, e * n, "expert " + std::to_string(e) + " gate")) ||
+                    (rc = conv(d->up_w[e], deu, e * n, "expert " + std::to_string(e) + " up")) ||
+                    (rc = conv(d->down_w[e], ded, e * n, "expert " + std::to_string(e) + " down"))) {
+                    free_layer(L);
+                    return rc;
+                }
+        }
+    }
+
     // router W (bf16) as [H/8][E][8] so lane e's 16-byte loads are coalesced
     // across the wave; an f32 router has no bf16 form (its layer takes the
     // f32-weight router on every path)
@@ -444,17 +582,24 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
         L->device_bytes += bytes;
         return UOCR_HIP_OK;
     };
+    const bool int4 = Ev > 0;
     if ((!rt.empty() && (rc = up_copy((void**)&L->router_t, rt.data(), rt.size() * 2, "router"))) ||
         (rc = up_copy((void**)&L->router_f32, rf.data(), rf.size() * 4, "router f32")) ||
-        (rc = up_copy((void**)&L->gate, hg.data(), hg.size(), "gate")) ||
-        (rc = up_copy((void**)&L->up, hu.data(), hu.size(), "up")) ||
-        (rc = up_copy((void**)&L->down, hd.data(), hd.size(), "down")) ||
-        (rc = up_copy((void**)&L->gate_s, hgs.data(), hgs.size() * 2, "gate scales")) ||
-        (rc = up_copy((void**)&L->up_s, hus.data(), hus.size() * 2, "up scales")) ||
-        (rc = up_copy((void**)&L->down_s, hds.data(), hds.size() * 2, "down scales")) ||
-        (!sym && (rc = up_copy((void**)&L->gate_z, hgz.data(), hgz.size() * 2, "gate zeros"))) ||
-        (!sym && (rc = up_copy((void**)&L->up_z, huz.data(), huz.size() * 2, "up zeros"))) ||
-        (!sym && (rc = up_copy((void**)&L->down_z, hdz.data(), hdz.size() * 2, "down zeros"))) ||
+        (int4 && (rc = up_copy((void**)&L->gate, hg.data(), hg.size(), "gate"))) ||
+        (int4 && (rc = up_copy((void**)&L->up, hu.data(), hu.size(), "up"))) ||
+        (int4 && (rc = up_copy((void**)&L->down, hd.data(), hd.size(), "down"))) ||
+        (int4 && (rc = up_copy((void**)&L->gate_s, hgs.data(), hgs.size() * 2, "gate scales"))) ||
+        (int4 && (rc = up_copy((void**)&L->up_s, hus.data(), hus.size() * 2, "up scales"))) ||
+        (int4 && (rc = up_copy((void**)&L->down_s, hds.data(), hds.size() * 2, "down scales"))) ||
+        (sdense && (rc = up_copy((void**)&L->sgate, dsg.data(), dsg.size() * 2, "shared gate"))) ||
+        (sdense && (rc = up_copy((void**)&L->sup, dsu.data(), dsu.size() * 2, "shared up"))) ||
+        (sdense && (rc = up_copy((void**)&L->sdown, dsd.data(), dsd.size() * 2, "shared down"))) ||
+        (edense && (rc = up_copy((void**)&L->egate, deg.data(), deg.size() * 2, "expert gate"))) ||
+        (edense && (rc = up_copy((void**)&L->eup, deu.data(), deu.size() * 2, "expert up"))) ||
+        (edense && (rc = up_copy((void**)&L->edown, ded.data(), ded.size() * 2, "expert down"))) ||
+        (int4 && !sym && (rc = up_copy((void**)&L->gate_z, hgz.data(), hgz.size() * 2, "gate zeros"))) ||
+        (int4 && !sym && (rc = up_copy((void**)&L->up_z, huz.data(), huz.size() * 2, "up zeros"))) ||
+        (int4 && !sym && (rc = up_copy((void**)&L->down_z, hdz.data(), hdz.size() * 2, "down zeros"))) ||
         (d->rms_weight && (rc = up_copy((void**)&L->rms_weight, d->rms_weight, (size_t)H * 4, "rms weight")))) {
         free_layer(L);
         return rc;
@@ -466,7 +611,7 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
             return rc;
         }
     }
-    {
+    if (!edense) {
         hipError_t e = hipMalloc((void**)&L->sync, sizeof(FusedSync));
         if (e == hipSuccess) e = hipMemset(L->sync, 0, sizeof(FusedSync));
         if (e != hipSuccess) {
@@ -490,7 +635,7 @@ size_t uocr_hip_moe_layer_device_bytes(const uocr_hip_moe_layer* layer) {
 
 size_t uocr_hip_moe_layer_workspace_size(const uocr_hip_moe_layer* layer, int seq) {
     if (!layer || seq <= 0) return 0;
-    if (use_prefill(layer, seq) && !group_fits(seq, layer->top_k, layer->n_experts)) return 0;
+    if (uses_grouping(layer, seq) && !group_fits(seq, layer->top_k, layer->n_experts)) return 0;
     return plan(layer, seq).total;
 }
 
@@ -528,7 +673,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     if (L->rms_weight && x_dtype != UOCR_HIP_DTYPE_F32)
         return fail(UOCR_HIP_EINVAL, "a layer with rms_weight adds the residual and needs f32 x");
     if ((uintptr_t)x % 16 || (uintptr_t)out % 16) return fail(UOCR_HIP_EINVAL, "x and out must be 16-byte aligned");
-    if (use_prefill(L, seq) && !group_fits(seq, L->top_k, L->n_experts))
+    if (uses_grouping(L, seq) && !group_fits(seq, L->top_k, L->n_experts))
         return fail(UOCR_HIP_EUNSUPPORTED, "seq * top_k too large for the grouping scan (" + std::to_string(seq) +
                                                " tokens)");
     const WsPlan p = plan(L, seq);
@@ -557,8 +702,39 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     struct Disarm {  // an early error return must not leave later launches armed
         ~Disarm() { stage_events() = StageEvents{}; }
     } disarm_on_exit;
+    // the unquantised shared MLP (dense.hip): act then y_shared [seq, hidden]
+    // f32, added by the combine after the routed sum (moe_decoder.cpp:110-112)
+    const float* shared_y = nullptr;
+    auto run_shared = [&](const void* src, int kind) -> int {
+        if (!L->shared_dense) return UOCR_HIP_OK;
+        const int bm = dense_shared_bm(L, seq);
+        stage(6);
+        DenseArgs sa{};
+        sa.a = src;
+        sa.a_kind = kind;
+        sa.w0 = L->sgate;
+        sa.w1 = L->sup;
+        sa.n_out = L->s_inter;
+        sa.k = L->hidden;
+        sa.seq = seq;
+        sa.out16 = (f16*)(ws + p.sact);
+        // the 128-slot tiles take f16 input only
+        HIP_TRY(launch_dense(sa, true, kind == 0 ? bm : kDenseSkinnyBM, 0, st), "shared gate/up launch");
+        DenseArgs sd{};
+        sd.a = sa.out16;
+        sd.a_kind = 0;
+        sd.w0 = L->sdown;
+        sd.n_out = L->hidden;
+        sd.k = L->s_inter;
+        sd.seq = seq;
+        sd.out32 = (float*)(ws + p.sy);
+        HIP_TRY(launch_dense(sd, false, bm, 0, st), "shared down launch");
+        shared_y = sd.out32;
+        return UOCR_HIP_OK;
+    };
+    int rc;
     stage(0);
-    if (!use_prefill(L, seq)) {
+    if (!uses_grouping(L, seq)) {
         DecodeArgs da{};
         da.x = x;
         da.x_bf16 = x_dtype == UOCR_HIP_DTYPE_BF16;
@@ -598,6 +774,8 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
         da.out = out;
         if (use_fused(L, seq, x_dtype)) {
             da.sync = L->sync;
+            if ((rc = run_shared(x, 1))) return rc;
+            da.shared_y = shared_y;
             stage(5);
             HIP_TRY(launch_decode_fused(da, st), "fused decode launch");
             stage(-1);
@@ -624,6 +802,8 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
             ra.weights = wts;
             HIP_TRY(launch_router(ra, x_dtype == UOCR_HIP_DTYPE_BF16, st), "router launch");
         }
+        if ((rc = run_shared(x16, 0))) return rc;
+        da.shared_y = shared_y;
         stage(2);
         HIP_TRY(launch_experts_decode2(da, true, st), "gate/up launch");
         stage(3);
@@ -670,10 +850,10 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     g.lrank = (int*)(ws + p.lrank);
     g.chunk_count = (int*)(ws + p.chunk_count);
     g.chunk_base = (int*)(ws + p.chunk_base);
-    if (L->router_t) {
+    if (L->router_t && seq > kRouterDecodeMaxSeq) {
         HIP_TRY(launch_router(ra, x_dtype == UOCR_HIP_DTYPE_BF16, st), "router launch");
     } else {
-        // f32 router: the per-token f32-weight router (same outputs)
+        // f32 router, or few tokens: the per-token router (same outputs)
         DecodeArgs da{};
         da.x = x;
         da.x_bf16 = x_dtype == UOCR_HIP_DTYPE_BF16;
@@ -699,7 +879,33 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     stage(1);
     HIP_TRY(launch_group(g, st), "group launch");
     stage(2);
-
+    const f16* y16 = (const f16*)(ws + p.y);
+    if (L->experts_dense) {
+        DenseArgs gu{};
+        gu.a = x16;
+        gu.a_kind = 0;
+        gu.slot_tok = g.slot_tok;
+        gu.w0 = L->egate;
+        gu.w1 = L->eup;
+        gu.w_stride = (long long)L->inter * L->hidden;
+        gu.n_out = L->inter;
+        gu.k = L->hidden;
+        gu.tile_info = g.tile_info;
+        gu.n_tiles = g.n_tiles;
+        gu.seq = seq;
+        gu.out16 = (f16*)(ws + p.act);
+        HIP_TRY(launch_dense(gu, true, p.bm, p.max_tiles, st), "gate/up launch");
+        stage(3);
+        DenseArgs dn = gu;
+        dn.a = gu.out16;
+        dn.slot_tok = nullptr;
+        dn.w0 = L->edown;
+        dn.w1 = nullptr;
+        dn.n_out = L->hidden;
+        dn.k = L->inter;
+        dn.out16 = (f16*)(ws + p.y);
+        HIP_TRY(launch_dense(dn, false, p.bm, p.max_tiles, st), "down launch");
+    } else {
     ExpertArgs gu{};
     gu.a = x16;
     gu.gather = 1;
@@ -744,10 +950,13 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     dn.y_out = (f16*)(ws + p.y);
     HIP_TRY(launch_experts_prefill(dn, false, p.max_tiles, st),
             "down launch");
+    }
+    if ((rc = run_shared(x16, 0))) return rc;
     stage(4);
 
     CombineArgs c{};
-    c.y = dn.y_out;
+    c.y = y16;
+    c.shared_y = shared_y;
     c.pos = g.pos;
     c.weights = wts;
     c.offsets = g.offsets;

@@ -45,6 +45,15 @@ __global__ __launch_bounds__(1024) void combine_kernel(CombineArgs c) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[i] += sh[i];
     }
+    if (c.shared_y) {
+        const f32x4 s0 = *reinterpret_cast<const f32x4*>(c.shared_y + (size_t)t * H + col);
+        const f32x4 s1 = *reinterpret_cast<const f32x4*>(c.shared_y + (size_t)t * H + col + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc[i] += s0[i];
+            acc[4 + i] += s1[i];
+        }
+    }
     if (c.residual) {
         const f32x4 r0 = *reinterpret_cast<const f32x4*>(c.residual + (size_t)t * H + col);
         const f32x4 r1 = *reinterpret_cast<const f32x4*>(c.residual + (size_t)t * H + col + 4);

@@ -763,6 +763,11 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
 #pragma unroll
                 for (int q = 0; q < 4; ++q) acc[q] += sh[q];
             }
+            if (a.shared_y) {  // written by an earlier launch: a plain load
+                const f32x4 sv = *reinterpret_cast<const f32x4*>(a.shared_y + (size_t)t * H + c);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc[q] += sv[q];
+            }
             if (bad) acc = f32x4{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")};
             *reinterpret_cast<f32x4*>(a.out + (size_t)t * H + c) = acc;
         }

@@ -297,6 +297,11 @@ __global__ __launch_bounds__(1024) void combine_decode_kernel(DecodeArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[i] += sh[i];
         }
+        if (a.shared_y) {
+            const f32x4 sv = *reinterpret_cast<const f32x4*>(a.shared_y + (size_t)t * H + c);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] += sv[i];
+        }
         if (res) {
             const f32x4 rv = *reinterpret_cast<const f32x4*>(res + c);
 #pragma unroll

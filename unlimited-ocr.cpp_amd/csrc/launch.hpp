@@ -104,6 +104,7 @@ struct CombineArgs {
     const float* weights;  // [seq, top_k]
     const int* offsets;    // virtual groups start at offsets[n_experts + v]
     const float* residual; // optional [seq, hidden]
+    const float* shared_y; // optional [seq, hidden] f32: the unquantised shared MLP's output
     float* out;            // [seq, hidden]
     int seq, hidden, top_k, n_experts, n_virtual;
 };
@@ -158,6 +159,7 @@ struct DecodeArgs {
     const uint16_t* down_z;
     long long gu_wstride, gu_sstride, dn_wstride, dn_sstride;
     FusedSync* sync;           // fused kernel only
+    const float* shared_y;     // optional [seq, hidden] f32: the unquantised shared MLP's output
     f16* act;                  // [slots, inter]; fused: [(E + n_virtual) * seq, inter]
     float* y;                  // [slots, hidden]
     float* out;                // [seq, hidden]
@@ -188,6 +190,28 @@ bool group_fits(int seq, int top_k, int n_experts);  // the grouping scan's LDS 
 hipError_t router_overflow_read(int clear, int* flag);  // sticky count > cap flag of the router mirror
 hipError_t launch_experts_prefill(const ExpertArgs& a, bool gate_up, int max_tiles, hipStream_t st);
 hipError_t launch_combine(const CombineArgs& c, hipStream_t st);
+
+// Unquantised (bf16 / f32 checkpoint) matrices held as f16 row-major
+// [experts][rows][cols] on the device (dense.hip).
+constexpr int kDenseSkinnyBM = 16;   // decode-sized tiles
+constexpr int kDenseTiledBM = 128;   // prefill-sized tiles
+struct DenseArgs {
+    const void* a;          // A rows: f16 (x16 / act) or bf16 (the layer input x)
+    int a_kind;             // 0 f16, 1 bf16
+    const int* slot_tok;    // non-null: A row of slot s is slot_tok[s]; null: row s
+    const f16* w0;          // gate (gate/up pass) or down, [experts][n_w][k]
+    const f16* w1;          // up (gate/up pass), else null
+    long long w_stride;     // elements between experts
+    int n_out;              // gate/up: act columns (= gate rows); down: output columns
+    int k;                  // input features
+    const int* tile_info;   // grouped tiles [max][4] (e, m0, rows, slot0); null: slot tiles over seq
+    const int* n_tiles;
+    int seq;
+    f16* out16;             // gate/up: act [slot][n_out]; down: y [slot][n_out] f16 (if out32 is null)
+    float* out32;           // down: y [slot][n_out] f32
+};
+bool dense_shapes_ok(int k, int n_out, bool gate_up, int bm);
+hipError_t launch_dense(const DenseArgs& a, bool gate_up, int bm, int max_tiles, hipStream_t st);
 
 // reference-layout operator mirrors (mirrors.hip)
 int set_error(int code, const std::string& msg);  // capi.hip: thread's last error text

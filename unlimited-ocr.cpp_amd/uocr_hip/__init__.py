@@ -6,5 +6,5 @@ tests, the benchmark and Python callers. Importing it never falls back to a
 CPU path: `load()` raises if the library has not been built.
 """
 from ._lib import HipError, load, lib_path  # noqa: F401
-from .layer import MoELayerInt4, QMatrix  # noqa: F401
+from .layer import MoELayer, MoELayerInt4, QMatrix  # noqa: F401
 from . import ops, synth  # noqa: F401

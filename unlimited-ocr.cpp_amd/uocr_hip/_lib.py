@@ -32,6 +32,12 @@ class QMatrixC(C.Structure):
                 ("rows", C.c_int), ("cols", C.c_int), ("group_size", C.c_int)]
 
 
+class DenseMatrixC(C.Structure):
+    """uocr_hip_dense_matrix (WeightMatrix BF16_EXT / F32, include/uocr/weights.h:18-46)."""
+
+    _fields_ = [("data", C.c_void_p), ("dtype", C.c_int), ("rows", C.c_int), ("cols", C.c_int)]
+
+
 class LayerDescC(C.Structure):
     _fields_ = [("hidden", C.c_int), ("inter", C.c_int), ("n_experts", C.c_int),
                 ("top_k", C.c_int), ("n_shared", C.c_int), ("norm_topk_prob", C.c_int),
@@ -40,7 +46,10 @@ class LayerDescC(C.Structure):
                 ("up", C.POINTER(QMatrixC)), ("down", C.POINTER(QMatrixC)),
                 ("shared_gate", C.POINTER(QMatrixC)), ("shared_up", C.POINTER(QMatrixC)),
                 ("shared_down", C.POINTER(QMatrixC)), ("rms_weight", C.c_void_p),
-                ("rms_eps", C.c_float), ("router_f32", C.c_void_p)]
+                ("rms_eps", C.c_float), ("router_f32", C.c_void_p),
+                ("shared_gate_w", C.POINTER(DenseMatrixC)), ("shared_up_w", C.POINTER(DenseMatrixC)),
+                ("shared_down_w", C.POINTER(DenseMatrixC)), ("gate_w", C.POINTER(DenseMatrixC)),
+                ("up_w", C.POINTER(DenseMatrixC)), ("down_w", C.POINTER(DenseMatrixC))]
 
 
 def lib_path():

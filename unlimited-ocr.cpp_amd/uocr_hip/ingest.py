@@ -114,10 +114,13 @@ def load_moe_layer(qfile, layer_index, base, fallback_group):
     present. Raises if a routed expert is missing from the file (this build
     does not quantize dense expert weights at load).
 
-    The fold also scales the shared gate/up columns (weights.cpp:205-206).
-    This layer takes INT4 shared experts, which cannot absorb a column scale
-    exactly, so `base.shared_gate` / `shared_up` must already be the folded
-    ones: quantized from scale_columns_f32(dense shared weight, s)."""
+    The fold also scales the shared gate/up columns (weights.cpp:205-206). An
+    unquantised shared MLP (`base.shared_gate_w` etc., the reference's form)
+    takes it as the reference does: gate/up become F32 matrices with column c
+    times s[c] (scale_columns, weights.cpp:185-197), down stays as it is. An
+    INT4 shared MLP cannot absorb a column scale exactly, so for such a base
+    `shared_gate` / `shared_up` must already be the folded ones: quantized from
+    scale_columns_f32(dense shared weight, s)."""
     p = f"model.layers.{layer_index}."
     H, I, E = base.hidden, base.inter, base.n_experts
     gate, up, down = [], [], []
@@ -136,6 +139,7 @@ def load_moe_layer(qfile, layer_index, base, fallback_group):
                     base.router_bf16, gate, up, down, base.shared_gate, base.shared_up, base.shared_down,
                     base.rms_weight, base.rms_eps, base.norm_topk_prob, base.routed_scaling_factor,
                     base.scoring_sigmoid)
+    L.shared_gate_w, L.shared_up_w, L.shared_down_w = base.shared_gate_w, base.shared_up_w, base.shared_down_w
     skey = p + "expert_in_scale"
     if qfile.contains(skey):
         s = qfile.read_f32(skey)
@@ -144,4 +148,7 @@ def load_moe_layer(qfile, layer_index, base, fallback_group):
         if base.rms_weight is None:
             raise ValueError("an expert input scale folds into the post-attention norm: rms_weight is required")
         L.rms_weight, L.router_f32 = fold_expert_input_scale(s, base.rms_weight, base.router_bf16)
+        if L.shared_gate_w is not None:
+            L.shared_gate_w = synth.Dense(scale_columns_f32(L.shared_gate_w.to_f32(), s))
+            L.shared_up_w = synth.Dense(scale_columns_f32(L.shared_up_w.to_f32(), s))
     return L

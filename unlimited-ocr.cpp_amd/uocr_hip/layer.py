@@ -4,9 +4,9 @@ import ctypes as C
 import numpy as np
 
 from . import _lib
-from ._lib import DTYPE_BF16, DTYPE_F32, LayerDescC, QMatrixC, check, load
+from ._lib import DTYPE_BF16, DTYPE_F32, DenseMatrixC, LayerDescC, QMatrixC, check, load
 
-STAGES = ("router", "group", "gate_up", "down", "combine", "fused")
+STAGES = ("router", "group", "gate_up", "down", "combine", "fused", "shared")
 
 
 class QMatrix:
@@ -26,20 +26,46 @@ def _qarray(qms):
     return arr, keep
 
 
+def _darray(ds):
+    """uocr_hip_dense_matrix array over synth.Dense-like objects (`data`:
+    uint16 bf16 bits or float32, [rows, cols])."""
+    keep = [np.ascontiguousarray(d.data) for d in ds]
+    for a in keep:
+        if a.dtype not in (np.uint16, np.float32):
+            raise TypeError("dense matrices must be bf16 bits (uint16) or float32")
+    arr = (DenseMatrixC * len(keep))(*[DenseMatrixC(a.ctypes.data, DTYPE_BF16 if a.dtype == np.uint16 else DTYPE_F32,
+                                                    a.shape[0], a.shape[1]) for a in keep])
+    return arr, keep
+
+
 class MoELayerInt4:
-    """Uploads a `synth.Layer`-like object (reference host layout) once, then runs
-    `forward` on torch device tensors through uocr_hip_moe_layer_forward."""
+    """Uploads a `synth.Layer`-like object (reference host layout: INT4
+    QuantizedMatrix experts, or unquantised bf16/f32 experts and shared MLP)
+    once, then runs `forward` on torch device tensors through
+    uocr_hip_moe_layer_forward."""
 
     def __init__(self, L):
         lib = load()
         self.lib = lib
         keep = []
-        gate, k1 = _qarray(L.gate)
-        up, k2 = _qarray(L.up)
-        down, k3 = _qarray(L.down)
-        keep += [gate, up, down, k1, k2, k3]
-        sg = su = sd = None
-        if L.n_shared:
+        gate = up = down = gw = uw = dw = None
+        if getattr(L, "gate_w", None) is not None:  # unquantised routed experts
+            gw, k1 = _darray(L.gate_w)
+            uw, k2 = _darray(L.up_w)
+            dw, k3 = _darray(L.down_w)
+            keep += [gw, uw, dw, k1, k2, k3]
+        else:
+            gate, k1 = _qarray(L.gate)
+            up, k2 = _qarray(L.up)
+            down, k3 = _qarray(L.down)
+            keep += [gate, up, down, k1, k2, k3]
+        sg = su = sd = sgw = suw = sdw = None
+        if L.n_shared and getattr(L, "shared_gate_w", None) is not None:  # unquantised shared MLP
+            sgw, k4 = _darray([L.shared_gate_w])
+            suw, k5 = _darray([L.shared_up_w])
+            sdw, k6 = _darray([L.shared_down_w])
+            keep += [sgw, suw, sdw, k4, k5, k6]
+        elif L.n_shared:
             sg, k4 = _qarray([L.shared_gate])
             su, k5 = _qarray([L.shared_up])
             sd, k6 = _qarray([L.shared_down])
@@ -57,7 +83,7 @@ class MoELayerInt4:
         d = LayerDescC(L.hidden, L.inter, L.n_experts, L.top_k, L.n_shared, L.norm_topk_prob,
                        L.routed_scaling_factor, L.scoring_sigmoid, router.ctypes.data,
                        gate, up, down, sg, su, sd, rms.ctypes.data if rms is not None else None,
-                       L.rms_eps, rf.ctypes.data if rf is not None else None)
+                       L.rms_eps, rf.ctypes.data if rf is not None else None, sgw, suw, sdw, gw, uw, dw)
         h = C.c_void_p()
         check(lib.uocr_hip_moe_layer_create(C.byref(d), C.byref(h)))
         self.handle = h
@@ -141,3 +167,7 @@ class MoELayerInt4:
         n = C.c_int()
         check(self.lib.uocr_hip_moe_layer_read_timing(self.handle, ms, len(STAGES), C.byref(n)))
         return dict(zip(STAGES, list(ms))), n.value
+
+
+# the layer takes every expert format the reference loads (INT4, BF16, F32)
+MoELayer = MoELayerInt4

@@ -57,6 +57,24 @@ class QMat:
 
 
 @dataclass
+class Dense:
+    """Unquantised matrix as the reference holds it (WeightMatrix BF16_EXT /
+    F32): `data` is uint16 bf16 bits or float32, shape [rows, cols]."""
+    data: np.ndarray
+
+    @property
+    def rows(self):
+        return self.data.shape[0]
+
+    @property
+    def cols(self):
+        return self.data.shape[1]
+
+    def to_f32(self):
+        return bf16_bits_to_f32(self.data) if self.data.dtype == np.uint16 else np.asarray(self.data, np.float32)
+
+
+@dataclass
 class Layer:
     hidden: int
     inter: int
@@ -77,6 +95,14 @@ class Layer:
     routed_scaling_factor: float = 1.0
     scoring_sigmoid: int = 0
     router_f32: Optional[np.ndarray] = None  # f32 [E, H]; replaces router_bf16 (AWQ-folded router)
+    # unquantised shared MLP (the reference's form, weights.cpp:289-292); replaces shared_*
+    shared_gate_w: Optional[Dense] = None
+    shared_up_w: Optional[Dense] = None
+    shared_down_w: Optional[Dense] = None
+    # unquantised routed experts (config.h:111); replace gate/up/down
+    gate_w: Optional[list] = None
+    up_w: Optional[list] = None
+    down_w: Optional[list] = None
     _keep: list = field(default_factory=list, repr=False)
 
 
@@ -106,6 +132,45 @@ def random_layer(seed, hidden=HIDDEN, inter=INTER, n_experts=N_EXPERTS, top_k=TO
         L.shared_gate = random_qmat(rng, si, hidden, group)
         L.shared_up = random_qmat(rng, si, hidden, group)
         L.shared_down = random_qmat(rng, hidden, si, group)
+    if rms:
+        L.rms_weight = rng.uniform(0.5, 2.0, size=hidden).astype(np.float32)
+    return L
+
+
+def random_dense_bf16(rng, rows, cols, std=0.02):
+    """bf16 N(0, std) matrix (a BF16_EXT checkpoint tensor)."""
+    return Dense(f32_to_bf16_bits(rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(std)))
+
+
+def with_bf16_shared(L, seed, std=0.02):
+    """L with its shared MLP replaced by bf16 matrices of the same shapes, as the
+    reference loads it (load_linear(..., quantize=false), weights.cpp:289-292)."""
+    rng = np.random.default_rng(seed)
+    si = L.n_shared * L.inter
+    L.shared_gate_w = random_dense_bf16(rng, si, L.hidden, std)
+    L.shared_up_w = random_dense_bf16(rng, si, L.hidden, std)
+    L.shared_down_w = random_dense_bf16(rng, L.hidden, si, std)
+    L.shared_gate = L.shared_up = L.shared_down = None
+    return L
+
+
+def random_layer_bf16(seed, hidden=HIDDEN, inter=INTER, n_experts=N_EXPERTS, top_k=TOP_K,
+                      n_shared=N_SHARED, router_bias=None, rms=False, std=0.02):
+    """A layer in the reference's default format (config.h:111): bf16 routed
+    experts and a bf16 shared MLP, bf16 router N(0, 0.02)."""
+    rng = np.random.default_rng(seed)
+    router = rng.standard_normal((n_experts, hidden), dtype=np.float32) * np.float32(0.02)
+    if router_bias is not None:
+        router[:, 0] = np.asarray(router_bias, np.float32)
+    L = Layer(hidden, inter, n_experts, top_k, n_shared, 32, f32_to_bf16_bits(router), [], [], [])
+    L.gate_w = [random_dense_bf16(rng, inter, hidden, std) for _ in range(n_experts)]
+    L.up_w = [random_dense_bf16(rng, inter, hidden, std) for _ in range(n_experts)]
+    L.down_w = [random_dense_bf16(rng, hidden, inter, std) for _ in range(n_experts)]
+    if n_shared:
+        si = n_shared * inter
+        L.shared_gate_w = random_dense_bf16(rng, si, hidden, std)
+        L.shared_up_w = random_dense_bf16(rng, si, hidden, std)
+        L.shared_down_w = random_dense_bf16(rng, hidden, si, std)
     if rms:
         L.rms_weight = rng.uniform(0.5, 2.0, size=hidden).astype(np.float32)
     return L
