@@ -33,18 +33,30 @@ MFMA_PEAK_TFLOPS = 2500.0  # dense bf16/f16
 
 
 def layer_bytes(L, counts, seq):
-    """Algorithmic HBM bytes of one layer call: every touched expert's packed
-    nibbles + bf16 scales once (zero point implicit), shared expert, router,
-    bf16 input and f32 output."""
+    """Algorithmic HBM bytes of one layer call: every touched expert's weights
+    once (INT4: packed nibbles + bf16-sized scales, zero point implicit; bf16:
+    2 bytes per weight), the shared expert (INT4 or bf16), router, bf16 input
+    and f32 output."""
     H, I, G = L.hidden, L.inter, L.group
-    gu_e = 2 * (I * H // 2 + I * (H // G) * 2)
-    dn_e = H * I // 2 + H * (I // G) * 2
+    if getattr(L, "gate_w", None) is not None:
+        gu_e, dn_e = 2 * I * H * 2, H * I * 2
+    else:
+        gu_e = 2 * (I * H // 2 + I * (H // G) * 2)
+        dn_e = H * I // 2 + H * (I // G) * 2
     U = int((counts > 0).sum())
     S = L.n_shared
-    shared_gu, shared_dn = S * gu_e, S * dn_e
+    if getattr(L, "shared_gate_w", None) is not None:
+        shared_gu, shared_dn = S * 2 * I * H * 2, S * H * I * 2
+    else:
+        shared_gu, shared_dn = S * gu_e, S * dn_e
     io = seq * H * 2 + seq * H * 4 + L.n_experts * H * 2
-    return {"U": U, "gate_up": U * gu_e + shared_gu + seq * H * 2,
-            "down": U * dn_e + shared_dn, "total": U * (gu_e + dn_e) + shared_gu + shared_dn + io}
+    dense_shared = getattr(L, "shared_gate_w", None) is not None
+    # an unquantised shared MLP runs in its own stage (dense.hip), an INT4 one
+    # inside the routed passes
+    return {"U": U, "gate_up": U * gu_e + (0 if dense_shared else shared_gu) + seq * H * 2,
+            "down": U * dn_e + (0 if dense_shared else shared_dn),
+            "shared": shared_gu + shared_dn if dense_shared else 0,
+            "total": U * (gu_e + dn_e) + shared_gu + shared_dn + io}
 
 
 def layer_flops(L, seq):
@@ -53,7 +65,25 @@ def layer_flops(L, seq):
     return seq * per_tok, seq * (L.top_k + L.n_shared) * 2 * 2 * I * H
 
 
-def run_config(cfg, steps, warmup, replicas, group=32, graph=False):
+FORMATS = {
+    "int4": "INT4 routed experts and INT4 shared MLP (BASELINE's synthetic layer)",
+    "bf16_shared": "INT4 routed experts, bf16 shared MLP (the reference's real INT4 layer: "
+                   "weights.cpp:289-292 keeps the shared MLP unquantised)",
+    "bf16": "bf16 routed experts and bf16 shared MLP (the reference's default expert format, config.h:111)",
+}
+
+
+def make_layer(cfg, seed, group, fmt, bias=None, rms=False):
+    from uocr_hip import synth
+    if fmt == "bf16":
+        return synth.random_layer_bf16(seed, router_bias=bias, rms=rms)
+    L = synth.random_layer(seed, group=group, router_bias=bias, rms=rms)
+    if fmt == "bf16_shared":
+        synth.with_bf16_shared(L, seed + 1)
+    return L
+
+
+def run_config(cfg, steps, warmup, replicas, group=32, graph=False, fmt="int4"):
     import numpy as np
     import torch
     from uocr_hip import MoELayerInt4, synth
@@ -61,14 +91,18 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False):
     dev = torch.device("cuda:0")
     if cfg == 4:
         wl = synth.make_config(4, group=group)
+        if fmt != "int4":
+            wl.layers = [make_layer(4, 1234 + 100 + i, group, fmt, rms=True) for i in range(len(wl.layers))]
         layers_np = wl.layers
         stack = True
     else:
         base = synth.make_config(cfg, group=group)
+        bias = synth.zipf_bias() if cfg == 3 else None
+        if fmt != "int4":
+            base.layers = [make_layer(cfg, 1234 + 10 + cfg, group, fmt, bias=bias)]
         layers_np = [base.layers[0]]
         for r in range(1, replicas):
-            bias = synth.zipf_bias() if cfg == 3 else None
-            layers_np.append(synth.random_layer(9000 + 100 * cfg + r, group=group, router_bias=bias))
+            layers_np.append(make_layer(cfg, 9000 + 100 * cfg + r, group, fmt, bias=bias))
         wl = base
         stack = False
     seq = wl.seq
@@ -150,8 +184,14 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False):
 
     torch.cuda.synchronize()
     counts = [np.bincount(t.cpu().numpy().ravel(), minlength=64) for t in ids]
-    res = {"config": cfg, "workload": wl.name, "seq": seq, "group": group, "ms_per_step": ms,
-           "graph": bool(graph)}
+    # one more call of replica 0 (the seeded layer the CPU leg checks): its
+    # routing and outputs (stack: the 12-layer output and layer 0's routing)
+    step(0)
+    torch.cuda.synchronize()
+    gpu_check = {"ids": ids[0].cpu().numpy(),
+                 "out": outs[(len(layers) - 1) % 2 if stack else 0].cpu().numpy()}
+    res = {"config": cfg, "workload": wl.name, "seq": seq, "group": group, "format": fmt,
+           "format_note": FORMATS[fmt], "ms_per_step": ms, "graph": bool(graph)}
     if ms_eager is not None and graph:
         res["ms_per_step_eager"] = ms_eager
     if stack:
@@ -171,17 +211,25 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False):
             # layer's (touched experts only, although from 12 tokens the dense
             # gate/up pass reads every expert by design)
             fu = stage["fused"] * 1e-3
+            fb = avg["total"] - avg["shared"]  # the fused launch's own bytes
             res["dominant"] = {"kernel": "decode_fused_kernel<4, 10, 7> (router + experts + combine)",
-                               "ms": stage["fused"], "bytes": avg["total"],
-                               "gbs": avg["total"] / fu / 1e9,
-                               "traffic_file": "decode_fused_config1_traffic.md" if cfg == 1 else None}
+                               "ms": stage["fused"], "bytes": fb,
+                               "gbs": fb / fu / 1e9,
+                               "traffic_file": "decode_fused_config1_traffic.md" if cfg == 1 and fmt == "int4" else None}
         elif stage:
             gu = stage["gate_up"] * 1e-3
             res["gate_up_gbs"] = avg["gate_up"] / gu / 1e9
             res["gate_up_tflops"] = fl_gu / gu / 1e12
             res["gate_up_hbm_frac"] = res["gate_up_gbs"] / HBM_PEAK_GBS
             res["gate_up_mfma_frac"] = res["gate_up_tflops"] / MFMA_PEAK_TFLOPS
-            if seq >= 256:  # prefill path: the large-tile MFMA kernel, MFMA-bound
+            if getattr(layers_np[0], "gate_w", None) is not None:  # bf16 experts (dense.hip)
+                big = seq >= 256
+                res["dominant"] = {"kernel": "dense_tiled_kernel<true> (gate+up)" if big else
+                                   "dense_skinny_kernel<4, 10, true, 0> (gate+up)", "ms": stage["gate_up"],
+                                   "bytes": avg["gate_up"], "gbs": res["gate_up_gbs"], "flops": fl_gu,
+                                   "tflops": res["gate_up_tflops"], "mfma_frac": res["gate_up_mfma_frac"],
+                                   "hbm_frac": res["gate_up_hbm_frac"]}
+            elif seq >= 256:  # prefill path: the large-tile MFMA kernel, MFMA-bound
                 res["dominant"] = {"kernel": f"experts_prefill_big_kernel<{128 // group}, true, 10> (gate+up)",
                                    "ms": stage["gate_up"], "flops": fl_gu, "tflops": res["gate_up_tflops"],
                                    "mfma_frac": res["gate_up_mfma_frac"],
@@ -202,6 +250,7 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False):
               "picked outside its candidates; its outputs were NaN)", file=sys.stderr)
     for lay in layers:
         lay.close()
+    res["_check"] = (wl, gpu_check)
     return res
 
 
@@ -215,41 +264,77 @@ def _cpu_model():
     return None
 
 
-def cpu_baseline(seconds=10.0, par_seconds=4.0):
-    """Oracle (port of the reference CPU path) on config 1's 16 tokens, repeated
-    for ~`seconds`, with the reference's threading: one thread runs the tokens
-    and each token's routed experts in order (src/engine/moe_decoder.cpp:76-113,
-    src/runtime/weights.cpp:51-72 serial INT4 matvecs; the INT4 shared expert is
-    serial too, and the router GEMM's OpenMP split moves well under 1% of the
-    work). A second, shorter run with one token per thread over the box's CPU
-    share is reported beside it as a deviation from the reference's threading."""
+def subsample(ids, seq, n, seed=7):
+    """Seeded token subsample that always includes tokens routed to the most
+    and the least loaded experts (the BASELINE CPU-baseline plan)."""
+    import numpy as np
+    if seq <= n:
+        return np.arange(seq, dtype=np.int32)
+    counts = np.bincount(ids.ravel(), minlength=ids.max() + 1)
+    live = np.nonzero(counts)[0]
+    most, least = live[np.argmax(counts[live])], live[np.argmin(counts[live])]
+    must = {int(np.nonzero((ids == most).any(1))[0][0]), int(np.nonzero((ids == least).any(1))[0][0])}
+    rng = np.random.default_rng(seed)
+    rest = [t for t in rng.permutation(seq) if t not in must][: n - len(must)]
+    return np.array(sorted(must | set(int(t) for t in rest)), dtype=np.int32)
+
+
+def cpu_leg(res, min_seconds=2.0, stack_tokens=8):
+    """The CPU reference path (the oracle: the restated reference CPU code) on
+    the GPU box's host, for the config `res` measured. Threading is the
+    reference's: the routed experts run token by token on one thread
+    (moe_decoder.cpp:76-113; the INT4 matvec has no OpenMP, weights.cpp:51-72;
+    a bf16 expert's matvec has m = 1, so its row-parallel loop runs one
+    iteration), the router and a bf16 shared MLP run as batch GEMMs with the
+    reference's OpenMP rule (cpu_ops.cpp:11-39, OpenMP over rows above 2^18
+    MACs), the INT4 shared MLP serially. Routing is computed and compared on
+    all T tokens; outputs on a seeded subsample of S = min(T, 64) tokens that
+    includes tokens of the most and least loaded experts (config 4: S =
+    `stack_tokens` tokens through all 12 layers, since a token's path through
+    the stack depends only on its own rows). The call is repeated until
+    `min_seconds` have passed."""
+    import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
-    from uocr_hip import synth
 
-    wl = synth.make_config(1)
+    wl, gpu = res.pop("_check")
+    T = wl.seq
+    x = wl.x.astype(np.float32)
+    L0 = wl.layers[0]
+    ids_all, w_all, _ = O.moe_layer(L0, x, sel=np.zeros(0, np.int32))
+    routing_exact = bool(np.array_equal(ids_all, gpu["ids"]))
+    stack = len(wl.layers) > 1
+    S = min(T, stack_tokens if stack else 64)
+    sel = subsample(ids_all, T, S)
+
+    def once():
+        if stack:
+            h = x[sel]
+            for L in wl.layers:
+                _, _, h = O.moe_layer(L, h)
+            return h
+        return O.moe_layer(L0, x, sel=sel)[2][sel]
+
+    n, t0 = 0, time.perf_counter()
+    while True:
+        got = once()
+        n += 1
+        if time.perf_counter() - t0 >= min_seconds:
+            break
+    dt = (time.perf_counter() - t0) / n
+    want = gpu["out"][sel].astype(np.float64)
+    err = got.astype(np.float64) - want
+    dense = getattr(L0, "shared_gate_w", None) is not None or getattr(L0, "gate_w", None) is not None
     nproc = os.cpu_count() or 1
-
-    def timed(threads, budget):
-        n = 0
-        t0 = time.perf_counter()
-        while True:
-            O.moe_layer(wl.layers[0], wl.x, threads=threads)
-            n += 1
-            if time.perf_counter() - t0 > budget:
-                break
-        dt = time.perf_counter() - t0
-        return n, dt
-
-    n, dt = timed(1, seconds)
-    threads = min(16, nproc)
-    pn, pdt = timed(threads, par_seconds)
-    return {"value": n * wl.seq / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
-            "nproc": nproc, "cpu_model": _cpu_model(), "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
-            "threading": "reference: tokens and routed experts in order on one thread",
-            "sample": f"config 1 layer (16 tokens, all routed+shared experts) x{n} runs, {dt:.1f}s",
-            "token_parallel": {"value": pn * wl.seq / pdt, "cores": threads,
-                               "sample": f"x{pn} runs, {pdt:.1f}s, one token per thread (not the reference's threading)"},
+    return {"value": S / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "threads_note": ("routed experts on one thread; the router" + (" and the bf16 shared MLP" if dense else "") +
+                             f" OpenMP row-parallel (OMP_NUM_THREADS={os.environ.get('OMP_NUM_THREADS')})"),
+            "nproc": nproc, "cpu_model": _cpu_model(),
+            "sample": (f"{S} of {T} tokens through {len(wl.layers)} layers" if stack else f"{S} of {T} tokens") +
+                      f", x{n} calls, {dt * n:.1f} s",
+            "routing_bit_exact_all_tokens": routing_exact,
+            "gpu_vs_cpu": {"rel_l2": float(np.linalg.norm(err) / np.linalg.norm(got)),
+                           "max_abs": float(np.abs(err).max())},
             "note": "reported baseline, not the target"}
 
 
@@ -334,6 +419,8 @@ def main():
     ap.add_argument("--graph", default="",
                     help="decode configs (0, 1) replayed from a hipGraph, as a decode engine runs its step; "
                          "their eager rate is reported beside it (config 4 always runs as a graph)")
+    ap.add_argument("--formats", default="1:bf16_shared,1:bf16,3:bf16",
+                    help="extra (config:format) lines; formats: " + ", ".join(FORMATS))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run a plain copy of BYTES bytes (counter calibration)")
@@ -348,7 +435,15 @@ def main():
 
     graph_cfgs = {v.strip() for v in args.graph.split(",") if v.strip()}
     main_res = run_config(1, args.steps, args.warmup, args.replicas, graph="1" in graph_cfgs)
+    cpu = None if args.no_cpu else cpu_leg(main_res, min_seconds=10.0)
+    main_res.pop("_check", None)
     extras = {}
+
+    def extra(key, r):
+        r["cpu_baseline"] = None if args.no_cpu else cpu_leg(r)
+        r.pop("_check", None)
+        extras[key] = r
+
     for c in [v.strip() for v in args.extra.split(",") if v.strip()]:
         if c == "rswa":
             extras["rswa"] = run_rswa(max(args.steps // 2, 20), 5)
@@ -356,13 +451,22 @@ def main():
         c = int(c)
         if c == 4:
             for g in (32, 128):
-                r = run_config(4, max(args.steps // 10, 5), 3, 1, group=g, graph=True)
-                extras[f"4_g{g}"] = r
+                extra(f"4_g{g}", run_config(4, max(args.steps // 10, 5), 3, 1, group=g, graph=True))
         else:
-            extras[str(c)] = run_config(c, max(args.steps // (5 if c >= 2 else 1), 20),
-                                        max(args.warmup // 4, 3), 3 if c >= 2 else args.replicas,
-                                        graph=str(c) in graph_cfgs)
-    cpu = None if args.no_cpu else cpu_baseline()
+            extra(str(c), run_config(c, max(args.steps // (5 if c >= 2 else 1), 20),
+                                     max(args.warmup // 4, 3), 3 if c >= 2 else args.replicas,
+                                     graph=str(c) in graph_cfgs))
+    for item in [v.strip() for v in args.formats.split(",") if v.strip()]:
+        c, fmt = item.split(":")
+        c = int(c)
+        if c == 4:
+            r = run_config(4, max(args.steps // 10, 5), 3, 1, graph=True, fmt=fmt)
+        else:
+            # bf16 experts: a layer is ~450 MB, so 2 replicas already exceed the memory-side cache
+            reps = 2 if fmt == "bf16" else (3 if c >= 2 else args.replicas)
+            r = run_config(c, max(args.steps // (5 if c >= 2 else 1), 20), max(args.warmup // 4, 3), reps,
+                           graph=str(c) in graph_cfgs, fmt=fmt)
+        extra(f"{c}_{fmt}", r)
     dom = main_res["dominant"]
     line = {
         "metric": "INT4 MoE layer tokens/s (batch-16 decode, config 1)",

@@ -212,7 +212,10 @@ int uocr_hip_moe_layer_status_async(const uocr_hip_moe_layer* layer, int* d_flag
  * gpu_decoder.cu:602-609): probabilities are bit-identical to the CPU
  * softmax (the CUDA kernel uses __expf and divides); slots are filled in
  * ascending (token, j) order instead of atomicAdd order; d_count receives
- * min(count, cap) and need not be zeroed by the caller. */
+ * min(count, cap) and need not be zeroed by the caller. Above 1024 routed
+ * entries (seq * top_k) the grouping runs on a library-owned per-device
+ * scratch (up to 131072 entries; single-workgroup rounds beyond): such calls
+ * on different streams of one device must not overlap. */
 int uocr_hip_moe_router_topk(const float* router_logits, int seq, int n_experts, int top_k,
                              int norm_topk_prob, float routed_scaling_factor,
                              int scoring_sigmoid, int* d_ids, float* d_weights,
@@ -307,6 +310,38 @@ int uocr_hip_moe_gemm_int4_tc_nk(const float* x, const uint8_t* packed, const fl
 int uocr_hip_moe_gemm_int4_tc_pipe(const float* x, const uint8_t* packed, const float* scales,
                                    const float* zeros, int m, int n, int k, int group_size, float* y, int bn,
                                    void* stream);
+
+/* ---- dense and elementwise operator mirrors: the calls GpuDecoder::mlp_block's
+ * host-grouping branch and shared expert make around the expert GEMMs
+ * (src/engine/gpu_decoder.cu:590-657). f32 activations, device pointers. */
+
+/* Mirror of uocr::cuda::matmul_t_bf16 (include/uocr/cuda_ops.h:31-32,
+ * src/kernels/cuda/backend.cu:607-627): y[m, n] = x[m, k] . W[n, k]^T + bias[n]
+ * (bias may be NULL), W bf16 row-major. x and W are rounded to f16 (exact for
+ * bf16 W in f16's normal range) and multiplied on MFMA with f32 accumulation
+ * (the reference rounds x to bf16 for its tensor cores). Requires n % 64 == 0
+ * and k % 32 == 0 (else UOCR_HIP_EUNSUPPORTED) and 16-byte aligned x and W. */
+int uocr_hip_matmul_t_bf16(const float* x, const uint16_t* w, const float* bias, float* y, int m, int n, int k,
+                           void* stream);
+/* Mirror of uocr::cuda::matvec_bf16 (cuda_ops.h:41-42, backend.cu:560-577):
+ * y[n] = W[n, k] . x[k] + bias; matmul_t_bf16 with m = 1. */
+int uocr_hip_matvec_bf16(const float* x, const uint16_t* w, const float* bias, float* y, int n, int k,
+                         void* stream);
+/* Mirror of uocr::cuda::silu_mul (cuda_ops.h:242-243, gpu_ops.cu:12-19):
+ * out[i] = gate[i] / (1 + exp(-gate[i])) * up[i]. */
+int uocr_hip_silu_mul(const float* gate, const float* up, float* out, int n, void* stream);
+/* Mirror of uocr::cuda::add_scaled (cuda_ops.h:245-246, gpu_ops.cu:21-26):
+ * dst[i] += scale * src[i] (one fused multiply-add per element). */
+int uocr_hip_add_scaled(float* dst, const float* src, float scale, int n, void* stream);
+/* Mirror of uocr::cuda::scatter_add_scaled (cuda_ops.h:248-250,
+ * gpu_ops.cu:28-37): out[row_idx[r], c] += weights[r] * vals[r, c]. Rows
+ * naming the same output row are added atomically (in the reference that
+ * case races); distinct rows give the reference's result exactly. */
+int uocr_hip_scatter_add_scaled(float* out, const float* vals, const int* row_idx, const float* weights, int rows,
+                                int cols, void* stream);
+/* Mirror of uocr::cuda::gather_rows (cuda_ops.h:252-253, gpu_ops.cu:39-45):
+ * dst[r, :] = src[row_idx[r], :]. */
+int uocr_hip_gather_rows(float* dst, const float* src, const int* row_idx, int rows, int cols, void* stream);
 
 /* Overflow report of uocr_hip_moe_router_topk (the reference drops entries
  * past `cap` silently, moe_device.cu:90-95): *flag = 1 if any call since the

@@ -444,31 +444,17 @@ void orc_routed_expert(const orc_layer* L, const float* x, float* out, int e) {
         orc_mlp(&L->gate[e], &L->up[e], &L->down[e], x, out, 1);
 }
 
-/* One token of src/engine/moe_decoder.cpp:76-113 (+ residual, :166-179). */
-static void layer_token(const orc_layer* L, const float* x, const float* h, const int* ids,
-                        const float* w, float* out_row) {
+/* The routed sum of one token, src/engine/moe_decoder.cpp:86-97:
+ * moe[d] += w[j] * routed(x, ids[j])[d], j ascending. */
+static void routed_token(const orc_layer* L, const float* x, const int* ids, const float* w, float* moe) {
     const int H = L->hidden;
     float* acc = (float*)malloc(sizeof(float) * H);
-    float* moe = (float*)calloc((size_t)H, sizeof(float));
-    float* sh = (float*)malloc(sizeof(float) * H);
+    for (int d = 0; d < H; ++d) moe[d] = 0.0f;
     for (int j = 0; j < L->top_k; ++j) {
         orc_routed_expert(L, x, acc, ids[j]);
         for (int d = 0; d < H; ++d) moe[d] = fmaf(w[j], acc[d], moe[d]);
     }
-    if (L->shared_inter > 0) { /* add_rows(out, shared) (moe_decoder.cpp:110-112) */
-        if (L->shared_gate_w.data)
-            orc_mlp_dense(&L->shared_gate_w, &L->shared_up_w, &L->shared_down_w, x, sh, 1);
-        else
-            orc_mlp(&L->shared_gate, &L->shared_up, &L->shared_down, x, sh, 1);
-        for (int d = 0; d < H; ++d) moe[d] += sh[d];
-    }
-    if (h)
-        for (int d = 0; d < H; ++d) out_row[d] = h[d] + moe[d];
-    else
-        memcpy(out_row, moe, sizeof(float) * H);
     free(acc);
-    free(moe);
-    free(sh);
 }
 
 void orc_moe_layer(const orc_layer* L, const float* h, int seq, const int* sel, int n_sel,
@@ -488,13 +474,46 @@ void orc_moe_layer(const orc_layer* L, const float* h, int seq, const int* sel, 
         orc_moe_gate(x, L->router_bf16, seq, H, L->n_experts, L->top_k, L->norm_topk_prob,
                      L->routed_scaling_factor, L->scoring_sigmoid, ids, weights);
     const int n = sel ? n_sel : seq;
+    if (n <= 0) {
+        free(xn);
+        return;
+    }
+    float* moe = (float*)malloc(sizeof(float) * (size_t)n * H);
+    /* routed experts, token by token (the reference's loop runs on one thread;
+       threads > 1 splits the tokens, each token's arithmetic unchanged) */
     (void)threads;
-#pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1)
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1) if (threads > 1)
     for (int i = 0; i < n; ++i) {
         const int t = sel ? sel[i] : i;
-        layer_token(L, x + (size_t)t * H, L->rms_weight ? h + (size_t)t * H : NULL,
-                    ids + (size_t)t * L->top_k, weights + (size_t)t * L->top_k,
-                    out + (size_t)t * H);
+        routed_token(L, x + (size_t)t * H, ids + (size_t)t * L->top_k, weights + (size_t)t * L->top_k,
+                     moe + (size_t)i * H);
     }
+    /* shared experts: one mlp_forward over the batch rows, then add_rows
+       (moe_decoder.cpp:109-112); its matmuls follow the reference's OpenMP rule */
+    if (L->shared_inter > 0) {
+        float* xs = (float*)malloc(sizeof(float) * (size_t)n * H);
+        float* sh = (float*)malloc(sizeof(float) * (size_t)n * H);
+        for (int i = 0; i < n; ++i)
+            memcpy(xs + (size_t)i * H, x + (size_t)(sel ? sel[i] : i) * H, sizeof(float) * H);
+        if (L->shared_gate_w.data)
+            orc_mlp_dense(&L->shared_gate_w, &L->shared_up_w, &L->shared_down_w, xs, sh, n);
+        else
+            orc_mlp(&L->shared_gate, &L->shared_up, &L->shared_down, xs, sh, n);
+        for (size_t i = 0; i < (size_t)n * H; ++i) moe[i] += sh[i];
+        free(xs);
+        free(sh);
+    }
+    for (int i = 0; i < n; ++i) {
+        const int t = sel ? sel[i] : i;
+        float* o = out + (size_t)t * H;
+        const float* m = moe + (size_t)i * H;
+        if (L->rms_weight) {
+            const float* hr = h + (size_t)t * H;
+            for (int d = 0; d < H; ++d) o[d] = hr[d] + m[d];
+        } else {
+            memcpy(o, m, sizeof(float) * H);
+        }
+    }
+    free(moe);
     free(xn);
 }

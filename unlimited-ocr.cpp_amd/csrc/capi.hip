@@ -1055,7 +1055,7 @@ int uocr_hip_moe_router_topk(const float* logits, int seq, int n_experts, int to
     g.assign_w = d_assign_w;
     g.assign_count = d_count;
     g.cap = cap;
-    HIP_TRY(launch_group(g, st), "group launch");
+    HIP_TRY(launch_group_mirror(g, st), "group launch");
     return UOCR_HIP_OK;
 }
 

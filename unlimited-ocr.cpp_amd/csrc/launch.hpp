@@ -184,6 +184,9 @@ inline bool prefill_big_ok(int hidden, int inter) {
 }
 hipError_t launch_router_from_logits(const RouterArgs& a, const float* logits, hipStream_t st);
 hipError_t launch_group(const GroupArgs& g, hipStream_t st);
+// launch_group for the moe_router_topk mirror: the multi-workgroup grouping on
+// a library-owned per-device scratch when the entries fit it
+hipError_t launch_group_mirror(GroupArgs g, hipStream_t st);
 int group_chunks(int seq, int top_k);  // 1024-entry chunks of the multi-workgroup grouping
 constexpr size_t kGroupScanLds = 96 * 1024;  // per-(chunk, expert) counts of the grouping scan
 bool group_fits(int seq, int top_k, int n_experts);  // the grouping scan's LDS holds seq * top_k entries
@@ -225,6 +228,13 @@ hipError_t mirror_down_int4(const float* act, const uint8_t* p, const float* s, 
                             int n_experts, int cap, int hidden, int inter, int group, float* out, hipStream_t st);
 hipError_t mirror_gemm_int4(const float* x, const uint8_t* p, const float* s, const float* z, int m, int n, int k,
                             int group, float* y, hipStream_t st);
+hipError_t mirror_gemm_bf16(const float* x, const uint16_t* w, const float* bias, int m, int n, int k, float* y,
+                            hipStream_t st);
+hipError_t mirror_silu_mul(const float* g, const float* u, float* out, long long n, hipStream_t st);
+hipError_t mirror_add_scaled(float* dst, const float* src, float scale, long long n, hipStream_t st);
+hipError_t mirror_scatter_add_scaled(float* out, const float* vals, const int* row_idx, const float* w, int rows,
+                                     int cols, hipStream_t st);
+hipError_t mirror_gather_rows(float* dst, const float* src, const int* row_idx, int rows, int cols, hipStream_t st);
 hipError_t mirror_gate_up_bf16(const float* x, const uint16_t* const* gw, const uint16_t* const* uw,
                                const int* assign_token, const int* count, int n_experts, int cap, int hidden,
                                int inter, float* act, hipStream_t st);

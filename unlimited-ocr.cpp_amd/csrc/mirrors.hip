@@ -21,6 +21,8 @@
 // moe_device.cu:261-266; the order of the adds is not fixed); plain GEMM -> y.
 #include "launch.hpp"
 
+#include <algorithm>
+
 namespace uocr_hip {
 
 namespace {
@@ -47,6 +49,8 @@ struct MirrorArgs {
     // bf16 tables
     const uint16_t* const* w0;
     const uint16_t* const* w1;
+    const uint16_t* wplain;   // plain bf16 GEMM: W [N, K]
+    const float* bias;        // plain GEMM: optional bias [N]
     const int* assign_token;  // [E, cap]
     const float* assign_w;    // [E, cap]
     const int* count;         // [E]
@@ -71,7 +75,9 @@ __global__ __launch_bounds__(256) void mirror_kernel(MirrorArgs a) {
     const int K = a.K, N = a.N;
     const int packed_row = (K + 1) / 2;
 
-    for (int m0 = 0; m0 < rows; m0 += kMBM) {
+    // m-tiles blockIdx.z, + gridDim.z, ...: a skewed expert's rows spread over
+    // gridDim.z workgroups per column block
+    for (int m0 = blockIdx.z * kMBM; m0 < rows; m0 += gridDim.z * kMBM) {
         f32x4 acc[NM][4];
 #pragma unroll
         for (int j = 0; j < NM; ++j)
@@ -156,7 +162,8 @@ __global__ __launch_bounds__(256) void mirror_kernel(MirrorArgs a) {
                     const int u = tid + 256 * it, mat = u >> 10, n = (u >> 4) & 63, c8 = u & 15;
                     u32x4 w = {0u, 0u, 0u, 0u};
                     if (c8 * 8 < kc) {
-                        const uint16_t* row = (mat ? a.w1 : a.w0)[e] + (size_t)(n0 + n) * K + k0 + c8 * 8;
+                        const uint16_t* wm = MODE == kPlain ? a.wplain : (mat ? a.w1 : a.w0)[e];
+                        const uint16_t* row = wm + (size_t)(n0 + n) * K + k0 + c8 * 8;
                         w = *reinterpret_cast<const u32x4*>(row);
                     }
                     f16x8 v;
@@ -203,7 +210,7 @@ __global__ __launch_bounds__(256) void mirror_kernel(MirrorArgs a) {
                     const size_t ai = (size_t)e * a.cap + slot;
                     atomicAdd(a.out + (size_t)a.assign_token[ai] * N + col, a.assign_w[ai] * acc[0][i][r]);
                 } else {
-                    a.out[(size_t)slot * N + col] = acc[0][i][r];
+                    a.out[(size_t)slot * N + col] = acc[0][i][r] + (a.bias ? a.bias[col] : 0.0f);
                 }
             }
     }
@@ -211,7 +218,11 @@ __global__ __launch_bounds__(256) void mirror_kernel(MirrorArgs a) {
 
 template <int MODE, int WFMT>
 hipError_t launch_mirror(const MirrorArgs& a, int n_experts, hipStream_t st) {
-    const dim3 grid(a.N / kMBN, MODE == kPlain ? 1 : n_experts);
+    // m-tile workgroups per (column block, expert): every m-tile of a plain
+    // GEMM; up to 32 per expert of the grouped calls (cap bounds the rows)
+    const int mt = ((MODE == kPlain ? a.m_plain : a.cap) + kMBM - 1) / kMBM;
+    const int mz = MODE == kPlain ? std::min(mt, 65535) : std::min(mt, 32);
+    const dim3 grid(a.N / kMBN, MODE == kPlain ? 1 : n_experts, std::max(mz, 1));
     launch_k((mirror_kernel<MODE, WFMT>), grid, dim3(256), 0, st, a);
     return hipGetLastError();
 }
@@ -257,6 +268,76 @@ hipError_t mirror_gemm_int4(const float* x, const uint8_t* p, const float* s, co
     a.p0 = p, a.s0 = s, a.z0 = z, a.pstride0 = 0, a.sstride0 = 0, a.ng0 = (k + group - 1) / group;
     a.K = k, a.N = n, a.group = group, a.m_plain = m, a.out = y;
     return launch_mirror<kPlain, 0>(a, 1, st);
+}
+
+hipError_t mirror_gemm_bf16(const float* x, const uint16_t* w, const float* bias, int m, int n, int k, float* y,
+                            hipStream_t st) {
+    MirrorArgs a{};
+    a.a = x;
+    a.wfmt = 1;
+    a.wplain = w;
+    a.bias = bias;
+    a.K = k, a.N = n, a.m_plain = m, a.out = y;
+    return launch_mirror<kPlain, 1>(a, 1, st);
+}
+
+// ---------------------------------------------------------------------------
+// Elementwise helpers of the host-grouping decode branch (the reference's
+// gpu_ops.cu:12-45,85-111): 4 elements per thread where the row length allows.
+// ---------------------------------------------------------------------------
+__global__ void silu_mul_kernel(const float* g, const float* u, float* out, long long n) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = silu_mul_ref(g[i], u[i]);
+}
+
+__global__ void add_scaled_kernel(float* dst, const float* src, float scale, long long n) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = fmaf(scale, src[i], dst[i]);
+}
+
+// out[row_idx[r], c] += w[r] * vals[r, c]; rows that name the same output row
+// add atomically (the reference's plain += leaves that case undefined)
+__global__ void scatter_add_scaled_kernel(float* out, const float* vals, const int* row_idx, const float* w, int rows,
+                                          int cols) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)rows * cols) return;
+    const int r = (int)(i / cols), c = (int)(i - (long long)r * cols);
+    atomicAdd(out + (size_t)row_idx[r] * cols + c, w[r] * vals[i]);
+}
+
+__global__ void gather_rows_kernel(float* dst, const float* src, const int* row_idx, int rows, int cols) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)rows * cols) return;
+    const int r = (int)(i / cols), c = (int)(i - (long long)r * cols);
+    dst[i] = src[(size_t)row_idx[r] * cols + c];
+}
+
+static dim3 grid_for(long long n) { return dim3((unsigned)((n + 255) / 256)); }
+
+hipError_t mirror_silu_mul(const float* g, const float* u, float* out, long long n, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    launch_k(silu_mul_kernel, grid_for(n), dim3(256), 0, st, g, u, out, n);
+    return hipGetLastError();
+}
+
+hipError_t mirror_add_scaled(float* dst, const float* src, float scale, long long n, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    launch_k(add_scaled_kernel, grid_for(n), dim3(256), 0, st, dst, src, scale, n);
+    return hipGetLastError();
+}
+
+hipError_t mirror_scatter_add_scaled(float* out, const float* vals, const int* row_idx, const float* w, int rows,
+                                     int cols, hipStream_t st) {
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    launch_k(scatter_add_scaled_kernel, grid_for((long long)rows * cols), dim3(256), 0, st, out, vals, row_idx, w,
+             rows, cols);
+    return hipGetLastError();
+}
+
+hipError_t mirror_gather_rows(float* dst, const float* src, const int* row_idx, int rows, int cols, hipStream_t st) {
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    launch_k(gather_rows_kernel, grid_for((long long)rows * cols), dim3(256), 0, st, dst, src, row_idx, rows, cols);
+    return hipGetLastError();
 }
 
 hipError_t mirror_gate_up_bf16(const float* x, const uint16_t* const* gw, const uint16_t* const* uw,

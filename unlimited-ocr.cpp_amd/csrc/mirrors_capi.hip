@@ -186,3 +186,50 @@ int uocr_hip_moe_gemm_int4_tc_pipe(const float* x, const uint8_t* packed, const 
 }
 
 }  // extern "C"
+
+// ---- dense and elementwise operator mirrors (include/uocr/cuda_ops.h:31-41,
+// 242-253; src/kernels/cuda/backend.cu:542-627, gpu_ops.cu:12-45,85-111) ----
+extern "C" {
+
+int uocr_hip_matmul_t_bf16(const float* x, const uint16_t* w, const float* bias, float* y, int m, int n, int k,
+                           void* stream) {
+    if (m <= 0 || n <= 0 || k <= 0) return UOCR_HIP_OK;  // reference: early return (backend.cu:611)
+    if (!x || !w || !y) return bad("null argument");
+    if (!mirror_shapes_ok(k, n, 32, false))
+        return set_error(UOCR_HIP_EUNSUPPORTED, "this build needs n % 64 == 0 and k % 32 == 0");
+    if (!aligned16(x) || !aligned16(w)) return bad("x and w must be 16-byte aligned");
+    return hip_status(mirror_gemm_bf16(x, w, bias, m, n, k, y, (hipStream_t)stream), "bf16 gemm launch");
+}
+
+int uocr_hip_matvec_bf16(const float* x, const uint16_t* w, const float* bias, float* y, int n, int k,
+                         void* stream) {
+    return uocr_hip_matmul_t_bf16(x, w, bias, y, 1, n, k, stream);
+}
+
+int uocr_hip_silu_mul(const float* gate, const float* up, float* out, int n, void* stream) {
+    if (n <= 0) return UOCR_HIP_OK;
+    if (!gate || !up || !out) return bad("null argument");
+    return hip_status(mirror_silu_mul(gate, up, out, n, (hipStream_t)stream), "silu_mul launch");
+}
+
+int uocr_hip_add_scaled(float* dst, const float* src, float scale, int n, void* stream) {
+    if (n <= 0) return UOCR_HIP_OK;
+    if (!dst || !src) return bad("null argument");
+    return hip_status(mirror_add_scaled(dst, src, scale, n, (hipStream_t)stream), "add_scaled launch");
+}
+
+int uocr_hip_scatter_add_scaled(float* out, const float* vals, const int* row_idx, const float* weights, int rows,
+                                int cols, void* stream) {
+    if (rows <= 0 || cols <= 0) return UOCR_HIP_OK;
+    if (!out || !vals || !row_idx || !weights) return bad("null argument");
+    return hip_status(mirror_scatter_add_scaled(out, vals, row_idx, weights, rows, cols, (hipStream_t)stream),
+                      "scatter_add_scaled launch");
+}
+
+int uocr_hip_gather_rows(float* dst, const float* src, const int* row_idx, int rows, int cols, void* stream) {
+    if (rows <= 0 || cols <= 0) return UOCR_HIP_OK;
+    if (!dst || !src || !row_idx) return bad("null argument");
+    return hip_status(mirror_gather_rows(dst, src, row_idx, rows, cols, (hipStream_t)stream), "gather_rows launch");
+}
+
+}  // extern "C"

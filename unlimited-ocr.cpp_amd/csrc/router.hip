@@ -17,6 +17,8 @@
 //   grouping src/engine/gpu_decoder.cu:602-609 -- per expert, tokens in
 //            ascending (token, j) order: a stable counting sort, built here from
 //            wave ballots (equal-expert masks) and per-wave LDS prefix counts.
+#include <mutex>
+
 #include "launch.hpp"
 #include "routing.hpp"
 
@@ -27,6 +29,17 @@ namespace uocr_hip {
 // silently, src/kernels/cuda/moe_device.cu:90-95). Written with vector atomics,
 // read and cleared by router_overflow_read.
 __device__ int g_router_overflow;
+
+// Grouping scratch of the moe_router_topk mirror, whose reference signature
+// has no workspace: the multi-workgroup grouping's per-entry ranks and
+// per-(chunk, expert) counts / bases for up to kMirrorGroupEntries routed
+// entries (larger calls run the single-workgroup rounds). One copy per device;
+// host code reaches it through hipGetSymbolAddress only.
+constexpr int kMirrorGroupEntries = 1 << 17;
+constexpr int kMirrorGroupChunks = kMirrorGroupEntries / 1024;
+__device__ int g_mirror_lrank[kMirrorGroupEntries];
+__device__ int g_mirror_chunk_count[kMirrorGroupChunks * kMaxExperts];
+__device__ int g_mirror_chunk_base[kMirrorGroupChunks * kMaxExperts];
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -630,6 +643,32 @@ hipError_t router_overflow_read(int clear, int* flag) {
     if (e != hipSuccess || !clear) return e;
     const int zero = 0;
     return hipMemcpyToSymbol(HIP_SYMBOL(g_router_overflow), &zero, sizeof(int), 0, hipMemcpyHostToDevice);
+}
+
+hipError_t launch_group_mirror(GroupArgs g, hipStream_t st) {
+    if (group_chunks(g.seq, g.top_k) > 1 && (long long)g.seq * g.top_k <= kMirrorGroupEntries) {
+        static std::mutex mu;
+        static void* addr[3][64] = {};
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return e;
+        if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+        {
+            std::lock_guard<std::mutex> lock(mu);
+            if (!addr[0][dev]) {
+                if ((e = hipGetSymbolAddress(&addr[0][dev], HIP_SYMBOL(g_mirror_lrank))) != hipSuccess ||
+                    (e = hipGetSymbolAddress(&addr[1][dev], HIP_SYMBOL(g_mirror_chunk_count))) != hipSuccess ||
+                    (e = hipGetSymbolAddress(&addr[2][dev], HIP_SYMBOL(g_mirror_chunk_base))) != hipSuccess) {
+                    addr[0][dev] = nullptr;
+                    return e;
+                }
+            }
+        }
+        g.lrank = static_cast<int*>(addr[0][dev]);
+        g.chunk_count = static_cast<int*>(addr[1][dev]);
+        g.chunk_base = static_cast<int*>(addr[2][dev]);
+    }
+    return launch_group(g, st);
 }
 
 hipError_t launch_group(const GroupArgs& g, hipStream_t st) {

@@ -107,6 +107,12 @@ SIGNATURES = {
     "uocr_hip_moe_gemm_int4_tc_n": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p]),
     "uocr_hip_moe_gemm_int4_tc_nk": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p]),
     "uocr_hip_moe_gemm_int4_tc_pipe": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p]),
+    "uocr_hip_matmul_t_bf16": (C.c_int, [C.c_void_p] * 4 + [C.c_int] * 3 + [C.c_void_p]),
+    "uocr_hip_matvec_bf16": (C.c_int, [C.c_void_p] * 4 + [C.c_int] * 2 + [C.c_void_p]),
+    "uocr_hip_silu_mul": (C.c_int, [C.c_void_p] * 3 + [C.c_int, C.c_void_p]),
+    "uocr_hip_add_scaled": (C.c_int, [C.c_void_p, C.c_void_p, C.c_float, C.c_int, C.c_void_p]),
+    "uocr_hip_scatter_add_scaled": (C.c_int, [C.c_void_p] * 4 + [C.c_int, C.c_int, C.c_void_p]),
+    "uocr_hip_gather_rows": (C.c_int, [C.c_void_p] * 3 + [C.c_int, C.c_int, C.c_void_p]),
     "uocr_hip_moe_router_topk": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int,
                                             C.c_float, C.c_int, C.c_void_p, C.c_void_p,
                                             C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,

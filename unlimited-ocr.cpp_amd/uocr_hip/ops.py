@@ -72,16 +72,22 @@ def moe_experts_masked_int4(x, gate, up, down, assign_token, assign_w, count, ca
         out.data_ptr(), _stream(stream)))
 
 
-def _ptr_array(mats, device):
+def _ptr_array(mats, device, stream=None):
+    """Device table of the matrices' pointers. Its upload is ordered on torch's
+    current stream; a launch on another `stream` first waits for that copy.
+    The caller keeps the returned tensor alive until the launch has run."""
     import torch
-    return torch.tensor([m.data_ptr() for m in mats], dtype=torch.int64, device=device)
+    t = torch.tensor([m.data_ptr() for m in mats], dtype=torch.int64, device=device)
+    if stream is not None:
+        torch.cuda.current_stream(device).synchronize()
+    return t
 
 
 def moe_experts_masked(x, gate_w, up_w, down_w, assign_token, assign_w, count, cap, act, out, stream=None):
     """Mirror of uocr::cuda::moe_experts_masked (cuda_ops.h:139-143). gate_w /
     up_w / down_w: lists of per-expert bf16 device tensors."""
     dev = x.device
-    pg, pu, pd = _ptr_array(gate_w, dev), _ptr_array(up_w, dev), _ptr_array(down_w, dev)
+    pg, pu, pd = _ptr_array(gate_w, dev, stream), _ptr_array(up_w, dev, stream), _ptr_array(down_w, dev, stream)
     inter, hidden = gate_w[0].shape
     check(load().uocr_hip_moe_experts_masked(
         x.data_ptr(), x.shape[0], pg.data_ptr(), pu.data_ptr(), pd.data_ptr(), assign_token.data_ptr(),
@@ -93,7 +99,7 @@ def moe_experts_masked(x, gate_w, up_w, down_w, assign_token, assign_w, count, c
 def moe_grouped_gate_up_bf16(x, gate_w, up_w, assign_token, count, cap, act, bn=16, bm=64, stream=None):
     """Mirror of uocr::cuda::moe_grouped_gate_up_bf16 (cuda_ops.h:192-195)."""
     dev = x.device
-    pg, pu = _ptr_array(gate_w, dev), _ptr_array(up_w, dev)
+    pg, pu = _ptr_array(gate_w, dev, stream), _ptr_array(up_w, dev, stream)
     inter, hidden = gate_w[0].shape
     check(load().uocr_hip_moe_grouped_gate_up_bf16(
         x.data_ptr(), pg.data_ptr(), pu.data_ptr(), assign_token.data_ptr(), count.data_ptr(), len(gate_w), cap,
@@ -104,7 +110,7 @@ def moe_grouped_gate_up_bf16(x, gate_w, up_w, assign_token, count, cap, act, bn=
 def moe_grouped_down_bf16(act, down_w, assign_token, assign_w, count, cap, out, bn=16, bm=64, stream=None):
     """Mirror of uocr::cuda::moe_grouped_down_bf16 (cuda_ops.h:197-200)."""
     dev = act.device
-    pd = _ptr_array(down_w, dev)
+    pd = _ptr_array(down_w, dev, stream)
     hidden, inter = down_w[0].shape
     check(load().uocr_hip_moe_grouped_down_bf16(
         act.data_ptr(), pd.data_ptr(), assign_token.data_ptr(), assign_w.data_ptr(), count.data_ptr(), len(down_w),
@@ -124,3 +130,43 @@ def moe_gemm_int4(x, packed, scales, zeros, n, k, group, y, variant="", stream=N
     else:
         rc = lib.uocr_hip_moe_gemm_int4_tc_nk(*base, 16, 64, _stream(stream))
     check(rc)
+
+
+def matmul_t_bf16(x, w_bits, y, bias=None, stream=None):
+    """Mirror of uocr::cuda::matmul_t_bf16 (cuda_ops.h:31-32): y = x . W^T + bias,
+    W bf16 bits (int16/uint16 tensor [n, k])."""
+    m, k = x.shape
+    n = w_bits.shape[0]
+    check(load().uocr_hip_matmul_t_bf16(x.data_ptr(), w_bits.data_ptr(), bias.data_ptr() if bias is not None else None,
+                                        y.data_ptr(), m, n, k, _stream(stream)))
+
+
+def matvec_bf16(x, w_bits, y, bias=None, stream=None):
+    """Mirror of uocr::cuda::matvec_bf16 (cuda_ops.h:41-42)."""
+    n, k = w_bits.shape
+    check(load().uocr_hip_matvec_bf16(x.data_ptr(), w_bits.data_ptr(), bias.data_ptr() if bias is not None else None,
+                                      y.data_ptr(), n, k, _stream(stream)))
+
+
+def silu_mul(gate, up, out, stream=None):
+    """Mirror of uocr::cuda::silu_mul (cuda_ops.h:242-243)."""
+    check(load().uocr_hip_silu_mul(gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.numel(), _stream(stream)))
+
+
+def add_scaled(dst, src, scale, stream=None):
+    """Mirror of uocr::cuda::add_scaled (cuda_ops.h:245-246)."""
+    check(load().uocr_hip_add_scaled(dst.data_ptr(), src.data_ptr(), float(scale), dst.numel(), _stream(stream)))
+
+
+def scatter_add_scaled(out, vals, row_idx, weights, stream=None):
+    """Mirror of uocr::cuda::scatter_add_scaled (cuda_ops.h:248-250)."""
+    rows, cols = vals.shape
+    check(load().uocr_hip_scatter_add_scaled(out.data_ptr(), vals.data_ptr(), row_idx.data_ptr(), weights.data_ptr(),
+                                             rows, cols, _stream(stream)))
+
+
+def gather_rows(dst, src, row_idx, stream=None):
+    """Mirror of uocr::cuda::gather_rows (cuda_ops.h:252-253)."""
+    rows, cols = dst.shape
+    check(load().uocr_hip_gather_rows(dst.data_ptr(), src.data_ptr(), row_idx.data_ptr(), rows, cols,
+                                      _stream(stream)))
