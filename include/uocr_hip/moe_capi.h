@@ -190,11 +190,15 @@ int uocr_hip_moe_layer_read_timing(uocr_hip_moe_layer* layer, float* stage_ms, i
  * 1 = prefill (LDS-tiled MFMA GEMM). */
 int uocr_hip_moe_layer_path(const uocr_hip_moe_layer* layer, int seq);
 
-/* Sticky fault flags of the single-kernel decode path (no counterpart in the
- * reference; for callers and tests that verify a run): bit 0 = a bounded wait
- * between workgroups timed out, bit 1 = an exact top-k pick was outside the
- * candidate experts the down pass was computed for. Either fault also makes
- * the affected call's `out` rows NaN, so a result is never silently wrong.
+/* Sticky fault flags of the layer (no counterpart in the reference; for
+ * callers and tests that verify a run): bit 0 = a bounded wait between
+ * workgroups of the single-kernel decode path timed out, bit 1 = an exact
+ * top-k pick was outside the candidate experts that path's down pass was
+ * computed for (either fault also makes the affected call's `out` rows NaN,
+ * so a result is never silently wrong); bit 2 = an expert activation
+ * (silu(g) * u) or a prefill / unquantised-expert down output staged as f16
+ * left f16's range (|v| >= 65520 or NaN) and was stored as inf / NaN, which
+ * reaches `out` as non-finite values.
  * Waits for the device, stores the flags in *flags and, if clear is non-zero,
  * resets them. */
 int uocr_hip_moe_layer_status(uocr_hip_moe_layer* layer, int clear, int* flags);
@@ -377,8 +381,10 @@ int uocr_hip_st_read_u8(const uocr_hip_st_file* file, const char* name, uint8_t*
 /* *value = the metadata string for key, or NULL (valid until close). */
 int uocr_hip_st_metadata(const uocr_hip_st_file* file, const char* key, const char** value);
 
-/* Group size of a pre-quantized (GPTQ) file: the integer "group" of its
- * "uocr_int4" JSON metadata, else fallback_group (weights.cpp:140-151). */
+/* Group size of a pre-quantized (GPTQ) file: the "group" of its "uocr_int4"
+ * JSON metadata as nlohmann's get<int>() reads it (an integer; a float
+ * truncated toward zero; a boolean as 0 / 1), else fallback_group -- no
+ * entry, unparsable JSON or another kind (weights.cpp:140-151). */
 int uocr_hip_gptq_group(const uocr_hip_st_file* file, int fallback_group);
 /* make_quantized's pre-quantized branch (weights.cpp:138-165): the INT4 matrix
  * <weight_name>.packed (U8 [rows, ceil(cols/2)]), .scales and .zeros (F32

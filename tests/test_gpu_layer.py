@@ -277,3 +277,19 @@ def test_symmetric_quantizer_f32_scales(dev, seq):
     assert all((q.zeros == 8).all() for q in L.down[:3])
     x = synth.bf16_normal(np.random.default_rng(seq), (seq, L.hidden), 1.0)
     check_parity(L, x, dev, sample=32 if seq > 64 else None, label=f"sym-f32scale-t{seq}")
+
+
+@pytest.mark.parametrize("seq,dtype", [(300, "bf16"), (16, "f32")])
+def test_f16_staging_overflow_flagged(dev, seq, dtype):
+    """Activations staged as f16 that leave f16's range set status bit 2 (and
+    reach the output as non-finite values); ordinary inputs leave it clear."""
+    from uocr_hip import MoELayerInt4, synth
+    L = synth.random_layer(900 + seq, group=32)
+    layer = MoELayerInt4(L)
+    x = synth.bf16_normal(np.random.default_rng(seq), (seq, L.hidden), 1.0)
+    run_layer(layer, x, dtype, dev)
+    assert layer.status() == 0
+    _, _, out = run_layer(layer, x * np.float32(2000.0), dtype, dev)  # |silu(g) * u| >> 65504
+    assert layer.status() & 4 and not np.isfinite(out).all()
+    assert layer.status() == 0  # cleared by the read
+    layer.close()

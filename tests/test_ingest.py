@@ -80,13 +80,28 @@ def test_reader_bf16_f16_special_values_and_misaligned_data(tmp_path):
     ({"uocr_int4": json.dumps({"group": 128})}, 128),
     ({"uocr_int4": "not json"}, 32),               # unparsable: fallback (weights.cpp:149-151)
     ({"uocr_int4": json.dumps({"scheme": "x"})}, 32),
-    ({"uocr_int4": json.dumps({"group": "64"})}, 32),  # not an integer
+    ({"uocr_int4": json.dumps({"group": "64"})}, 32),  # a string: get<int>() throws, fallback
+    ({"uocr_int4": json.dumps({"group": 128.0})}, 128),  # a float: get<int>() converts it
+    ({"uocr_int4": json.dumps({"group": 64.9})}, 64),    # ... truncating toward zero
+    ({"uocr_int4": json.dumps({"group": [64]})}, 32),    # an array: throws, fallback
 ])
 def test_gptq_group_metadata(tmp_path, meta, expect):
     p = tmp_path / "m.safetensors"
     write_st(p, {"w.packed": ("U8", (1, 1), b"\x00")}, metadata=meta)
     with ingest.SafetensorsFile(p) as f:
         assert f.gptq_group(32) == expect
+
+
+def test_shape_overflow_rejected_at_open(tmp_path):
+    """A header shape whose element count wraps size_t is refused at open
+    (EINVAL), not turned into a huge allocation at read time."""
+    p = tmp_path / "bad.safetensors"
+    write_st(p, {"w": ("F32", (1 << 40, 1 << 40), b"\0" * 16)})
+    with pytest.raises(HipError, match="shape too large"):
+        ingest.SafetensorsFile(p)
+    write_st(p, {"w": ("F32", (1 << 31, 1 << 31, 1 << 3), b"\0" * 16)})
+    with pytest.raises(HipError, match="shape too large"):
+        ingest.SafetensorsFile(p)
 
 
 def gptq_file(path, mats, group, extra=None):

@@ -611,7 +611,7 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
             return rc;
         }
     }
-    if (!edense) {
+    {
         hipError_t e = hipMalloc((void**)&L->sync, sizeof(FusedSync));
         if (e == hipSuccess) e = hipMemset(L->sync, 0, sizeof(FusedSync));
         if (e != hipSuccess) {
@@ -718,6 +718,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
         sa.k = L->hidden;
         sa.seq = seq;
         sa.out16 = (f16*)(ws + p.sact);
+        sa.status = &L->sync->error;
         // the 128-slot tiles take f16 input only
         HIP_TRY(launch_dense(sa, true, kind == 0 ? bm : kDenseSkinnyBM, 0, st), "shared gate/up launch");
         DenseArgs sd{};
@@ -772,6 +773,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
         da.act = (f16*)(ws + p.act);
         da.y = (float*)(ws + p.y);
         da.out = out;
+        da.status = &L->sync->error;
         if (use_fused(L, seq, x_dtype)) {
             da.sync = L->sync;
             if ((rc = run_shared(x, 1))) return rc;
@@ -894,6 +896,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
         gu.n_tiles = g.n_tiles;
         gu.seq = seq;
         gu.out16 = (f16*)(ws + p.act);
+        gu.status = &L->sync->error;
         HIP_TRY(launch_dense(gu, true, p.bm, p.max_tiles, st), "gate/up launch");
         stage(3);
         DenseArgs dn = gu;
@@ -929,6 +932,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     gu.tile_info = g.tile_info;
     gu.n_tiles = g.n_tiles;
     gu.act_out = (f16*)(ws + p.act);
+    gu.status = &L->sync->error;
     HIP_TRY(launch_experts_prefill(gu, true, p.max_tiles, st),
             "gate/up launch");
     stage(3);

@@ -141,6 +141,15 @@ __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// An f32 value staged as f16 that leaves f16's finite range (rounds to +-inf,
+// or is NaN): the kernels that stage act / y rows in f16 report it once per
+// lane with atomicOr(status, kStatusF16Overflow) on the layer's status word.
+constexpr int kStatusF16Overflow = 4;
+__device__ __forceinline__ bool f16_overflow(float v) { return !(__builtin_fabsf(v) < 65520.0f); }
+__device__ __forceinline__ void report_f16_overflow(int* status, bool ovf) {
+    if (ovf && status) atomicOr(status, kStatusF16Overflow);
+}
+
 // silu(g) * u with the hardware reciprocal (1 ulp) in place of an IEEE divide
 __device__ __forceinline__ float silu_mul_f(float g, float u) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u; }
 

@@ -236,7 +236,9 @@ __global__ __launch_bounds__(256, (GU && (GPT == 4 || ZP)) ? 2 : 3) void expert_
                 const int m = 4 * (lane >> 4) + i;
                 if (m < rows) {
                     if constexpr (GU) {
-                        a.act[(size_t)(slot_base + m0 + m) * n_rows + col] = (f16)silu_mul_f(acc0[i], acc1[i]);
+                        const float v = silu_mul_f(acc0[i], acc1[i]);
+                        report_f16_overflow(a.status, f16_overflow(v));
+                        a.act[(size_t)(slot_base + m0 + m) * n_rows + col] = (f16)v;
                     } else {
                         // y is indexed by entry: routed (t, j) at t*top_k + j,
                         // shared group v's token t at N + v*T + t

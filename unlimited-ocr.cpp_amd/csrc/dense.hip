@@ -84,9 +84,11 @@ __device__ __forceinline__ bool tile_desc(const DenseArgs& a, int tile, int bm, 
     return true;
 }
 
-__device__ __forceinline__ void store_f16x4(f16* p, float v0, float v1, float v2, float v3) {
+// four values staged as f16 (a value beyond f16's range is reported)
+__device__ __forceinline__ void store_f16x4(f16* p, float v0, float v1, float v2, float v3, int* status) {
     f16x4 h = {(f16)v0, (f16)v1, (f16)v2, (f16)v3};
     *reinterpret_cast<f16x4*>(p) = h;
+    report_f16_overflow(status, f16_overflow(v0) || f16_overflow(v1) || f16_overflow(v2) || f16_overflow(v3));
 }
 
 }  // namespace
@@ -151,11 +153,11 @@ __global__ __launch_bounds__(64 * NW) void dense_skinny_kernel(DenseArgs a) {
     const size_t o = (size_t)(t.slot0 + m) * a.n_out + nb * 16 + 4 * (lane >> 4);
     if constexpr (GU) {
         store_f16x4(a.out16 + o, silu_mul_f(acc0[0], acc1[0]), silu_mul_f(acc0[1], acc1[1]),
-                    silu_mul_f(acc0[2], acc1[2]), silu_mul_f(acc0[3], acc1[3]));
+                    silu_mul_f(acc0[2], acc1[2]), silu_mul_f(acc0[3], acc1[3]), a.status);
     } else if (a.out32) {
         *reinterpret_cast<f32x4*>(a.out32 + o) = acc0;
     } else {
-        store_f16x4(a.out16 + o, acc0[0], acc0[1], acc0[2], acc0[3]);
+        store_f16x4(a.out16 + o, acc0[0], acc0[1], acc0[2], acc0[3], a.status);
     }
 }
 
@@ -268,7 +270,7 @@ __global__ __launch_bounds__(256) void dense_tiled_kernel(DenseArgs a) {
                 store_f16x4(a.out16 + o, silu_mul_f(acc[0][i][4 * q], acc[1][i][4 * q]),
                             silu_mul_f(acc[0][i][4 * q + 1], acc[1][i][4 * q + 1]),
                             silu_mul_f(acc[0][i][4 * q + 2], acc[1][i][4 * q + 2]),
-                            silu_mul_f(acc[0][i][4 * q + 3], acc[1][i][4 * q + 3]));
+                            silu_mul_f(acc[0][i][4 * q + 3], acc[1][i][4 * q + 3]), a.status);
             } else {
 #pragma unroll
                 for (int b = 0; b < WB; ++b) {
@@ -278,7 +280,7 @@ __global__ __launch_bounds__(256) void dense_tiled_kernel(DenseArgs a) {
                             f32x4{acc[b][i][4 * q], acc[b][i][4 * q + 1], acc[b][i][4 * q + 2], acc[b][i][4 * q + 3]};
                     else
                         store_f16x4(a.out16 + o, acc[b][i][4 * q], acc[b][i][4 * q + 1], acc[b][i][4 * q + 2],
-                                    acc[b][i][4 * q + 3]);
+                                    acc[b][i][4 * q + 3], a.status);
                 }
             }
         }

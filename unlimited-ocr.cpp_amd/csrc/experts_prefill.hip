@@ -198,6 +198,7 @@ __global__ __launch_bounds__(256) void experts_prefill_kernel(ExpertArgs a) {
     }
 
     // epilogue: lane holds C[m = msub*16 + 4*(lane/16) + r][n = nsub*16 + lane%16]
+    bool ovf = false;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -209,17 +210,21 @@ __global__ __launch_bounds__(256) void experts_prefill_kernel(ExpertArgs a) {
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const int col = ntile * 64 + wn * 32 + j * 16 + (lane & 15);
-                    a.act_out[orow + col] = (f16)silu_mul_f(acc[i][j][r], acc[i][j + 2][r]);
+                    const float v = silu_mul_f(acc[i][j][r], acc[i][j + 2][r]);
+                    ovf |= f16_overflow(v);
+                    a.act_out[orow + col] = (f16)v;
                 }
             } else {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int col = ntile * kPreBN + wn * 64 + j * 16 + (lane & 15);
+                    ovf |= f16_overflow(acc[i][j][r]);
                     a.y_out[orow + col] = (f16)acc[i][j][r];
                 }
             }
         }
     }
+    report_f16_overflow(a.status, ovf);
 }
 
 // ---------------------------------------------------------------------------
@@ -475,6 +480,7 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
                 for (int r = 0; r < 16; ++r)
                     write_vals(j, r, ep + (j * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * kEpStride);
         };
+        bool ovf = false;
         if constexpr (GU) {
             stage_rows([&](int j, int r, uint8_t* row) {
 #pragma unroll
@@ -486,6 +492,10 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
             for (int i = 0; i < 8 * JN; ++i) {
                 const int m = wave * 32 * JN + i * 4 + er;
                 const u32x4 v = *reinterpret_cast<const u32x4*>(ep + (i * 4 + er) * kEpStride + ec);
+                // an f16 with an all-ones exponent: the value left f16's range
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    ovf |= m < rows && ((v[q] & 0x7c00u) == 0x7c00u || (v[q] & 0x7c000000u) == 0x7c000000u);
                 if (m < rows)
                     *reinterpret_cast<u32x4*>(a.act_out + (size_t)(slot0 + m) * a.n_rows + ntile * (kBigBN / 2) + ec / 2) = v;
             }
@@ -504,12 +514,15 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
                     const f32x4 v = *reinterpret_cast<const f32x4*>(ep + (i * 4 + er) * kEpStride + ec);
                     // f16 rows (8 bytes per lane, 128 contiguous bytes per row)
                     const f16x4 h = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+                    ovf |= m < rows && (f16_overflow(v[0]) || f16_overflow(v[1]) || f16_overflow(v[2]) ||
+                                        f16_overflow(v[3]));
                     if (m < rows)
                         *reinterpret_cast<f16x4*>(a.y_out + (size_t)(slot0 + m) * a.n_rows + ntile * kBigBN + pass * 64 +
                                                   ec / 4) = h;
                 }
             }
         }
+        report_f16_overflow(a.status, ovf);
     };
     if (rows <= kBigBM / 2)
         body(std::integral_constant<int, 1>{});

@@ -425,8 +425,12 @@ int uocr_hip_st_open(const char* path, uocr_hip_st_file** out) {
             return set_error(UOCR_HIP_EINVAL, "unsupported or missing dtype: " + kv.first);
         if (!shape || shape->kind != Json::Arr || !offs || offs->kind != Json::Arr || offs->arr.size() != 2)
             return set_error(UOCR_HIP_EINVAL, "bad shape / data_offsets: " + kv.first);
+        size_t elems = 1;  // checked: a crafted shape must not wrap the byte counts below
         for (const Json& d : shape->arr) {
             if (!d.is_int || d.integer < 0) return set_error(UOCR_HIP_EINVAL, "bad shape: " + kv.first);
+            if (d.integer != 0 && elems > (SIZE_MAX / 8) / (size_t)d.integer)
+                return set_error(UOCR_HIP_EINVAL, "shape too large: " + kv.first);
+            elems *= (size_t)d.integer;
             ti.shape.push_back(d.integer);
         }
         if (!offs->arr[0].is_int || !offs->arr[1].is_int || offs->arr[0].integer < 0 ||
@@ -487,8 +491,9 @@ int uocr_hip_st_metadata(const uocr_hip_st_file* f, const char* key, const char*
 }
 
 // weights.cpp:140-151: the quantizer's group size from the "uocr_int4" JSON
-// metadata entry; the caller's group when it is absent, not JSON, or has no
-// integer "group".
+// metadata entry, converted as nlohmann's get<int>() converts it; the
+// caller's group when the entry is absent, not JSON, or has no convertible
+// "group".
 int uocr_hip_gptq_group(const uocr_hip_st_file* f, int fallback_group) {
     if (!f) return fallback_group;
     auto it = f->metadata.find("uocr_int4");
@@ -497,8 +502,15 @@ int uocr_hip_gptq_group(const uocr_hip_st_file* f, int fallback_group) {
     std::string err;
     if (!parse_json(it->second.data(), it->second.size(), j, err) || j.kind != Json::Obj) return fallback_group;
     const Json* g = j.get("group");
-    if (!g || !g->is_int || g->integer < INT32_MIN || g->integer > INT32_MAX) return fallback_group;
-    return (int)g->integer;
+    if (!g) return fallback_group;
+    // nlohmann's get<int>() converts any number (a float truncated toward
+    // zero, e.g. 128.0 -> 128) and a boolean; other kinds throw, and the
+    // reference then keeps the caller's group
+    if (g->kind == Json::Bool) return g->b ? 1 : 0;
+    if (g->kind != Json::Num) return fallback_group;
+    if (g->is_int) return (g->integer < INT32_MIN || g->integer > INT32_MAX) ? fallback_group : (int)g->integer;
+    if (!(g->num > -2147483649.0 && g->num < 2147483648.0)) return fallback_group;  // NaN or beyond int
+    return (int)g->num;
 }
 
 int uocr_hip_gptq_qmatrix(const uocr_hip_st_file* f, const char* weight_name, int rows, int cols,

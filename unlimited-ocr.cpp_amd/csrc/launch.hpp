@@ -96,6 +96,7 @@ struct ExpertArgs {
     const int* n_tiles;
     f16* act_out;            // gate/up: [slots, n_rows] f16
     f16* y_out;              // down: [slots, n_rows] f16 (summed in f32 by the combine)
+    int* status;             // layer status word: bit 2 when a value left f16's range
 };
 
 struct CombineArgs {
@@ -159,6 +160,7 @@ struct DecodeArgs {
     const uint16_t* down_z;
     long long gu_wstride, gu_sstride, dn_wstride, dn_sstride;
     FusedSync* sync;           // fused kernel only
+    int* status;               // layer status word: bit 2 when an act value left f16's range
     const float* shared_y;     // optional [seq, hidden] f32: the unquantised shared MLP's output
     f16* act;                  // [slots, inter]; fused: [(E + n_virtual) * seq, inter]
     float* y;                  // [slots, hidden]
@@ -212,6 +214,7 @@ struct DenseArgs {
     int seq;
     f16* out16;             // gate/up: act [slot][n_out]; down: y [slot][n_out] f16 (if out32 is null)
     float* out32;           // down: y [slot][n_out] f32
+    int* status;            // layer status word: bit 2 when a value left f16's range
 };
 bool dense_shapes_ok(int k, int n_out, bool gate_up, int bm);
 hipError_t launch_dense(const DenseArgs& a, bool gate_up, int bm, int max_tiles, hipStream_t st);
