@@ -422,6 +422,10 @@ def main():
     ap.add_argument("--formats", default="1:bf16_shared,1:bf16,3:bf16",
                     help="extra (config:format) lines; formats: " + ", ".join(FORMATS))
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="",
+                    help="run one configuration only, CFG or CFG:FORMAT (e.g. 4, 1:bf16_shared), and print its "
+                         "record (for per-kernel profiles); config 4 runs at --group")
+    ap.add_argument("--group", type=int, default=32)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run a plain copy of BYTES bytes (counter calibration)")
     args = ap.parse_args()
@@ -434,6 +438,18 @@ def main():
         sys.exit(2)
 
     graph_cfgs = {v.strip() for v in args.graph.split(",") if v.strip()}
+    if args.only:
+        c, _, fmt = args.only.partition(":")
+        c, fmt = int(c), fmt or "int4"
+        if c == 4:
+            r = run_config(4, max(args.steps // 10, 5), 3, 1, group=args.group, graph=True, fmt=fmt)
+        else:
+            reps = 2 if fmt == "bf16" else (3 if c >= 2 else args.replicas)
+            r = run_config(c, args.steps, args.warmup, reps, group=args.group, graph=str(c) in graph_cfgs, fmt=fmt)
+        r["cpu_baseline"] = None if args.no_cpu else cpu_leg(r)
+        r.pop("_check", None)
+        print(json.dumps(r))
+        return
     main_res = run_config(1, args.steps, args.warmup, args.replicas, graph="1" in graph_cfgs)
     cpu = None if args.no_cpu else cpu_leg(main_res, min_seconds=10.0)
     main_res.pop("_check", None)

@@ -431,8 +431,11 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
     L->inter = I;
     L->n_experts = E;
     L->top_k = d->top_k;
-    L->n_virtual = sdense ? 0 : S;  // an INT4 shared MLP runs as virtual expert groups
-    L->shared_dense = sdense;
+    // the shared MLP runs as virtual expert groups when it has the routed
+    // experts' format (INT4 beside INT4, unquantised beside unquantised), as
+    // its own stage (dense.hip) beside INT4 routed experts
+    L->n_virtual = (sdense && !edense) ? 0 : S;
+    L->shared_dense = sdense && !edense;
     L->experts_dense = edense;
     L->s_inter = S * I;
     L->group = G;
@@ -465,7 +468,7 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
                 delete L;
                 return rc;
             }
-        if (L->n_virtual > 0 && ((rc = scan(*d->shared_gate, "shared_gate")) || (rc = scan(*d->shared_up, "shared_up")) ||
+        if (S > 0 && !sdense && ((rc = scan(*d->shared_gate, "shared_gate")) || (rc = scan(*d->shared_up, "shared_up")) ||
                       (rc = scan(*d->shared_down, "shared_down")))) {
             delete L;
             return rc;
@@ -532,8 +535,11 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
             }
         }
         if (edense) {
+            // routed experts, then the shared MLP as S virtual groups of width
+            // inter (gate / up rows v*I.., down columns v*I..), so the grouped
+            // kernels run it as groups that see every token
             const size_t n = (size_t)I * H;
-            deg.resize((size_t)E * n);
+            deg.resize((size_t)(E + S) * n);
             deu.resize(deg.size());
             ded.resize(deg.size());
             for (int e = 0; e < E; ++e)
@@ -543,6 +549,18 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
                     free_layer(L);
                     return rc;
                 }
+            if (S > 0) {
+                std::copy(dsg.begin(), dsg.end(), deg.begin() + (size_t)E * n);
+                std::copy(dsu.begin(), dsu.end(), deu.begin() + (size_t)E * n);
+                for (int v = 0; v < S; ++v)
+                    for (int h = 0; h < H; ++h)
+                        std::copy(dsd.begin() + (size_t)h * S * I + (size_t)v * I,
+                                  dsd.begin() + (size_t)h * S * I + (size_t)(v + 1) * I,
+                                  ded.begin() + (size_t)(E + v) * n + (size_t)h * I);
+                dsg.clear();
+                dsu.clear();
+                dsd.clear();
+            }
         }
     }
 
@@ -591,9 +609,9 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
         (int4 && (rc = up_copy((void**)&L->gate_s, hgs.data(), hgs.size() * 2, "gate scales"))) ||
         (int4 && (rc = up_copy((void**)&L->up_s, hus.data(), hus.size() * 2, "up scales"))) ||
         (int4 && (rc = up_copy((void**)&L->down_s, hds.data(), hds.size() * 2, "down scales"))) ||
-        (sdense && (rc = up_copy((void**)&L->sgate, dsg.data(), dsg.size() * 2, "shared gate"))) ||
-        (sdense && (rc = up_copy((void**)&L->sup, dsu.data(), dsu.size() * 2, "shared up"))) ||
-        (sdense && (rc = up_copy((void**)&L->sdown, dsd.data(), dsd.size() * 2, "shared down"))) ||
+        (L->shared_dense && (rc = up_copy((void**)&L->sgate, dsg.data(), dsg.size() * 2, "shared gate"))) ||
+        (L->shared_dense && (rc = up_copy((void**)&L->sup, dsu.data(), dsu.size() * 2, "shared up"))) ||
+        (L->shared_dense && (rc = up_copy((void**)&L->sdown, dsd.data(), dsd.size() * 2, "shared down"))) ||
         (edense && (rc = up_copy((void**)&L->egate, deg.data(), deg.size() * 2, "expert gate"))) ||
         (edense && (rc = up_copy((void**)&L->eup, deu.data(), deu.size() * 2, "expert up"))) ||
         (edense && (rc = up_copy((void**)&L->edown, ded.data(), ded.size() * 2, "expert down"))) ||

@@ -128,6 +128,9 @@ __global__ __launch_bounds__(64 * NW) void dense_skinny_kernel(DenseArgs a) {
 #pragma unroll
         for (int i = 0; i < CH; ++i)
             if (KSW > 0 || c + i < ksw) af[i] = load_a8<AK>(a.a, abase + (c + i) * 32);
+        // every load of the chunk is in flight before the first use (left to
+        // itself the scheduler sinks loads to their uses, one round trip each)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < CH; ++i)
             if (KSW > 0 || c + i < ksw) {
