@@ -363,6 +363,114 @@ def copy_probe(nbytes, reps=5):
     print(json.dumps({"copy_probe_bytes": nbytes, "reps": reps}))
 
 
+def run_mirrors(steps, warmup, replicas=6):
+    """Config 1 through the reference's operator calls one for one (the path of
+    an engine that swaps each CUDA call for its mirror, GpuDecoder::mlp_block's
+    device branch, src/engine/gpu_decoder.cu:537-657): router GEMV
+    (matmul_t_bf16) -> moe_router_topk -> zero out -> moe_experts_masked_int4
+    on the reference's table layout; the INT4 shared MLP as moe_gemm_int4 x 3
+    + silu_mul; out += shared (add_scaled). Weight replicas as in config 1."""
+    import numpy as np
+    import torch
+    from uocr_hip import ops, synth
+    dev = torch.device("cuda:0")
+    wl = synth.make_config(1)
+    T, H, I = wl.seq, wl.layers[0].hidden, wl.layers[0].inter
+    layers = [wl.layers[0]] + [synth.random_layer(9000 + 100 + r) for r in range(1, replicas)]
+    reps = []
+    for L in layers:
+        g, u, d = (ops.RefInt4Table(q, dev) for q in (L.gate, L.up, L.down))
+        sq = [(torch.from_numpy(q.packed).to(dev), torch.from_numpy(q.scales).to(dev), torch.from_numpy(q.zeros).to(dev),
+               q.rows, q.cols, q.group) for q in (L.shared_gate, L.shared_up, L.shared_down)]
+        router = torch.from_numpy(L.router_bf16.view(np.int16)).to(dev)
+        reps.append((g, u, d, sq, router))
+    x = torch.from_numpy(wl.x).to(dev)
+    E, K, SI = 64, 6, layers[0].n_shared * I
+    logits = torch.empty(T, E, device=dev)
+    ids = torch.empty(T, K, dtype=torch.int32, device=dev)
+    w = torch.empty(T, K, device=dev)
+    at = torch.empty(E, T, dtype=torch.int32, device=dev)
+    aw = torch.empty(E, T, device=dev)
+    cnt = torch.empty(E, dtype=torch.int32, device=dev)
+    act = torch.empty(E, T, I, device=dev)
+    out = torch.empty(T, H, device=dev)
+    sg, su, sa = (torch.empty(T, SI, device=dev) for _ in range(3))
+    so = torch.empty(T, H, device=dev)
+
+    def step(i):
+        g, u, d, sq, router = reps[i % len(reps)]
+        ops.matmul_t_bf16(x, router, logits)
+        ops.moe_router_topk(logits, K, False, 1.0, False, ids, w, at, aw, cnt, T)
+        out.zero_()
+        ops.moe_experts_masked_int4(x, g, u, d, at, aw, cnt, T, act, out)
+        ops.moe_gemm_int4(x, *sq[0][:3], sq[0][3], sq[0][4], sq[0][5], sg)
+        ops.moe_gemm_int4(x, *sq[1][:3], sq[1][3], sq[1][4], sq[1][5], su)
+        ops.silu_mul(sg, su, sa)
+        ops.moe_gemm_int4(sa, *sq[2][:3], sq[2][3], sq[2][4], sq[2][5], so)
+        ops.add_scaled(out, so, 1.0)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        step(i)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    return {"workload": "config1_decode_t16_g32 via the operator mirrors", "ms_per_step": ms,
+            "tokens_per_s": T / (ms * 1e-3),
+            "sequence": "matmul_t_bf16, moe_router_topk, zero, moe_experts_masked_int4, moe_gemm_int4 x3, silu_mul, add_scaled",
+            "note": "hipEvent-timed on torch's current stream; the mirrors run a 64x64-tile MFMA kernel, the fused layer "
+                    "call is the fast path"}
+
+
+def run_rswa_prefill(steps, warmup, batch=4, rows=1000, heads=10, kv_heads=10, head_dim=128):
+    """Ragged multi-request R-SWA prefill attention (uocr_hip_rswa_attention_ragged,
+    cuda_ops.h:109-124): `batch` requests of `rows` query rows each, row t of a
+    request attending its rows [0, t] (causal). Work: 4 * head_dim flops per
+    (query row, key row, head) for the scores and the weighted sum."""
+    import ctypes as C
+    import torch
+    from uocr_hip import _lib
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    cap = rows + 128
+    stride = kv_heads * head_dim
+    g = torch.Generator(device=dev).manual_seed(6)
+    kc = torch.randn(batch * cap * stride, device=dev, generator=g)
+    vc = torch.randn(batch * cap * stride, device=dev, generator=g)
+    total = batch * rows
+    q = torch.randn(total * heads * head_dim, device=dev, generator=g)
+    out = torch.empty_like(q)
+    slots = torch.arange(batch, dtype=torch.int32, device=dev).repeat_interleave(rows)
+    pos = torch.arange(rows, dtype=torch.int32, device=dev).repeat(batch)
+    P = lambda t: C.c_void_p(t.data_ptr())
+
+    def call():
+        rc = lib.uocr_hip_rswa_attention_ragged(P(q), P(kc), P(vc), P(slots), P(pos), total, cap, heads, kv_heads,
+                                                head_dim, P(out), None)
+        if rc:
+            raise RuntimeError(lib.uocr_hip_last_error().decode())
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        call()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    pairs = batch * rows * (rows + 1) // 2
+    flops = 4.0 * head_dim * heads * pairs
+    return {"workload": f"rswa_prefill_ragged_{batch}x{rows}_h{heads}_d{head_dim}", "ms_per_step": ms,
+            "kernel": "rswa_kernel (uocr_hip_rswa_attention_ragged)", "flops": flops,
+            "tflops": flops / (ms * 1e-3) / 1e12,
+            "note": "f32 VALU online softmax, one workgroup per (row, head); no MFMA query tiling"}
+
+
 def run_rswa(steps, warmup, batch=16, prefill=1000, window=128, heads=10, kv_heads=10, head_dim=128, replicas=2):
     """R-SWA decode attention (uocr_hip_rswa_attention_batch) at the decoder's
     shapes: `batch` requests with full caches (prefill + window rows), one
@@ -414,8 +522,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--replicas", type=int, default=6)
-    ap.add_argument("--extra", default="0,2,3,4,rswa",
-                    help="extra configs to report: 0,2,3,4 and rswa (R-SWA decode attention); '' = none")
+    ap.add_argument("--extra", default="0,2,3,4,rswa,rswa_prefill,mirrors",
+                    help="extra configs to report: 0,2,3,4, rswa (R-SWA decode attention) and mirrors (config 1 "
+                         "through the operator mirrors); '' = none")
     ap.add_argument("--graph", default="",
                     help="decode configs (0, 1) replayed from a hipGraph, as a decode engine runs its step; "
                          "their eager rate is reported beside it (config 4 always runs as a graph)")
@@ -463,6 +572,12 @@ def main():
     for c in [v.strip() for v in args.extra.split(",") if v.strip()]:
         if c == "rswa":
             extras["rswa"] = run_rswa(max(args.steps // 2, 20), 5)
+            continue
+        if c == "rswa_prefill":
+            extras["rswa_prefill"] = run_rswa_prefill(10, 2)
+            continue
+        if c == "mirrors":
+            extras["mirrors"] = run_mirrors(max(args.steps // 2, 20), 5)
             continue
         c = int(c)
         if c == 4:

@@ -70,7 +70,16 @@ __global__ __launch_bounds__(256, (GU && (GPT == 4 || ZP)) ? 2 : 3) void expert_
     // then the routed experts with tokens).
     for (int e = tid; e < kMaxExperts; e += 256) hist[e] = 0;
     __syncthreads();
-    for (int i = tid; i < N; i += 256) atomicAdd(&hist[a.ids[i]], 1);
+    // the ids of a 1024-entry chunk are all requested before the first use
+    // (one L2 round trip per chunk, not per 256 entries)
+    for (int i0 = 0; i0 < N; i0 += 1024) {
+        int v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = i0 + tid + 256 * u < N ? a.ids[i0 + tid + 256 * u] : -1;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (v[u] >= 0) atomicAdd(&hist[v[u]], 1);
+    }
     __syncthreads();
     if (wave == 0) {
         int run_off = 0, run_live = a.n_virtual;
@@ -114,6 +123,15 @@ __global__ __launch_bounds__(256, (GU && (GPT == 4 || ZP)) ? 2 : 3) void expert_
     }
     __syncthreads();
     const int n_items = ipre[n_live_s];
+    // Up to 512 routed entries: every wave keeps the ids in registers (lane l,
+    // register u: entry 64u + l), read once here -- an item's entry list then
+    // needs no global load, whose round trip would queue behind the weight
+    // stream of the other workgroups (measured at 3-4 us per item).
+    constexpr int kIdRegs = 8;
+    const bool ids_in_regs = N <= 64 * kIdRegs;
+    int idr[kIdRegs];
+#pragma unroll
+    for (int u = 0; u < kIdRegs; ++u) idr[u] = ids_in_regs && 64 * u + lane < N ? a.ids[64 * u + lane] : -1;
 
     const int r = lane & 15;
     const uint8_t* wsrc0 = GU ? a.gate : a.down;
@@ -145,12 +163,20 @@ __global__ __launch_bounds__(256, (GU && (GPT == 4 || ZP)) ? 2 : 3) void expert_
         if (g < E) {
             const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
             int run = 0;
-            for (int base = 0; base < N; base += 64) {
-                const int i = base + lane;
-                const bool hit = i < N && a.ids[i] == g;
-                const uint64_t m = __ballot(hit);
-                if (hit) ent[run + __popcll(m & below)] = i;
-                run += __popcll(m);
+            // 512 entries per round: every id of the round is requested
+            // before the first compare (one L2 round trip, not eight)
+            for (int base = 0; base < N; base += 512) {
+                int v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    v[u] = ids_in_regs ? idr[u] : (base + 64 * u + lane < N ? a.ids[base + 64 * u + lane] : -1);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const bool hit = v[u] == g;
+                    const uint64_t m = __ballot(hit);
+                    if (hit) ent[run + __popcll(m & below)] = base + 64 * u + lane;
+                    run += __popcll(m);
+                }
             }
         } else {
             for (int i = lane; i < T; i += 64) ent[i] = i;
