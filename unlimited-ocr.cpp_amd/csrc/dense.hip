@@ -19,9 +19,12 @@
 //     weight stream is limited by HBM, not by latency; the waves' partial sums
 //     meet in LDS.
 //   * dense_tiled_kernel -- 128 slots per tile (prefill). Activations are
-//     staged in LDS per 128-column k-tile (double-buffered); each wave streams
-//     its own weight rows into registers one k-tile ahead and runs
-//     v_mfma_f32_32x32x16_f16 against the 4 staged 32-slot subtiles.
+//     staged in LDS per 128-column k-tile, one k-tile ahead (double-buffered);
+//     each wave loads its own weight rows for the k-tile into registers and
+//     runs v_mfma_f32_32x32x16_f16 against the 4 staged 32-slot subtiles. Two
+//     workgroups per CU hide each other's load latency (measured faster than
+//     one workgroup per CU with the weights double-buffered in registers, and
+//     than 192-slot tiles).
 // Gate/up (GU) pairs a gate block with the same up rows and writes
 // silu(g) * u as f16 act; down writes y (f16 per slot for the combine of the
 // grouped path, f32 per token for the shared MLP).
@@ -165,14 +168,14 @@ __global__ __launch_bounds__(64 * NW) void dense_skinny_kernel(DenseArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Prefill-sized tiles (128 slots). Workgroup = (tile, output columns: GU 128
-// act columns = 4 waves x (32 gate + 32 up rows); down 256 = 4 waves x 64
-// rows). Activations: wave w stages 32-slot subtile w of each 128-column
+// Prefill-sized tiles (128 slots), two workgroups per CU. Workgroup = (tile,
+// output columns: GU 128 act columns = 4 waves x (32 gate + 32 up rows); down
+// 256 = 4 waves x 64 rows). Activations: wave w stages 32-slot subtile w of each 128-column
 // k-tile into LDS in 32x32x16 operand order (fragment (msub, s) = 1 KiB,
 // lane l: slot l % 32, columns s * 16 + 8 * (l / 32) .. + 8).
 // ---------------------------------------------------------------------------
 template <bool GU>
-__global__ __launch_bounds__(256) void dense_tiled_kernel(DenseArgs a) {
+__global__ __launch_bounds__(256, 2) void dense_tiled_kernel(DenseArgs a) {
     constexpr int NS = 8;  // k16-steps per 128-column k-tile
     constexpr int WB = 2;  // 32-row weight blocks per wave
     __shared__ __attribute__((aligned(16))) f16 As[2][4 * NS * 512];
@@ -213,22 +216,22 @@ __global__ __launch_bounds__(256) void dense_tiled_kernel(DenseArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[b][i][r] = 0.f;
     f16x8 ar[NS];
-    f16x8 bq[2][WB][NS];
-    auto load_a = [&](int kt) {
+    f16x8 bq[WB][NS];
+    auto load_a = [&](int kt) __attribute__((always_inline)) {
 #pragma unroll
         for (int s = 0; s < NS; ++s) ar[s] = *reinterpret_cast<const f16x8*>(asrc + kt * kTileK + s * 16);
     };
-    auto write_a = [&](int buf) {
+    auto write_a = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int s = 0; s < NS; ++s) *reinterpret_cast<f16x8*>(&As[buf][((wave * NS + s) * 64 + lane) * 8]) = ar[s];
     };
-    auto load_b = [&](int kt, f16x8 (&dst)[WB][NS]) {
+    auto load_b = [&](int kt) __attribute__((always_inline)) {
 #pragma unroll
         for (int b = 0; b < WB; ++b)
 #pragma unroll
-            for (int s = 0; s < NS; ++s) dst[b][s] = load_w8(bsrc[b] + kt * kTileK + s * 16);
+            for (int s = 0; s < NS; ++s) bq[b][s] = load_w8(bsrc[b] + kt * kTileK + s * 16);
     };
-    auto compute = [&](int buf, f16x8 (&bw)[WB][NS]) {
+    auto compute = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
             f16x8 af[4];
@@ -237,27 +240,22 @@ __global__ __launch_bounds__(256) void dense_tiled_kernel(DenseArgs a) {
 #pragma unroll
             for (int b = 0; b < WB; ++b)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[b][i] = mfma32(bw[b][s], af[i], acc[b][i]);
+                for (int i = 0; i < 4; ++i) acc[b][i] = mfma32(bq[b][s], af[i], acc[b][i]);
         }
     };
-    load_b(0, bq[0]);
+    // the weights of k-tile kt are issued at the top of its own iteration (no
+    // register double buffer: two workgroups per CU hide each other's
+    // latency), the activations one k-tile ahead through LDS
     load_a(0);
     write_a(0);
     __syncthreads();
-    for (int kt0 = 0; kt0 < KT; kt0 += 2) {
-        sfor<2>([&](auto u) {
-            constexpr int U = decltype(u)::value;
-            const int kt = kt0 + U;
-            if (kt >= KT) return;
-            const bool more = kt + 1 < KT;
-            if (more) {
-                load_b(kt + 1, bq[U ^ 1]);
-                load_a(kt + 1);
-            }
-            compute(U, bq[U]);
-            if (more) write_a(U ^ 1);
-            __syncthreads();
-        });
+    for (int kt = 0; kt < KT; ++kt) {
+        const bool more = kt + 1 < KT;
+        load_b(kt);
+        if (more) load_a(kt + 1);
+        compute(kt & 1);
+        if (more) write_a((kt + 1) & 1);
+        __syncthreads();
     }
     // D lane l: weight row 8 * (r / 4) + 4 * (l / 32) + r % 4 of the block, slot l % 32 of subtile i
 #pragma unroll
