@@ -166,9 +166,9 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* layer, const void* x, i
  * allocation. No counterpart in the reference: for callers that cannot call
  * hipMalloc (code under HIP graph capture without a pre-allocated workspace,
  * serving loops or harnesses that forbid allocation). The workspace is a
- * library-owned device array of 16 MiB per device (held until the process
+ * library-owned device array of 64 MiB per device (held until the process
  * ends); calls whose uocr_hip_moe_layer_workspace_size exceeds it return
- * UOCR_HIP_EINVAL (about 250 decode tokens at the Unlimited-OCR shapes).
+ * UOCR_HIP_EINVAL (about 1100 tokens at the Unlimited-OCR shapes).
  * Every call on one device shares that array: calls that overlap in time on
  * one device (different streams without ordering) race and must not be
  * issued. The layer's device must be current. */
@@ -189,6 +189,23 @@ int uocr_hip_moe_layer_read_timing(uocr_hip_moe_layer* layer, float* stage_ms, i
 /* Which expert kernels forward uses for `seq` tokens: 0 = decode (GEMV-like),
  * 1 = prefill (LDS-tiled MFMA GEMM). */
 int uocr_hip_moe_layer_path(const uocr_hip_moe_layer* layer, int seq);
+
+/* Decode-path kernel choice (no counterpart in the reference: a tuning and
+ * testing knob of this build). AUTO picks by batch size and input; the others
+ * force one implementation wherever it applies (else forward falls back to the
+ * four-launch path): STREAM = one launch, every expert group streamed once with
+ * gate/up and down together (split-K partials); FUSED = one launch with the
+ * gate/up -> down hand-over between workgroups; FOUR_LAUNCH = router, gate/up,
+ * down and combine kernels. uocr_hip_moe_layer_decode_kernel reports the
+ * choice forward makes for (seq, x_dtype), -1 on the prefill path. */
+enum {
+    UOCR_HIP_DECODE_AUTO = 0,
+    UOCR_HIP_DECODE_STREAM = 1,
+    UOCR_HIP_DECODE_FUSED = 2,
+    UOCR_HIP_DECODE_FOUR_LAUNCH = 3
+};
+int uocr_hip_moe_layer_set_decode_kernel(uocr_hip_moe_layer* layer, int kind);
+int uocr_hip_moe_layer_decode_kernel(const uocr_hip_moe_layer* layer, int seq, int x_dtype);
 
 /* Sticky fault flags of the layer (no counterpart in the reference; for
  * callers and tests that verify a run): bit 0 = a bounded wait between

@@ -1,5 +1,8 @@
-"""GPU parity of the single-kernel decode path (router + experts + combine in
-one persistent launch; seq <= 16, bf16 input, hidden 1280 / inter 896).
+"""GPU parity of the single-kernel decode paths (router + experts + combine in
+one persistent launch; seq <= 16, bf16 input, hidden 1280 / inter 896): the
+streamed kernel (every expert group once, gate/up and down together as split-K
+partials) and the fused kernel (gate/up -> down hand-over between
+workgroups), each forced with set_decode_kernel and run on the same cases.
 
 The kernel's workgroups publish per-call progress words that must advance in
 step across calls, so the tests reuse one layer object across batch sizes and
@@ -12,6 +15,15 @@ import pytest
 from helpers import MAX_ABS_TOL, REL_L2_TOL, max_abs, rel_l2
 
 pytestmark = pytest.mark.gpu
+
+KINDS = ["stream", "fused"]
+
+
+def _layer(L, kind):
+    from uocr_hip import MoELayerInt4
+    layer = MoELayerInt4(L)
+    layer.set_decode_kernel(kind)
+    return layer
 
 
 def _forward(layer, x_np, dev, ws=None):
@@ -34,7 +46,7 @@ def _check(L, x, got, label):
     assert np.array_equal(ids, ids_o), f"{label}: routing ids differ at {np.argwhere(ids != ids_o)[:5]}"
     assert np.array_equal(w.view(np.uint32), w_o.view(np.uint32)), f"{label}: routing weights not bit-exact"
     r, m = rel_l2(out, out_o), max_abs(out, out_o)
-    print(f"[fused] {label}: rel_l2={r:.3e} max_abs={m:.3e}", flush=True)
+    print(f"[decode1] {label}: rel_l2={r:.3e} max_abs={m:.3e}", flush=True)
     assert r <= REL_L2_TOL and m <= MAX_ABS_TOL, label
 
 
@@ -43,29 +55,32 @@ def _status_clear(layer, label):
     assert flags == 0, f"{label}: fused status flags {flags:#x}"
 
 
+@pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("group", [32, 64, 128])
-def test_fused_batch_sizes_one_layer(dev, group):
+def test_fused_batch_sizes_one_layer(dev, group, kind):
     """One layer object, the batch size changing between calls: 12..16 tokens
     run the single kernel with dense gate/up, 1..11 tokens the same kernel with
     gate/up over the candidate groups only, so the progress words and the
     schedule must stay consistent across calls that switch modes."""
     from uocr_hip import MoELayerInt4, synth
     L = synth.random_layer(4100 + group, group=group)
-    layer = MoELayerInt4(L)
+    layer = _layer(L, kind)
     for seq in (16, 1, 3, 11, 12, 16, 7):
         x = synth.bf16_normal(np.random.default_rng(seq * 7 + group), (seq, L.hidden), 1.0)
-        print(f"[fused] group={group} seq={seq}", flush=True)
-        _check(L, x, _forward(layer, x, dev), f"g{group}-t{seq}")
+        print(f"[decode1] {kind} group={group} seq={seq}", flush=True)
+        assert layer.decode_kernel(seq) == kind
+        _check(L, x, _forward(layer, x, dev), f"{kind}-g{group}-t{seq}")
     _status_clear(layer, f"g{group}")
     layer.close()
 
 
-def test_fused_repeat_deterministic(dev):
+@pytest.mark.parametrize("kind", KINDS)
+def test_fused_repeat_deterministic(dev, kind):
     """Ten calls in a row give bit-identical results (fixed reduction order,
     progress words advancing every call)."""
     from uocr_hip import MoELayerInt4, synth
     L = synth.random_layer(4200)
-    layer = MoELayerInt4(L)
+    layer = _layer(L, kind)
     x = synth.bf16_normal(np.random.default_rng(5), (16, L.hidden), 1.0)
     first = _forward(layer, x, dev)
     _check(L, x, first, "repeat-0")
@@ -76,11 +91,12 @@ def test_fused_repeat_deterministic(dev):
     layer.close()
 
 
-def test_fused_two_layers_interleaved(dev):
+@pytest.mark.parametrize("kind", KINDS)
+def test_fused_two_layers_interleaved(dev, kind):
     """Two layers (separate progress words) called alternately on one workspace."""
     from uocr_hip import MoELayerInt4, synth
     La, Lb = synth.random_layer(4300), synth.random_layer(4301)
-    la, lb = MoELayerInt4(La), MoELayerInt4(Lb)
+    la, lb = _layer(La, kind), _layer(Lb, kind)
     x = synth.bf16_normal(np.random.default_rng(9), (14, La.hidden), 1.0)
     ws = la.alloc_workspace(14, dev)
     for rep in range(3):
@@ -90,13 +106,14 @@ def test_fused_two_layers_interleaved(dev):
     lb.close()
 
 
-def test_fused_graph_replay(dev):
+@pytest.mark.parametrize("kind", KINDS)
+def test_fused_graph_replay(dev, kind):
     """Captured in a HIP graph and replayed: every replay equals the eager
     result, with eager work and synchronisations between the replays."""
     import torch
     from uocr_hip import MoELayerInt4, synth
     L = synth.random_layer(4400)
-    layer = MoELayerInt4(L)
+    layer = _layer(L, kind)
     seq = 16
     x_np = synth.bf16_normal(np.random.default_rng(11), (seq, L.hidden), 1.0)
     eager = _forward(layer, x_np, dev)
@@ -127,8 +144,9 @@ def test_fused_graph_replay(dev):
     layer.close()
 
 
+@pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("ulps", [0, 1])
-def test_fused_tied_router_rows(dev, ulps):
+def test_fused_tied_router_rows(dev, ulps, kind):
     """Ties at the top-k boundary: five experts lead by a router bias, then a
     pair whose router rows are identical (ulps=0: equal scores, the lower index
     wins) or one bf16 ulp apart in one column. The candidate experts must hold
@@ -141,12 +159,12 @@ def test_fused_tied_router_rows(dev, ulps):
     L.router_bf16[20] = L.router_bf16[9]
     if ulps:
         L.router_bf16[20, 100] = L.router_bf16[9, 100] + np.uint16(ulps)
-    layer = MoELayerInt4(L)
+    layer = _layer(L, kind)
     # every candidate source: 16 tokens (dense, the routers' candidates), 7
     # (sparse, the routers' candidates), 3 and 1 (sparse, the per-expert
     # estimate workgroups)
     for seq in (16, 7, 3, 1):
-        print(f"[fused] tied ulps={ulps} seq={seq}", flush=True)
+        print(f"[decode1] {kind} tied ulps={ulps} seq={seq}", flush=True)
         # small channels 1.. keep the bias order: five leaders, then the pair
         x = synth.bf16_normal(np.random.default_rng(13), (seq, L.hidden), 0.01)
         x[:, 0] = 1.0
@@ -158,13 +176,14 @@ def test_fused_tied_router_rows(dev, ulps):
     layer.close()
 
 
-def test_fused_status_async_and_path(dev):
+@pytest.mark.parametrize("kind", KINDS)
+def test_fused_status_async_and_path(dev, kind):
     """The stream-ordered status copy reads the same (clear) flags as the
     synchronising query, and 16-token bf16 calls take the decode path."""
     import torch
     from uocr_hip import MoELayerInt4, synth
     L = synth.random_layer(4600)
-    layer = MoELayerInt4(L)
+    layer = _layer(L, kind)
     x = synth.bf16_normal(np.random.default_rng(21), (16, L.hidden), 1.0)
     _check(L, x, _forward(layer, x, dev), "status-async")
     flags = torch.full((1,), -1, dtype=torch.int32, device=dev)
@@ -174,3 +193,41 @@ def test_fused_status_async_and_path(dev):
     assert layer.path(16) == "decode"
     _status_clear(layer, "status-async")
     layer.close()
+
+
+@pytest.mark.parametrize("group", [32, 128])
+@pytest.mark.parametrize("quantizer", ["awq", "symmetric"])
+def test_stream_reference_quantizers(dev, group, quantizer):
+    """The streamed kernel on layers from the reference's own quantizers
+    (asymmetric zeros in [0, 15] and arbitrary f32 scales for AWQ): its down
+    scales and zero offsets come from the k-tile-ordered copy made at create."""
+    from helpers import awq_layer
+    L = awq_layer(4700 + group, group=group, quantizer=quantizer)
+    layer = _layer(L, "stream")
+    for seq in (16, 5):
+        x = synth_x(seq, L.hidden, 4700 + seq)
+        print(f"[decode1] stream {quantizer} g{group} seq={seq}", flush=True)
+        _check(L, x, _forward(layer, x, dev), f"stream-{quantizer}-g{group}-t{seq}")
+    _status_clear(layer, f"stream-{quantizer}")
+    layer.close()
+
+
+def test_stream_bf16_shared(dev):
+    """INT4 routed experts beside the reference's unquantised (bf16) shared
+    MLP: the shared MLP's launches write y_shared, which the streamed kernel's
+    combine adds."""
+    from uocr_hip import synth
+    L = synth.random_layer(4800)
+    synth.with_bf16_shared(L, 4801)
+    layer = _layer(L, "stream")
+    for seq in (16, 3):
+        x = synth_x(seq, L.hidden, 4800 + seq)
+        print(f"[decode1] stream bf16-shared seq={seq}", flush=True)
+        _check(L, x, _forward(layer, x, dev), f"stream-bf16shared-t{seq}")
+    _status_clear(layer, "stream-bf16shared")
+    layer.close()
+
+
+def synth_x(seq, hidden, seed):
+    from uocr_hip import synth
+    return synth.bf16_normal(np.random.default_rng(seed), (seq, hidden), 1.0)

@@ -32,7 +32,7 @@ def test_noalloc_matches_forward(dev, sizes, dtype):
     layer = MoELayerInt4(L)
     for seq in sizes:  # second call smaller than the first
         print(f"[noalloc] seq={seq} dtype={dtype}", flush=True)
-        assert layer.workspace_size(seq) <= 16 << 20
+        assert layer.workspace_size(seq) <= 64 << 20
         xn = synth.bf16_normal(np.random.default_rng(seq), (seq, L.hidden), 1.0)
         x = torch.from_numpy(xn).to(dev)
         x = x.to(torch.bfloat16) if dtype == "bf16" else x.float()
@@ -50,8 +50,8 @@ def test_noalloc_rejects_oversized_batch(dev):
 
     L = synth.random_layer(6200, group=32)
     layer = MoELayerInt4(L)
-    seq = 1024
-    assert layer.workspace_size(seq) > 16 << 20
+    seq = 4096
+    assert layer.workspace_size(seq) > 64 << 20
     x = torch.zeros(seq, L.hidden, dtype=torch.bfloat16, device=dev)
     out = torch.empty(seq, L.hidden, dtype=torch.float32, device=dev)
     with pytest.raises(HipError) as ei:

@@ -133,7 +133,7 @@ int repack(const uocr_hip_qmatrix& q, int row0, int R, int col0, int K, uint8_t*
 // device, held until the process ends; the host-side name `scratch` is only a
 // stand-in -- its device address comes from hipGetSymbolAddress, looked up once
 // per device at layer creation (scratch_ptr) and used for every access.
-constexpr size_t kScratchBytes = 16u << 20;
+constexpr size_t kScratchBytes = 64u << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace {
@@ -176,6 +176,14 @@ struct uocr_hip_moe_layer {
     uint16_t* gate_z = nullptr;  // zero offsets (null: symmetric layer, zero 8 implicit)
     uint16_t* up_z = nullptr;
     uint16_t* down_z = nullptr;
+    // down scales / zero offsets of the streamed decode kernel, [Ev][inter/128][hidden][128/group]
+    uint16_t* down_skt = nullptr;
+    uint16_t* down_zkt = nullptr;
+    // the streamed decode kernel's copy of the packed weights, in the order
+    // its waves use them: unit u (1 KiB: a gate, up or down tile) of every
+    // (item, wave) side by side, [kUnits][Ev * inter/128][8 waves][1 KiB]
+    uint8_t* sw = nullptr;
+    int decode_kernel = UOCR_HIP_DECODE_AUTO;  // uocr_hip_moe_layer_set_decode_kernel
     long long gu_wstride = 0, gu_sstride = 0, dn_wstride = 0, dn_sstride = 0;
     // unquantised matrices as f16 row-major (dense.hip): the shared MLP
     // [s_inter][hidden] / [hidden][s_inter] and the routed experts
@@ -203,7 +211,7 @@ namespace {
 void free_layer(uocr_hip_moe_layer* L) {
     if (!L) return;
     void* ptrs[] = {L->router_t, L->router_f32, L->rms_weight, L->gate,   L->up,   L->down, L->gate_s,
-                    L->up_s,     L->down_s,     L->gate_z,     L->up_z,   L->down_z, L->sync,
+                    L->up_s,     L->down_s,     L->gate_z,     L->up_z,   L->down_z, L->sync, L->down_skt, L->down_zkt, L->sw,
                     L->sgate,    L->sup,        L->sdown,      L->egate,  L->eup,    L->edown};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
@@ -289,9 +297,24 @@ bool use_prefill(const uocr_hip_moe_layer* L, int seq) {
 constexpr int kFusedMinSeq = 1;
 
 bool use_fused(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
+    if (L->decode_kernel == UOCR_HIP_DECODE_FOUR_LAUNCH || L->decode_kernel == UOCR_HIP_DECODE_STREAM) return false;
     return L->sync && !L->experts_dense && L->router_t && seq >= kFusedMinSeq && seq <= kFusedMaxSeq && x_dtype == UOCR_HIP_DTYPE_BF16 &&
            !L->rms_weight &&
            decode_fused_ok(L->hidden, L->inter, L->group) && L->n_experts + L->n_virtual <= kMaxExperts;
+}
+
+// Streamed decode kernel (decode_stream.hip): from kStreamMinSeq tokens every
+// expert group streams once for all tokens, gate/up and the matching down
+// columns together (split-K partials), with no wait between expert passes.
+constexpr int kStreamMinSeq = 6;
+bool stream_layer_ok(const uocr_hip_moe_layer* L) {
+    return L->sync && !L->experts_dense && L->router_t && L->down_skt && L->sw && !L->rms_weight &&
+           decode_stream_ok(L->hidden, L->inter, L->group) && L->n_experts + L->n_virtual <= kMaxExperts;
+}
+bool use_stream(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
+    if (L->decode_kernel == UOCR_HIP_DECODE_FOUR_LAUNCH || L->decode_kernel == UOCR_HIP_DECODE_FUSED) return false;
+    const int lo = L->decode_kernel == UOCR_HIP_DECODE_STREAM ? 1 : kStreamMinSeq;
+    return stream_layer_ok(L) && seq >= lo && seq <= kStreamMaxSeq && x_dtype == UOCR_HIP_DTYPE_BF16;
 }
 
 
@@ -345,8 +368,12 @@ WsPlan plan(const uocr_hip_moe_layer* L, int seq) {
     const bool fused_rows =
         seq <= kFusedMaxSeq && L->sync && !L->experts_dense && decode_fused_ok(L->hidden, L->inter, L->group);
     const size_t rows = fused_rows ? (size_t)std::max(p.slots, Ev * seq) : (size_t)p.slots;
+    // the streamed decode kernel's y: split-K partial rows [group][inter/128][token]
+    const size_t yrows = (seq <= kStreamMaxSeq && stream_layer_ok(L))
+                             ? std::max(rows, (size_t)Ev * (L->inter / kTileK) * seq)
+                             : rows;
     p.act = take(rows * L->inter * 2);
-    p.y = take(rows * L->hidden * 4);
+    p.y = take(yrows * L->hidden * 4);
     const int chunks = group_chunks(seq, L->top_k);
     p.lrank = take((size_t)seq * L->top_k * 4);
     p.chunk_count = take((size_t)chunks * L->n_experts * 4);
@@ -592,6 +619,52 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
                 rf[((size_t)c4 * 64 + e) * 4 + i] = v;
             }
 
+    // down scales (and zero offsets) once more as [Ev][inter/128][hidden][128/group]
+    // for the streamed decode kernel: an item (group, 128 inter columns) reads
+    // its k-tile's scales of every hidden row as one contiguous block
+    std::vector<uint16_t> hdsk, hdzk;
+    if (Ev > 0 && decode_stream_ok(H, I, G)) {
+        const int KTD = I / kTileK, GPT = kTileK / G, NGD = scale_row_stride(I, G);
+        hdsk.resize((size_t)Ev * KTD * H * GPT);
+        if (!sym) hdzk.resize(hdsk.size());
+        for (int e = 0; e < Ev; ++e)
+            for (int s = 0; s < KTD; ++s)
+                for (int row = 0; row < H; ++row)
+                    for (int gi = 0; gi < GPT; ++gi) {
+                        const size_t dst = (((size_t)e * KTD + s) * H + row) * GPT + gi;
+                        const size_t src = (size_t)e * L->dn_sstride + (size_t)row * NGD + s * GPT + gi;
+                        hdsk[dst] = hds[src];
+                        if (!sym) hdzk[dst] = hdz[src];
+                    }
+    }
+    // streamed copy of the weights (see uocr_hip_moe_layer::sw): item
+    // i = g * (inter/128) + s covers inter rows s*128.. of group g; its wave w
+    // uses gate / up k-tiles kt of row block s*8 + w (units 2kt, 2kt + 1) and
+    // the down tiles of row blocks w*NTD + j at k-tile s (units 2*KTG + j)
+    std::vector<uint8_t> hsw;
+    if (Ev > 0 && decode_stream_ok(H, I, G)) {
+        constexpr int NW = 8;
+        const int KTG = H / kTileK, KTD = I / kTileK, NS = KTD, NTD = H / kTileRows / NW;
+        const int U = 2 * KTG + NTD;
+        const size_t NI = (size_t)Ev * NS;
+        hsw.resize((size_t)U * NI * NW * kTileBytes);
+        for (size_t i = 0; i < NI; ++i) {
+            const int g = (int)(i / NS), s = (int)(i % NS);
+            for (int w = 0; w < NW; ++w)
+                for (int u = 0; u < U; ++u) {
+                    const uint8_t* src;
+                    if (u < 2 * KTG) {
+                        const int kt = u / 2, rb = s * NW + w;
+                        const std::vector<uint8_t>& m = (u & 1) ? hu : hg;
+                        src = &m[(size_t)g * L->gu_wstride + ((size_t)rb * KTG + kt) * kTileBytes];
+                    } else {
+                        const int j = u - 2 * KTG, rb = w * NTD + j;
+                        src = &hd[(size_t)g * L->dn_wstride + ((size_t)rb * KTD + s) * kTileBytes];
+                    }
+                    std::memcpy(&hsw[(((size_t)u * NI + i) * NW + w) * kTileBytes], src, kTileBytes);
+                }
+        }
+    }
     auto up_copy = [&](void** dst, const void* src, size_t bytes, const char* what) -> int {
         hipError_t e = hipMalloc(dst, bytes);
         if (e != hipSuccess) return fail(UOCR_HIP_ENOMEM, std::string("hipMalloc(") + what + "): " + hipGetErrorString(e));
@@ -609,6 +682,9 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
         (int4 && (rc = up_copy((void**)&L->gate_s, hgs.data(), hgs.size() * 2, "gate scales"))) ||
         (int4 && (rc = up_copy((void**)&L->up_s, hus.data(), hus.size() * 2, "up scales"))) ||
         (int4 && (rc = up_copy((void**)&L->down_s, hds.data(), hds.size() * 2, "down scales"))) ||
+        (!hdsk.empty() && (rc = up_copy((void**)&L->down_skt, hdsk.data(), hdsk.size() * 2, "down scales (k-tile order)"))) ||
+        (!hsw.empty() && (rc = up_copy((void**)&L->sw, hsw.data(), hsw.size(), "streamed weights"))) ||
+        (!hdzk.empty() && (rc = up_copy((void**)&L->down_zkt, hdzk.data(), hdzk.size() * 2, "down zeros (k-tile order)"))) ||
         (L->shared_dense && (rc = up_copy((void**)&L->sgate, dsg.data(), dsg.size() * 2, "shared gate"))) ||
         (L->shared_dense && (rc = up_copy((void**)&L->sup, dsu.data(), dsu.size() * 2, "shared up"))) ||
         (L->shared_dense && (rc = up_copy((void**)&L->sdown, dsd.data(), dsd.size() * 2, "shared down"))) ||
@@ -630,13 +706,16 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
         }
     }
     {
-        hipError_t e = hipMalloc((void**)&L->sync, sizeof(FusedSync));
-        if (e == hipSuccess) e = hipMemset(L->sync, 0, sizeof(FusedSync));
+        // [0]: the fused decode kernel (its error word is the layer's status
+        // word), [1]: the streamed decode kernel (own progress words and
+        // candidate tags, so that calls may switch between the two kernels)
+        hipError_t e = hipMalloc((void**)&L->sync, 2 * sizeof(FusedSync));
+        if (e == hipSuccess) e = hipMemset(L->sync, 0, 2 * sizeof(FusedSync));
         if (e != hipSuccess) {
             free_layer(L);
             return hip_fail(e, "fused work queue");
         }
-        L->device_bytes += sizeof(FusedSync);
+        L->device_bytes += 2 * sizeof(FusedSync);
     }
     *out = L;
     return UOCR_HIP_OK;
@@ -792,6 +871,19 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
         da.y = (float*)(ws + p.y);
         da.out = out;
         da.status = &L->sync->error;
+        if (use_stream(L, seq, x_dtype)) {
+            da.sync = L->sync + 1;
+            da.down_skt = L->down_skt;
+            da.sw = L->sw;
+            da.down_zkt = L->down_zkt;
+            if ((rc = run_shared(x, 1))) return rc;
+            da.shared_y = shared_y;
+            stage(5);
+            HIP_TRY(launch_decode_stream(da, st), "streamed decode launch");
+            stage(-1);
+            if (timing) Lm->pending = true;
+            return UOCR_HIP_OK;
+        }
         if (use_fused(L, seq, x_dtype)) {
             da.sync = L->sync;
             if ((rc = run_shared(x, 1))) return rc;
@@ -1008,6 +1100,22 @@ int uocr_hip_moe_layer_forward_noalloc(const uocr_hip_moe_layer* L, const void* 
     int rc = scratch_ptr(L->device, &ws);
     if (rc) return rc;
     return uocr_hip_moe_layer_forward(L, x, x_dtype, seq, out, ids_out, weights_out, ws, kScratchBytes, stream);
+}
+
+int uocr_hip_moe_layer_set_decode_kernel(uocr_hip_moe_layer* L, int kind) {
+    if (!L) return fail(UOCR_HIP_EINVAL, "null layer");
+    if (kind < UOCR_HIP_DECODE_AUTO || kind > UOCR_HIP_DECODE_FOUR_LAUNCH)
+        return fail(UOCR_HIP_EINVAL, "unknown decode kernel choice");
+    L->decode_kernel = kind;
+    return UOCR_HIP_OK;
+}
+
+int uocr_hip_moe_layer_decode_kernel(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
+    if (!L || seq <= 0) return -1;
+    if (uses_grouping(L, seq)) return -1;
+    if (use_stream(L, seq, x_dtype)) return UOCR_HIP_DECODE_STREAM;
+    if (use_fused(L, seq, x_dtype)) return UOCR_HIP_DECODE_FUSED;
+    return UOCR_HIP_DECODE_FOUR_LAUNCH;
 }
 
 int uocr_hip_moe_layer_set_timing(uocr_hip_moe_layer* L, int enable) {

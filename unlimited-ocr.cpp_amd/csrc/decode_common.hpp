@@ -174,11 +174,11 @@ __device__ __forceinline__ void lds_barrier() {
 // token t): for scale group g of the item and token t, Cs[g][t] =
 // -(1032 * sum of A at the positions that dequant8_biased biases by 1024 +
 // 72 * sum at the positions biased by 64), summed with v_dot2_f32_f16.
-template <int KT, int GPT>
+template <int KT, int GPT, int NT = 256>
 __device__ __forceinline__ void bias_seeds(const f16* As, float* Cs, int tid) {
     constexpr int NGI = KT * GPT;
     const f16x2 one = {(f16)1.0f, (f16)1.0f};
-    for (int p = tid; p < NGI * 16; p += 256) {
+    for (int p = tid; p < NGI * 16; p += NT) {
         const int g = p >> 4, t = p & 15, kt = g / GPT, gi = g % GPT;
         float xe = 0.0f, xo = 0.0f;
 #pragma unroll
@@ -227,15 +227,38 @@ __device__ __forceinline__ void lds_issue_seeds(uint32_t c_addr, f32x4 (&c)[GPT]
 // accumulator (f16 scale x f32, one fma per element). LDS operands are read
 // one k-tile ahead (asm reads, explicit lgkmcnt waits). ZOFF: bytes from a
 // scale row to its zero-offset row.
-template <int GPT, int KT, bool TWO = true, bool ZP = false, int ZOFF = 0>
+struct NoHook {
+    __device__ __forceinline__ void operator()(int) const {}
+};
+// hook(kt) runs once the MFMAs of k-tile kt are issued (its weight registers
+// are then free: a caller may load the next item's tile kt into them)
+// item_mma_f: the weight words of k-tile kt come from w0(kt) / w1(kt); ZC:
+// every zero point is 8 (symmetric layer) and the MFMAs run on the exact
+// integers q - 8 from a zero seed, with neither bias seeds nor zero-offset
+// rows (c_base unused)
+// PF: the LDS operands of k-tile kt + 1 are read while k-tile kt computes
+// (else each k-tile's are read and waited for in turn: fewer registers)
+template <int GPT, int KT, bool TWO, bool ZP, int ZOFF, bool ZC, bool PF, typename W0, typename W1, typename Hook>
+__device__ __forceinline__ void item_mma_f(W0 w0, W1 w1, uint32_t a_base, uint32_t s_base0, uint32_t s_base1,
+                                           uint32_t c_base, f32x4& acc0, f32x4& acc1, Hook hook);
+template <int GPT, int KT, bool TWO = true, bool ZP = false, int ZOFF = 0, typename Hook = NoHook>
 __device__ __forceinline__ void item_mma(const u32x4 (&bw0)[KT], const u32x4 (&bw1)[KT], uint32_t a_base,
                                          uint32_t s_base0, uint32_t s_base1, uint32_t c_base, f32x4& acc0,
-                                         f32x4& acc1) {
-    constexpr int NSEED = ZP ? 0 : GPT;  // seed reads per k-tile
+                                         f32x4& acc1, Hook hook = Hook()) {
+    item_mma_f<GPT, KT, TWO, ZP, ZOFF, false, true>([&](int kt) -> const u32x4& { return bw0[kt]; },
+                                       [&](int kt) -> const u32x4& { return bw1[kt]; }, a_base, s_base0, s_base1,
+                                       c_base, acc0, acc1, hook);
+}
+template <int GPT, int KT, bool TWO, bool ZP, int ZOFF, bool ZC, bool PF, typename W0, typename W1, typename Hook>
+__device__ __forceinline__ void item_mma_f(W0 w0, W1 w1, uint32_t a_base, uint32_t s_base0, uint32_t s_base1,
+                                           uint32_t c_base, f32x4& acc0, f32x4& acc1, Hook hook) {
+    static_assert(!(ZP && ZC), "one zero-point form");
+    constexpr bool SEEDS = !ZP && !ZC;
+    constexpr int NSEED = SEEDS ? GPT : 0;  // seed reads per k-tile
     TileRegs<GPT> tr[2];
     f32x4 cr[2][GPT];
     lds_issue_tile<GPT, ZP, ZOFF>(a_base, s_base0, s_base1, tr[0]);
-    if constexpr (!ZP) lds_issue_seeds<GPT>(c_base, cr[0]);
+    if constexpr (SEEDS) lds_issue_seeds<GPT>(c_base, cr[0]);
     // the previous group's results, scaled in after the next group's MFMAs
     // are issued (the MFMA latency is then covered)
     f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = {0.f, 0.f, 0.f, 0.f};
@@ -243,37 +266,49 @@ __device__ __forceinline__ void item_mma(const u32x4 (&bw0)[KT], const u32x4 (&b
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
         f16 s0[4], s1[4], z0[4], z1[4];
-        if (kt + 1 < KT) {
+        if constexpr (!PF) {
+            if (kt > 0) {
+                lds_issue_tile<GPT, ZP, ZOFF>(a_base + (uint32_t)(kt * 4096), s_base0 + (uint32_t)(kt * GPT * 2),
+                                              s_base1 + (uint32_t)(kt * GPT * 2), tr[0]);
+                if constexpr (SEEDS) lds_issue_seeds<GPT>(c_base + (uint32_t)(kt * GPT * 64), cr[0]);
+            }
+            lds_wait_tile<GPT, 0, ZP>(tr[0], s0, s1, z0, z1);
+        } else if (kt + 1 < KT) {
             lds_issue_tile<GPT, ZP, ZOFF>(a_base + (uint32_t)((kt + 1) * 4096), s_base0 + (uint32_t)((kt + 1) * GPT * 2),
                                           s_base1 + (uint32_t)((kt + 1) * GPT * 2), tr[(kt + 1) & 1]);
-            if constexpr (!ZP) lds_issue_seeds<GPT>(c_base + (uint32_t)((kt + 1) * GPT * 64), cr[(kt + 1) & 1]);
+            if constexpr (SEEDS) lds_issue_seeds<GPT>(c_base + (uint32_t)((kt + 1) * GPT * 64), cr[(kt + 1) & 1]);
             lds_wait_tile<GPT, tile_reads<ZP>() + NSEED, ZP>(tr[kt & 1], s0, s1, z0, z1);
         } else {
             lds_wait_tile<GPT, 0, ZP>(tr[kt & 1], s0, s1, z0, z1);
         }
-        if constexpr (!ZP) {
+        constexpr int B = PF ? 1 : 0;  // buffer mask
+        if constexpr (SEEDS) {
 #pragma unroll
-            for (int gi = 0; gi < GPT; ++gi) asm volatile("" : "+v"(cr[kt & 1][gi]));  // landed with the tile
+            for (int gi = 0; gi < GPT; ++gi) asm volatile("" : "+v"(cr[kt & B][gi]));  // landed with the tile
         }
-        const f16x8* av = tr[kt & 1].av;
+        const f16x8* av = tr[kt & B].av;
 #pragma unroll
         for (int gi = 0; gi < GPT; ++gi) {
             f32x4 r0, r1;
-            if constexpr (ZP) {
+            if constexpr (!SEEDS) {
                 r0 = f32x4{0.f, 0.f, 0.f, 0.f};
                 r1 = r0;
             } else {
-                r0 = cr[kt & 1][gi];
+                r0 = cr[kt & B][gi];
                 r1 = r0;
             }
 #pragma unroll
             for (int s = gi * 4 / GPT; s < (gi + 1) * 4 / GPT; ++s) {
                 if constexpr (ZP) {
-                    r0 = mfma16(av[s], dequant8z_unscaled(bw0[kt][s], z0[s]), r0);
-                    if constexpr (TWO) r1 = mfma16(av[s], dequant8z_unscaled(bw1[kt][s], z1[s]), r1);
+                    r0 = mfma16(av[s], dequant8z_unscaled(w0(kt)[s], z0[s]), r0);
+                    if constexpr (TWO) r1 = mfma16(av[s], dequant8z_unscaled(w1(kt)[s], z1[s]), r1);
+                } else if constexpr (ZC) {
+                    const f16 zo = (f16)-1032.0f;  // -(1024 + 8)
+                    r0 = mfma16(av[s], dequant8z_unscaled(w0(kt)[s], zo), r0);
+                    if constexpr (TWO) r1 = mfma16(av[s], dequant8z_unscaled(w1(kt)[s], zo), r1);
                 } else {
-                    r0 = mfma16(av[s], dequant8_biased(bw0[kt][s]), r0);
-                    if constexpr (TWO) r1 = mfma16(av[s], dequant8_biased(bw1[kt][s]), r1);
+                    r0 = mfma16(av[s], dequant8_biased(w0(kt)[s]), r0);
+                    if constexpr (TWO) r1 = mfma16(av[s], dequant8_biased(w1(kt)[s]), r1);
                 }
             }
 #pragma unroll
@@ -287,6 +322,7 @@ __device__ __forceinline__ void item_mma(const u32x4 (&bw0)[KT], const u32x4 (&b
             ps0 = (float)s0[gi * 4 / GPT];
             ps1 = (float)s1[gi * 4 / GPT];
         }
+        hook(kt);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -623,7 +659,7 @@ __device__ __forceinline__ void router_token(const DecodeArgs& a, int t, unsigne
     __shared__ float topv[kMaxTopK];
     __shared__ uint64_t etab[32];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int H = a.hidden, E = a.n_experts, K = a.top_k;
+    const int H = a.hidden;
     if (tid < 32) etab[tid] = uocr_exp2_tab[tid];
     const int NCH = H / kRChunkCols;
     const XT* x = static_cast<const XT*>(a.x) + (size_t)t * H;

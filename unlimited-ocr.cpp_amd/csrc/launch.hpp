@@ -117,6 +117,7 @@ constexpr int kFusedMaxSeq = 16;
 constexpr int kFusedDenseMinSeq = 12;  // fewer tokens: gate/up over the candidate groups only
 constexpr int kFusedEstMaxSeq = 4;     // up to this many: candidates from per-expert estimate workgroups
 constexpr int kFusedMaxGrid = 4096;
+constexpr int kStreamMaxSeq = 16;      // streamed decode kernel (decode_stream.hip)
 struct FusedSync {
     int progress[kFusedMaxGrid];
     int error;  // sticky: bit 0 a bounded wait timed out, bit 1 an exact pick outside the candidates
@@ -159,7 +160,10 @@ struct DecodeArgs {
     const uint16_t* up_z;
     const uint16_t* down_z;
     long long gu_wstride, gu_sstride, dn_wstride, dn_sstride;
-    FusedSync* sync;           // fused kernel only
+    const uint16_t* down_skt;  // down scales as [E + n_virtual][inter / 128][hidden][128 / group] (streamed kernel)
+    const uint16_t* down_zkt;  // down zero offsets in that layout (null: symmetric layer)
+    const uint8_t* sw;         // the streamed kernel's copy of the weights (units in order of use)
+    FusedSync* sync;           // fused kernels only
     int* status;               // layer status word: bit 2 when an act value left f16's range
     const float* shared_y;     // optional [seq, hidden] f32: the unquantised shared MLP's output
     f16* act;                  // [slots, inter]; fused: [(E + n_virtual) * seq, inter]
@@ -172,6 +176,8 @@ hipError_t launch_experts_decode2(const DecodeArgs& a, bool gate_up, hipStream_t
 hipError_t launch_combine_decode(const DecodeArgs& a, hipStream_t st);
 bool decode_fused_ok(int hidden, int inter, int group);
 hipError_t launch_decode_fused(const DecodeArgs& a, hipStream_t st);
+bool decode_stream_ok(int hidden, int inter, int group);
+hipError_t launch_decode_stream(const DecodeArgs& a, hipStream_t st);
 
 hipError_t launch_router(const RouterArgs& a, bool x_is_bf16, hipStream_t st);
 size_t router_smem_bytes(int hidden);

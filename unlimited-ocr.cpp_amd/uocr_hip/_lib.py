@@ -65,6 +65,8 @@ SIGNATURES = {
     "uocr_hip_moe_layer_device_bytes": (C.c_size_t, [C.c_void_p]),
     "uocr_hip_moe_layer_workspace_size": (C.c_size_t, [C.c_void_p, C.c_int]),
     "uocr_hip_moe_layer_path": (C.c_int, [C.c_void_p, C.c_int]),
+    "uocr_hip_moe_layer_set_decode_kernel": (C.c_int, [C.c_void_p, C.c_int]),
+    "uocr_hip_moe_layer_decode_kernel": (C.c_int, [C.c_void_p, C.c_int, C.c_int]),
     "uocr_hip_moe_layer_status": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_int)]),
     "uocr_hip_moe_layer_status_async": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
     "uocr_hip_moe_router_overflow": (C.c_int, [C.c_int, C.POINTER(C.c_int)]),

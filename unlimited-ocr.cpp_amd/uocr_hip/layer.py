@@ -110,6 +110,19 @@ class MoELayerInt4:
     def path(self, seq):
         return "prefill" if self.lib.uocr_hip_moe_layer_path(self.handle, seq) else "decode"
 
+    DECODE_KERNELS = {"auto": 0, "stream": 1, "fused": 2, "four_launch": 3}
+
+    def set_decode_kernel(self, kind):
+        """Force the decode-path implementation ("auto", "stream", "fused",
+        "four_launch"); a forced kernel that does not apply falls back to the
+        four-launch path."""
+        check(self.lib.uocr_hip_moe_layer_set_decode_kernel(self.handle, self.DECODE_KERNELS[kind]))
+
+    def decode_kernel(self, seq, x_dtype="bf16"):
+        """The decode kernel forward uses for `seq` tokens (None: prefill path)."""
+        v = self.lib.uocr_hip_moe_layer_decode_kernel(self.handle, seq, DTYPE_BF16 if x_dtype == "bf16" else DTYPE_F32)
+        return {1: "stream", 2: "fused", 3: "four_launch"}.get(v)
+
     def status(self, clear=True):
         """Sticky fault flags of the single-kernel decode path (bit 0: a wait
         between workgroups timed out; bit 1: an exact pick outside the
