@@ -6,10 +6,11 @@ tokens/s with inputs and weights resident in HBM. Each timed step runs the layer
 on the next of R distinct weight replicas, so the ~128 MB layer is streamed
 from HBM rather than from the 256 MB Infinity Cache.
 
-Roofline: the dominant kernel is the single fused decode kernel (router,
-experts and combine in one launch; algorithmic bytes = the layer's: touched
-experts' weights + shared expert + router + activations), or, where that path
-does not apply, the gate/up expert pass. Its average duration comes from HIP events stamped on that kernel's own dispatch
+Roofline: the dominant kernel is the single-launch decode kernel (streamed
+from 6 tokens, fused below; router, experts and combine in one launch;
+algorithmic bytes = the layer's: touched experts' weights + shared expert +
+router + activations), or, where that path does not apply, the gate/up expert
+pass. Its average duration comes from HIP events stamped on that kernel's own dispatch
 (hipExtLaunchKernelGGL start/stop events on the layer's stream, enabled by
 uocr_hip_moe_layer_set_timing) over a second pass of the same steps;
 achieved = algorithmic bytes per launch / that duration. traffic = HBM bytes per
@@ -212,10 +213,14 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False, fmt="int4"):
             # gate/up pass reads every expert by design)
             fu = stage["fused"] * 1e-3
             fb = avg["total"] - avg["shared"]  # the fused launch's own bytes
-            res["dominant"] = {"kernel": "decode_fused_kernel<4, 10, 7> (router + experts + combine)",
+            kind = layers[0].decode_kernel(seq, "f32" if stack else "bf16")
+            gpt = 128 // group
+            res["decode_kernel"] = kind
+            res["dominant"] = {"kernel": f"decode_{kind}_kernel<{gpt}, 10, 7, false> (router + experts + combine)",
                                "ms": stage["fused"], "bytes": fb,
                                "gbs": fb / fu / 1e9,
-                               "traffic_file": "decode_fused_config1_traffic.md" if cfg == 1 and fmt == "int4" else None}
+                               "traffic_file": f"decode_{kind}_config{cfg}_traffic.md" if fmt == "int4" else None,
+                               "profile_file": f"decode_layer_config{cfg}_kernel_stats.md" if fmt == "int4" else None}
         elif stage:
             gu = stage["gate_up"] * 1e-3
             res["gate_up_gbs"] = avg["gate_up"] / gu / 1e9

@@ -303,18 +303,28 @@ bool use_fused(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
            decode_fused_ok(L->hidden, L->inter, L->group) && L->n_experts + L->n_virtual <= kMaxExperts;
 }
 
-// Streamed decode kernel (decode_stream.hip): from kStreamMinSeq tokens every
-// expert group streams once for all tokens, gate/up and the matching down
-// columns together (split-K partials), with no wait between expert passes.
+// Streamed decode kernel (decode_stream.hip): every expert group streams once
+// for all tokens, gate/up and the matching down columns together (split-K
+// partials), with no wait between expert passes. bf16 input without RMSNorm
+// from kStreamMinSeq to kStreamMaxSeq tokens (below that the fused kernel is
+// faster); in its wide mode (after the exact routing, per-group token blocks)
+// any input, with the RMSNorm prologue, up to kStreamWideMaxSeq tokens.
 constexpr int kStreamMinSeq = 6;
 bool stream_layer_ok(const uocr_hip_moe_layer* L) {
-    return L->sync && !L->experts_dense && L->router_t && L->down_skt && L->sw && !L->rms_weight &&
+    return L->sync && !L->experts_dense && L->router_t && L->down_skt && L->sw &&
            decode_stream_ok(L->hidden, L->inter, L->group) && L->n_experts + L->n_virtual <= kMaxExperts;
+}
+bool stream_wide(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
+    return seq > kStreamMaxSeq || x_dtype != UOCR_HIP_DTYPE_BF16 || L->rms_weight;
 }
 bool use_stream(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
     if (L->decode_kernel == UOCR_HIP_DECODE_FOUR_LAUNCH || L->decode_kernel == UOCR_HIP_DECODE_FUSED) return false;
+    if (!stream_layer_ok(L) || seq < 1) return false;
+    // wide mode: an unquantised shared MLP would need the normalised input
+    // before the launch
+    if (stream_wide(L, seq, x_dtype)) return seq <= kStreamWideMaxSeq && !L->shared_dense;
     const int lo = L->decode_kernel == UOCR_HIP_DECODE_STREAM ? 1 : kStreamMinSeq;
-    return stream_layer_ok(L) && seq >= lo && seq <= kStreamMaxSeq && x_dtype == UOCR_HIP_DTYPE_BF16;
+    return seq >= lo && seq <= kStreamMaxSeq;
 }
 
 
@@ -368,10 +378,14 @@ WsPlan plan(const uocr_hip_moe_layer* L, int seq) {
     const bool fused_rows =
         seq <= kFusedMaxSeq && L->sync && !L->experts_dense && decode_fused_ok(L->hidden, L->inter, L->group);
     const size_t rows = fused_rows ? (size_t)std::max(p.slots, Ev * seq) : (size_t)p.slots;
-    // the streamed decode kernel's y: split-K partial rows [group][inter/128][token]
-    const size_t yrows = (seq <= kStreamMaxSeq && stream_layer_ok(L))
-                             ? std::max(rows, (size_t)Ev * (L->inter / kTileK) * seq)
-                             : rows;
+    // the streamed decode kernel's y: split-K partial rows [group][inter/128][token],
+    // wide mode [pick or shared row][inter/128]
+    const size_t ns = (size_t)(L->inter / kTileK);
+    size_t yrows = rows;
+    if (stream_layer_ok(L)) {
+        if (seq <= kStreamMaxSeq) yrows = std::max(yrows, (size_t)Ev * ns * seq);
+        if (seq <= kStreamWideMaxSeq) yrows = std::max(yrows, (size_t)(kStreamCandRows + L->n_virtual) * seq * ns);
+    }
     p.act = take(rows * L->inter * 2);
     p.y = take(yrows * L->hidden * 4);
     const int chunks = group_chunks(seq, L->top_k);
@@ -707,15 +721,16 @@ int uocr_hip_moe_layer_create(const uocr_hip_layer_desc* d, uocr_hip_moe_layer**
     }
     {
         // [0]: the fused decode kernel (its error word is the layer's status
-        // word), [1]: the streamed decode kernel (own progress words and
-        // candidate tags, so that calls may switch between the two kernels)
-        hipError_t e = hipMalloc((void**)&L->sync, 2 * sizeof(FusedSync));
-        if (e == hipSuccess) e = hipMemset(L->sync, 0, 2 * sizeof(FusedSync));
+        // word), [1]: the streamed decode kernel, [2]: its wide mode (own
+        // progress words and candidate tags each, so that calls may switch
+        // between kernels and modes, whose grids differ)
+        hipError_t e = hipMalloc((void**)&L->sync, 3 * sizeof(FusedSync));
+        if (e == hipSuccess) e = hipMemset(L->sync, 0, 3 * sizeof(FusedSync));
         if (e != hipSuccess) {
             free_layer(L);
             return hip_fail(e, "fused work queue");
         }
-        L->device_bytes += 2 * sizeof(FusedSync);
+        L->device_bytes += 3 * sizeof(FusedSync);
     }
     *out = L;
     return UOCR_HIP_OK;
@@ -872,7 +887,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
         da.out = out;
         da.status = &L->sync->error;
         if (use_stream(L, seq, x_dtype)) {
-            da.sync = L->sync + 1;
+            da.sync = L->sync + (stream_wide(L, seq, x_dtype) ? 2 : 1);
             da.down_skt = L->down_skt;
             da.sw = L->sw;
             da.down_zkt = L->down_zkt;

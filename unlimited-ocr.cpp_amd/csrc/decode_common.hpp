@@ -645,6 +645,62 @@ __device__ __forceinline__ void router_select(const DecodeArgs& a, int t, float 
 // build does not contract the loop; src/kernels/cpu_ops.cpp:11-24)
 #define UOCR_RMAC_SEP(X, W) "v_mul_f32 v112, " X ", " W "\nv_add_f32 %[acc], %[acc], v112\n"
 
+// The sum of the rounded squares pq[0 .. H) in column order, by one lane
+// (src/kernels/cpu_ops.cpp:58-67 as the reference build computes it; H is a
+// multiple of 64 and pq has 64 readable floats past H). The LDS reads run one
+// 32-column step ahead of the adds (asm reads with explicit waits: the
+// compiler's schedule waited on every read).
+__device__ __forceinline__ float rms_sum_chain(const float* pq, int H) {
+    // 32 columns per step: eight 16-byte reads at immediate offsets,
+    // the next step's issued before this step's adds (one instruction
+    // per column beyond the add)
+    uint32_t pb = lds_addr(pq);
+    f32x4 cur[8], nxt[8];
+    asm volatile("ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:16\n\t"
+                 "ds_read_b128 %2, %8 offset:32\n\tds_read_b128 %3, %8 offset:48\n\t"
+                 "ds_read_b128 %4, %8 offset:64\n\tds_read_b128 %5, %8 offset:80\n\t"
+                 "ds_read_b128 %6, %8 offset:96\n\tds_read_b128 %7, %8 offset:112\n\t"
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(cur[0]), "=&v"(cur[1]), "=&v"(cur[2]), "=&v"(cur[3]), "=&v"(cur[4]), "=&v"(cur[5]),
+                   "=&v"(cur[6]), "=&v"(cur[7])
+                 : "v"(pb)
+                 : "memory");
+    // Two 32-column steps per iteration with the two buffers swapping
+    // roles (no register copies between the adds; H / 32 is even).
+    auto read8 = [&](f32x4 (&d)[8], uint32_t p) {
+        asm volatile("ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:16\n\t"
+                     "ds_read_b128 %2, %8 offset:32\n\tds_read_b128 %3, %8 offset:48\n\t"
+                     "ds_read_b128 %4, %8 offset:64\n\tds_read_b128 %5, %8 offset:80\n\t"
+                     "ds_read_b128 %6, %8 offset:96\n\tds_read_b128 %7, %8 offset:112"
+                     : "=&v"(d[0]), "=&v"(d[1]), "=&v"(d[2]), "=&v"(d[3]), "=&v"(d[4]), "=&v"(d[5]),
+                       "=&v"(d[6]), "=&v"(d[7])
+                     : "v"(p)
+                     : "memory");
+    };
+    auto wait8 = [&](f32x4 (&d)[8], float& acc) {
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]), "+v"(d[4]), "+v"(d[5]), "+v"(d[6]),
+                       "+v"(d[7]), "+v"(acc));
+    };
+    float ss = 0.0f;
+    for (int c = 0; c < H; c += 64) {
+        read8(nxt, pb + 128u);  // the next step
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) ss = __fadd_rn(ss, cur[k][q]);
+        wait8(nxt, ss);
+        read8(cur, pb + 256u);  // the step after (past the end: the pad, never added)
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) ss = __fadd_rn(ss, nxt[k][q]);
+        wait8(cur, ss);
+        pb += 256u;
+    }
+    return ss;
+}
+
 // One token's routing by one 256-thread workgroup: rsmem = RING chunks of the
 // router matrix, then the token row as f32 (H floats), then H + 32 floats of
 // scratch for the RMSNorm. Waves 1..3 return after
@@ -689,53 +745,7 @@ __device__ __forceinline__ void router_token(const DecodeArgs& a, int t, unsigne
         for (int c = tid; c < H; c += 256) pq[c] = __fmul_rn(xs[c], xs[c]);
         __syncthreads();
         if (tid == 0) {
-            // 32 columns per step: eight 16-byte reads at immediate offsets,
-            // the next step's issued before this step's adds (one instruction
-            // per column beyond the add)
-            uint32_t pb = lds_addr(pq);
-            f32x4 cur[8], nxt[8];
-            asm volatile("ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:16\n\t"
-                         "ds_read_b128 %2, %8 offset:32\n\tds_read_b128 %3, %8 offset:48\n\t"
-                         "ds_read_b128 %4, %8 offset:64\n\tds_read_b128 %5, %8 offset:80\n\t"
-                         "ds_read_b128 %6, %8 offset:96\n\tds_read_b128 %7, %8 offset:112\n\t"
-                         "s_waitcnt lgkmcnt(0)"
-                         : "=&v"(cur[0]), "=&v"(cur[1]), "=&v"(cur[2]), "=&v"(cur[3]), "=&v"(cur[4]), "=&v"(cur[5]),
-                           "=&v"(cur[6]), "=&v"(cur[7])
-                         : "v"(pb)
-                         : "memory");
-            // Two 32-column steps per iteration with the two buffers swapping
-            // roles (no register copies between the adds; H / 32 is even).
-            auto read8 = [&](f32x4 (&d)[8], uint32_t p) {
-                asm volatile("ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:16\n\t"
-                             "ds_read_b128 %2, %8 offset:32\n\tds_read_b128 %3, %8 offset:48\n\t"
-                             "ds_read_b128 %4, %8 offset:64\n\tds_read_b128 %5, %8 offset:80\n\t"
-                             "ds_read_b128 %6, %8 offset:96\n\tds_read_b128 %7, %8 offset:112"
-                             : "=&v"(d[0]), "=&v"(d[1]), "=&v"(d[2]), "=&v"(d[3]), "=&v"(d[4]), "=&v"(d[5]),
-                               "=&v"(d[6]), "=&v"(d[7])
-                             : "v"(p)
-                             : "memory");
-            };
-            auto wait8 = [&](f32x4 (&d)[8], float& acc) {
-                asm volatile("s_waitcnt lgkmcnt(0)"
-                             : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]), "+v"(d[4]), "+v"(d[5]), "+v"(d[6]),
-                               "+v"(d[7]), "+v"(acc));
-            };
-            float ss = 0.0f;
-            for (int c = 0; c < H; c += 64) {
-                read8(nxt, pb + 128u);  // the next step
-#pragma unroll
-                for (int k = 0; k < 8; ++k)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) ss = __fadd_rn(ss, cur[k][q]);
-                wait8(nxt, ss);
-                read8(cur, pb + 256u);  // the step after (past the end: the pad, never added)
-#pragma unroll
-                for (int k = 0; k < 8; ++k)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) ss = __fadd_rn(ss, nxt[k][q]);
-                wait8(cur, ss);
-                pb += 256u;
-            }
+            const float ss = rms_sum_chain(pq, H);
             sc[0] = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)H), a.rms_eps)));
         }
         __syncthreads();

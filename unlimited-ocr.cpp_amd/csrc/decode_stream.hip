@@ -43,11 +43,17 @@
 namespace uocr_hip {
 
 constexpr int kStreamWaves = 8;
-// weight units (1 KiB each) in flight per wave: 6 keeps the kernel within 128
-// VGPRs, so two workgroups (16 waves) share a CU; a unit and the unit kRing
-// further on share a ring slot, so kRing divides the units of an item
-constexpr int kRing = 6;
+// weight units (1 KiB each) in flight per wave. A CU streams about (bytes in
+// flight) / (memory latency): 6 units per wave keep a kernel within 128 VGPRs,
+// so that two workgroups (16 waves) share a CU where the rest of the kernel
+// fits (group 64 / 128, 16-token mode); where it does not (group 32, wide
+// mode), one workgroup per CU keeps 10 units per wave in flight. A unit and
+// the unit kRing further on share a ring slot, so kRing divides the units of
+// an item.
+template <int GPT, bool WIDE>
+constexpr int ring_units() { return (WIDE || GPT == 4) ? 10 : 6; }
 constexpr int kStreamThreads = 64 * kStreamWaves;
+constexpr size_t align_up_c(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // LDS of a worker (the router role uses the first bytes for its own data)
 template <int GPT, int KTG, int KTD, bool ZP>
@@ -64,12 +70,20 @@ struct StreamLds {
     static constexpr int DSW = NTD * kTileRows * GPT;          // one wave's down scales (f16)
     static constexpr size_t ds_bytes = (size_t)kStreamWaves * DSW * 2 * (ZP ? 2 : 1);
     static constexpr int ZOFF_D = kStreamWaves * DSW * 2;      // scale -> zero offset (down)
-    static constexpr int n_ints = 2 * kFusedMaxSeq + kMaxExperts + 2 * kMaxTopK;
+    static constexpr int n_ints = 2 * kFusedMaxSeq + kMaxExperts + 2 * kMaxTopK + 2;
     static constexpr size_t o_ss = as_bytes;
     static constexpr size_t o_ad = o_ss + ss_bytes;
     static constexpr size_t o_ds = o_ad + ad_bytes;
     static constexpr size_t o_int = o_ds + ds_bytes;
-    static constexpr size_t bytes = o_int + (size_t)n_ints * 4;
+    // wide mode: every token's expert mask, the routing ids, per group its
+    // token count, first partial row, 16-token blocks and first extra block,
+    // each wave's token list, a combine unit's rows and items
+    static constexpr size_t o_mask = align_up_c(o_int + (size_t)n_ints * 4, 8);
+    static constexpr size_t o_ids = o_mask + (size_t)kStreamWideMaxSeq * 8;
+    static constexpr size_t o_tab = o_ids + (size_t)kStreamWideMaxSeq * kMaxTopK * 4;
+    static constexpr size_t o_wl = o_tab + (size_t)4 * kMaxExperts * 4;
+    static constexpr size_t o_cu = o_wl + (size_t)kStreamWaves * 16 * 4;
+    static constexpr size_t bytes = o_cu + (size_t)2 * (kMaxTopK + kMaxExperts) * 4 + 16;
 };
 
 // 16-byte global -> LDS DMA per lane (to lds_base + 16 * lane; lds_base
@@ -85,7 +99,17 @@ __device__ __forceinline__ void dma16(const void* src, const void* lds_base) {
     // (an M0 write needs a wait state before the LDS DMA that reads it)
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m) : "memory", "m0");
 }
+// the same, agent-coherent (rows other workgroups of the launch wrote)
+__device__ __forceinline__ void dma16_sc1(const void* src, const void* lds_base) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane(lds_addr(lds_base));
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 1\n\tglobal_load_lds_dwordx4 %0, off sc1" ::"v"(src), "s"(m)
+                 : "memory", "m0");
+}
 #pragma clang diagnostic pop
+// asm LDS word write (see lds_read_u32)
+__device__ __forceinline__ void lds_write_u32(void* p, int v) {
+    asm volatile("ds_write_b32 %0, %1" ::"v"(lds_addr(p)), "v"(v) : "memory");
+}
 // Stores whose completion only the explicit counter waits track: written as
 // asm, so the compiler's own waits for loaded registers do not see pending
 // stores (with both loads and stores pending it would wait for everything).
@@ -200,37 +224,36 @@ __device__ __forceinline__ void down_pair(const u32x4& w0, const u32x4& w1, cons
 // Combine of one unit (token t, output columns cb*128 ..): thread (slot jj,
 // column quad q); slot j < K holds the routed pick j, slot K the sum of the
 // shared groups. Rows are read agent-coherent (written by other workgroups).
+// Partial rows: [group][slice][token] (rows = null), or (wide mode) row
+// rows[jj] of [row][slice] for routed pick jj < K and shared group jj - K.
+// With an RMSNorm prologue the layer adds its input (the residual) last.
 template <int NS>
 __device__ __forceinline__ void stream_combine(const DecodeArgs& a, int t, int cb, const int* ids_t,
-                                               const float* wts_t, bool bad, float* ys) {
+                                               const float* wts_t, const int* rows, bool bad, float* ys) {
     const int tid = threadIdx.x;
     const int T = a.seq, E = a.n_experts, V = a.n_virtual, K = a.top_k, H = a.hidden;
     const int q = tid & 31, tg = tid >> 5;  // 16 thread groups of 32 column quads
     const int c = cb * 128 + q * 4;
     const bool colv = c < H;
+    // byte offset of slice 0 of pick / shared group jj
+    auto row_off = [&](int jj) -> size_t {
+        if (rows) return ((size_t)rows[jj] * NS * H + c) * 4;
+        const size_t g = jj < K ? (size_t)ids_t[jj] : (size_t)(E + jj - K);
+        return (((g * NS) * T + t) * H + c) * 4;
+    };
+    const size_t s_step = (rows ? (size_t)H : (size_t)T * H) * 4;  // bytes between slices
     for (int jj = tg; jj <= K; jj += kStreamThreads / 32) {
         f32x4 y = {0.f, 0.f, 0.f, 0.f};
         if (colv) {
-            if (jj < K) {
-                const size_t g = (size_t)ids_t[jj];
+            for (int jv = jj; jv < (jj < K ? jj + 1 : K + V); ++jv) {
+                const size_t o = row_off(jv);
                 f32x4 v[NS];
 #pragma unroll
-                for (int s = 0; s < NS; ++s) v[s] = load16_cg(a.y, (((g * NS + s) * T + t) * H + c) * 4);
+                for (int s = 0; s < NS; ++s) v[s] = load16_cg(a.y, o + s * s_step);
 #pragma unroll
                 for (int s = 0; s < NS; ++s)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) y[i] += v[s][i];
-            } else {
-                for (int vg = 0; vg < V; ++vg) {
-                    const size_t g = (size_t)(E + vg);
-                    f32x4 v[NS];
-#pragma unroll
-                    for (int s = 0; s < NS; ++s) v[s] = load16_cg(a.y, (((g * NS + s) * T + t) * H + c) * 4);
-#pragma unroll
-                    for (int s = 0; s < NS; ++s)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) y[i] += v[s][i];
-                }
             }
         }
         *reinterpret_cast<f32x4*>(ys + jj * 128 + q * 4) = y;
@@ -254,15 +277,28 @@ __device__ __forceinline__ void stream_combine(const DecodeArgs& a, int t, int c
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[i] += sv[i];
         }
+        if (a.rms_weight) {  // the residual (f32 input)
+            const f32x4 rv = *reinterpret_cast<const f32x4*>(static_cast<const float*>(a.x) + (size_t)t * H + c);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = rv[i] + acc[i];
+        }
         if (bad) acc = f32x4{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")};
         *reinterpret_cast<f32x4*>(a.out + (size_t)t * H + c) = acc;
     }
     __syncthreads();
 }
 
-template <int GPT, int KTG, int KTD, bool ZP>
+// One item of a worker: expert group g, slice s, and in wide mode the
+// 16-token block tb of the group's tokens (n of them, partial rows row0 ..);
+// wi = g * NS + s indexes the weights; tok: the token of the lane's row
+struct StreamItem {
+    int g, s, tb, wi, n, row0, tok;
+};
+
+template <int GPT, int KTG, int KTD, bool ZP, bool WIDE>
 __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(DecodeArgs a) {
     using Lay = StreamLds<GPT, KTG, KTD, ZP>;
+    constexpr int kRing = ring_units<GPT, WIDE>();
     constexpr int NS = KTD;             // slices per group (128 inter rows each)
     constexpr int NTD = Lay::NTD;       // down tiles per wave
     constexpr int NGG = Lay::NGG;
@@ -275,6 +311,15 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
     uint32_t* cm32 = reinterpret_cast<uint32_t*>(smem + Lay::o_int);  // candidate masks per token
     int* tokmask = reinterpret_cast<int*>(cm32 + 2 * kFusedMaxSeq);  // per routed group: candidate tokens
     int* misc = tokmask + kMaxExperts;
+    // wide mode tables
+    uint64_t* masks = reinterpret_cast<uint64_t*>(smem + Lay::o_mask);  // [token] picked experts
+    int* idsL = reinterpret_cast<int*>(smem + Lay::o_ids);               // [token][K]
+    int* cntL = reinterpret_cast<int*>(smem + Lay::o_tab);               // [group] tokens
+    int* baseL = cntL + kMaxExperts;                                     // [group] first partial row
+    int* nbL = baseL + kMaxExperts;                                      // [group] 16-token blocks
+    int* extL = nbL + kMaxExperts;                                       // [group] first extra block
+    int* cuL = reinterpret_cast<int*>(smem + Lay::o_cu);  // combine unit: rows [K + V], first items [K + V]
+    int* ntotL = cuL + 2 * (kMaxTopK + kMaxExperts);
 
     int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, r = lane & 15;
     auto fresh_indices = [&]() { asm volatile("" : "+v"(tid), "+v"(lane), "+v"(r), "+s"(wave)); };
@@ -343,6 +388,104 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
         have_cand = true;
     };
 
+    // Wide mode: every token's candidate experts (tagged words the routers
+    // publish with the expert input rows, before their exact chains) -> the
+    // token masks; then per group its token count, first partial row (groups
+    // in order, tokens ascending: routed rows first, then T rows per shared
+    // group), 16-token blocks and first extra block. Items: (g, s) for every
+    // group and slice (block 0), then (g, block tb >= 1, s) in group order ->
+    // NTOT. When the candidates' rows exceed the partial-row budget
+    // (kStreamCandRows per token), the exact picks take their place (every
+    // workgroup sees the same words and decides alike).
+    int NTOT = NI;
+    uint64_t my_mask = 0;  // lane t: token t's experts (every wave)
+    bool wide_ready = false;
+    auto wide_tables = [&]() -> int {  // the routed rows
+        my_mask = masks[lane];
+        for (int g = wave; g < E; g += kStreamWaves) {
+            const uint64_t bb = __ballot((my_mask >> g) & 1);
+            if (lane == 0) cntL[g] = (int)__popcll(bb);
+        }
+        __syncthreads();
+        if (wave == 0) {
+            int run_n = 0, run_x = 0;
+            for (int h = 0; h < G; h += 64) {
+                const int g = h + lane;
+                const int n = g < E ? cntL[g] : (g < G ? T : 0);
+                const int nb = (n + 15) >> 4;
+                const int xb = nb > 1 ? nb - 1 : 0;
+                int sn = n, sx = xb;
+                for (int d = 1; d < 64; d <<= 1) {
+                    const int u1 = __shfl_up(sn, d, 64), u2 = __shfl_up(sx, d, 64);
+                    if (lane >= d) {
+                        sn += u1;
+                        sx += u2;
+                    }
+                }
+                if (g < G) {
+                    baseL[g] = run_n + sn - n;
+                    nbL[g] = nb;
+                    extL[g] = run_x + sx - xb;
+                }
+                run_n += __shfl(sn, 63, 64);
+                run_x += __shfl(sx, 63, 64);
+            }
+            if (lane == 0) {
+                ntotL[0] = NI + run_x * NS;
+                ntotL[1] = run_n - V * T;  // the shared groups hold T rows each
+            }
+        }
+        __syncthreads();
+        NTOT = ntotL[0];
+        return ntotL[1];
+    };
+    auto wide_setup = [&]() {
+        if (wave == 0) {
+            uint64_t c0 = (uint64_t)rtag << 32, c1 = c0;
+            int it = 0;
+            while (true) {
+                if (lane < T) {
+                    c0 = __hip_atomic_load(sy->cand + 2 * lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    c1 = __hip_atomic_load(sy->cand + 2 * lane + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                if (!__ballot((uint32_t)(c0 >> 32) != rtag || (uint32_t)(c1 >> 32) != rtag)) break;
+                if (++it > kSpinLimit) {
+                    if (lane == 0) report_timeout_to(a.status, sy, rtag);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            masks[lane] = lane < T ? (uint64_t)(uint32_t)c0 | ((uint64_t)(uint32_t)c1 << 32) : 0ull;
+        }
+        __syncthreads();
+        fence_wg_acquire();  // the expert input rows published with the words
+        // (readfirstlane: the branch is uniform, which the compiler cannot see through LDS)
+        if (__builtin_amdgcn_readfirstlane(wide_tables()) > T * kStreamCandRows) {
+            // the exact picks (all routers done)
+            if (wave == 0) {
+                int it = 0;
+                while (__ballot(lane < T && (int)(load_cg(prog + lane) - (S + 1)) < 0)) {
+                    if (++it > kSpinLimit) {
+                        if (lane == 0) report_timeout_to(a.status, sy, rtag);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+            }
+            __syncthreads();
+            fence_wg_acquire();
+            if (wave == 0) {
+                uint64_t m = 0;
+                if (lane < T)
+                    for (int j = 0; j < K; ++j) m |= 1ull << (load_cg(a.ids + (size_t)lane * K + j) & 63);
+                masks[lane] = m;
+            }
+            __syncthreads();
+            wide_tables();
+        }
+        wide_ready = true;
+    };
+
     // ---- 1. router (workgroups 0 .. T-1)
     if (b < T) {
         float* hand = reinterpret_cast<float*>(smem);
@@ -350,7 +493,7 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
         float* topv = sc + 64;
         uint64_t* etab = reinterpret_cast<uint64_t*>(topv + kMaxTopK);
         float* xs = hand + 256;
-        router_token_regs<KTG, kStreamWaves>(a, b, hand, sc, topv, etab, xs, xs + kMaxHidden, rtag);
+        router_token_regs<KTG, kStreamWaves, WIDE>(a, b, hand, sc, topv, etab, xs, xs + kMaxHidden, rtag);
         store_fence();
         publish_now();
     }
@@ -375,12 +518,13 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
     constexpr int kUnits = 2 * KTG + NTD;
     static_assert(kUnits % kRing == 0 && kRing <= 2 * KTG, "ring slots repeat every item");
     u32x4 ring[kRing];
-    // unit u of item i (u < kUnits) into its ring slot u % kRing
+    // unit u of the item with weight index i (u < kUnits) into its ring slot u % kRing
     auto unit = [&](int i, int u) {
         ring[u % kRing] = *reinterpret_cast<const u32x4*>(
             a.sw + (((size_t)u * NI + i) * kStreamWaves + wave) * kTileBytes + (size_t)lane * 16);
     };
-    // after consuming unit u of item i: the unit kRing further on
+    // after consuming unit u of weight item i: the unit kRing further on (of
+    // i, or of the next item nx)
     auto advance = [&](int i, int u, int nx, bool more) {
         const int v = u + kRing;
         asm volatile("" ::: "memory");
@@ -417,26 +561,108 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
         }
     };
 
-    if (b >= T && b - T < NI) {
-        const int w = b - T;
-        // the token rows (all T, once): bf16 DMA, then f16 in place, then the
-        // bias seeds of every scale group. Wave w stages MFMA step w & 3 of
-        // k-tiles w >> 2, (w >> 2) + 2, ...
-        if (r < T) {
-            const uint16_t* src = xb + (size_t)r * H + (wave & 3) * 32 + 8 * (lane >> 4);
-            for (int kt = wave >> 2; kt < KTG; kt += 2) dma16(src + kt * kTileK, As + (size_t)(kt * 4 + (wave & 3)) * 64 * 8);
+    // the item at list position idx (wide mode; every wave, after wide_setup)
+    int* wlw = reinterpret_cast<int*>(smem + Lay::o_wl) + wave * 16;  // this wave's token list
+    auto witem = [&](int idx) -> StreamItem {
+        StreamItem it;
+        if (idx < NI) {
+            it.g = idx / NS;
+            it.s = idx - it.g * NS;
+            it.tb = 0;
+        } else {
+            const int e = idx - NI, xbk = e / NS;
+            it.s = e - xbk * NS;
+            it.g = 0;
+            for (int h = 0; h < G; h += 64) {
+                const int gg = h + lane;
+                const int eb = (int)lds_read_u32(extL + gg), nb = (int)lds_read_u32(nbL + gg);
+                const uint64_t hit = __ballot(gg < G && xbk >= eb && xbk < eb + nb - 1);
+                if (hit) {
+                    it.g = h + (int)__builtin_ctzll(hit);
+                    break;
+                }
+            }
+            it.tb = xbk - (int)lds_read_u32(extL + it.g) + 1;
         }
-        // issue order = the order the explicit counter waits assume
+        it.wi = it.g * NS + it.s;
+        const int ng = it.g < E ? (int)lds_read_u32(cntL + it.g) : T;
+        it.n = min(16, ng - 16 * it.tb);
+        it.row0 = (int)lds_read_u32(baseL + it.g) + 16 * it.tb;
+        if (it.g < E) {
+            const bool mem = (my_mask >> it.g) & 1;
+            const uint64_t bal = __ballot(mem);
+            const int rank = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+            if (mem && rank >= 16 * it.tb && rank < 16 * it.tb + 16) lds_write_u32(wlw + rank - 16 * it.tb, lane);
+            it.tok = it.n > 0 ? (int)lds_read_u32(wlw + (r < it.n ? r : 0)) : 0;
+        } else {
+            it.tok = 16 * it.tb + (r < it.n ? r : 0);
+        }
+        return it;
+    };
+    // StreamItem of list position i (streamed mode: every item is block 0 of all tokens)
+    auto sitem = [&](int i) -> StreamItem {
+        StreamItem it;
+        it.g = i / NS;
+        it.s = i - it.g * NS;
+        it.tb = 0;
+        it.wi = i;
+        it.n = T;
+        it.row0 = 0;
+        it.tok = r;
+        return it;
+    };
+    // wide mode: the f16 token rows of an item's block -> As (the MFMA A
+    // layout; wave w stages blocks w, w + 8, ...: k-tile blk / 4, step blk % 4)
+    constexpr int NXD = KTG * 4 / kStreamWaves;  // x DMAs per wave
+    static_assert(KTG * 4 % kStreamWaves == 0, "x blocks per wave");
+    auto x_rows = [&](int tok) {
+        const f16* src = a.x16 + (size_t)tok * H + 8 * (lane >> 4);
+#pragma unroll
+        for (int q = 0; q < NXD; ++q) {
+            const int blk = wave + kStreamWaves * q;
+            dma16_sc1(src + (blk >> 2) * kTileK + (blk & 3) * 32, As + (size_t)blk * 64 * 8);
+        }
+    };
+    // the first kRing units and the scales of weight item wi
+    auto prefetch = [&](int wi) {
         asm volatile("" ::: "memory");
-        gu_scales(w);
-        dn_scales(w);
+        gu_scales(wi);
+        dn_scales(wi);
         asm volatile("" ::: "memory");
         // (one compiler barrier per unit: the issue order is the order of use)
 #pragma unroll
         for (int u = 0; u < kRing; ++u) {
-            unit(w, u);
+            unit(wi, u);
             asm volatile("" ::: "memory");
         }
+    };
+
+    if (b >= T && (WIDE || b - T < NI)) {
+        const int w = b - T;
+        StreamItem first_item;
+        if constexpr (WIDE) {
+            // weights first (block 0 items exist whatever the routing), then
+            // the routing, then this item's token rows
+            if (w < NI) prefetch(w);
+            wide_setup();
+            if (w < NTOT) {
+                first_item = witem(w);
+                if (w >= NI) prefetch(first_item.wi);
+                x_rows(first_item.tok);
+            }
+        } else {
+            // the token rows (all T, once): bf16 DMA, then f16 in place. Wave
+            // w stages MFMA step w & 3 of k-tiles w >> 2, (w >> 2) + 2, ...
+            if (r < T) {
+                const uint16_t* src = xb + (size_t)r * H + (wave & 3) * 32 + 8 * (lane >> 4);
+                for (int kt = wave >> 2; kt < KTG; kt += 2) dma16(src + kt * kTileK, As + (size_t)(kt * 4 + (wave & 3)) * 64 * 8);
+            }
+            // issue order = the order the explicit counter waits assume
+            prefetch(w);
+            first_item = sitem(w);
+        }
+      if (w < NTOT) {
 
         // candidates: wave 0 requests the tagged words here, ahead of their
         // use in the first item's down phase, so waiting for them is part of
@@ -445,7 +671,7 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
         // retry loop and each path stores the result itself: the compiler's
         // counter waits then never merge with the loop's.
         uint64_t cw = 0;
-        if (wave == 0)
+        if (!WIDE && wave == 0)
             cw = lane < 2 * T ? __hip_atomic_load(sy->cand + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                               : ((uint64_t)rtag << 32);
         // -> cm32 (every token's candidate mask) and tokmask, wave 0 (the
@@ -481,22 +707,29 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
         // One item; MORE: a next item exists (its weights stream under this
         // item's work). The last item is a separate copy, so that the
         // compiler's own counter waits see one fixed issue order.
-        auto item = [&](int i, bool first, auto more_tag) {
+        auto item = [&](int i, const StreamItem& cur, StreamItem& nxt, bool first, auto more_tag) {
             constexpr bool MORE = decltype(more_tag)::value;
             fresh_indices();
-            const int g = i / NS, s = i % NS;
+            const int g = cur.g, s = cur.s, wi = cur.wi;
             const int nx = i + PW;
+            int wnx = WIDE ? 0 : nx;  // the next item's weight index (wide: known from the down phase on)
             // this item's gate/up scales (and, first item, the token rows and
             // down scales): older than the last kRing ops (first item: the
             // ring's loads) or 2 * NTD ops (later items: the previous down
             // phase's NTD unit loads and NTD partial stores, and its down-scale
             // DMA)
             if (first) {
-                wait_vm<kRing>();
+                if constexpr (WIDE) {
+                    wait_vm<0>();  // (the routing wait came between)
+                } else {
+                    wait_vm<kRing>();
+                }
             } else {
                 wait_vm<2 * NTD>();
             }
-            if (first) {
+            if constexpr (WIDE) {
+                lds_barrier();  // every wave's token-row DMA has landed
+            } else if (first) {
                 // this wave's DMA'd rows -> f16 in place
                 for (int kt = wave >> 2; kt < KTG; kt += 2) {
                     const uint32_t ad = lds_addr(As + (size_t)(kt * 4 + (wave & 3)) * 64 * 8 + (size_t)lane * 8);
@@ -522,17 +755,24 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
                     [&](int kt) -> const u32x4& { return ring[(2 * kt + 1) % kRing]; }, lds_addr(As + (size_t)lane * 8),
                     lds_addr(ssw + r * NGG), lds_addr(ssw + Lay::SRM + r * NGG), 0u,
                     acc0, acc1, [&](int kt) {
-                        advance(i, 2 * kt, nx, MORE);
-                        advance(i, 2 * kt + 1, nx, MORE);
+                        advance(wi, 2 * kt, wnx, MORE);
+                        advance(wi, 2 * kt + 1, wnx, MORE);
                     });
                 const int kl = 16 * wave + r;
                 const int sp = kl >> 5, cp = (kl & 31) >> 3, ip = kl & 7;
-                if (!first) lds_barrier();  // every wave is past the previous item's down (Ad, CsD reads)
+                // every wave is past the previous item's down (Ad reads) and,
+                // wide mode, this item's gate/up (As reads)
+                if (WIDE || !first) lds_barrier();
+                if constexpr (WIDE && MORE) {
+                    nxt = witem(nx);
+                    wnx = nxt.wi;
+                    x_rows(nxt.tok);
+                }
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int t = 4 * (lane >> 4) + q;
                     const float v = silu_mul_f(acc0[q], acc1[q]);
-                    ovf |= t < T && f16_overflow(v);
+                    ovf |= t < cur.n && f16_overflow(v);
                     // asm write: a plain LDS access after the DMAs would make the
                     // compiler wait for every outstanding global load
                     const f16 hv = (f16)v;
@@ -543,20 +783,20 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
             }
             // the next item's gate/up scales (this wave's gate/up MMA is done)
             asm volatile("" ::: "memory");
-            if constexpr (MORE) gu_scales(nx);
+            if constexpr (MORE) gu_scales(wnx);
             asm volatile("" ::: "memory");
             // this item's down scales and the previous item's partial stores:
             // older than the 2 * KTG unit loads of this gate/up phase (and the
-            // next item's gate/up scales)
-            wait_vm<2 * KTG>();
-            if (first) cand_resolve();
+            // next item's token rows and gate/up scales)
+            wait_vm<2 * KTG + (WIDE && MORE ? NXD : 0)>();
+            if (!WIDE && first) cand_resolve();
             lds_barrier();  // Ad, cm32 / tokmask complete; every wave's older stores done
             if (!first) {
                 ++k;  // the previous item
                 if (tid == 0) store_sc1(prog + b, S + k);  // (no fence: the counter waits ordered the stores)
             }
             have_cand = true;
-            const int tm = g < E ? (int)lds_read_u32(tokmask + g) : (int)((1u << T) - 1u);
+            const int tm = WIDE ? 0 : (g < E ? (int)lds_read_u32(tokmask + g) : (int)((1u << T) - 1u));
             // down: the act fragments (B operand) once for the item, then the
             // tile pairs; each consumed pair takes the next units of the ring.
             // A pair's partial rows of the candidate tokens are stored right
@@ -574,9 +814,9 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
             }
             const int rq = 4 * (lane >> 4);  // the lane's first row in a tile
             const u32x4 prs = buffer_desc(a.y);
-            const bool keep = r < T && ((tm >> r) & 1);
-            const int off0 = keep ? (int)(((((size_t)g * NS + s) * T + r) * H + wave * NTD * kTileRows + rq) * 4)
-                                  : (int)0x80000000;
+            const bool keep = WIDE ? r < cur.n : r < T && ((tm >> r) & 1);
+            const size_t prow = WIDE ? ((size_t)(cur.row0 + r) * NS + s) : (((size_t)g * NS + s) * T + r);
+            const int off0 = keep ? (int)((prow * H + wave * NTD * kTileRows + rq) * 4) : (int)0x80000000;
             auto store_pair = [&](int j, const f32x4& v0, const f32x4& v1) {
                 store16_sc1(prs, keep ? off0 + j * kTileRows * 4 : off0, v0);
                 store16_sc1(prs, keep ? off0 + (j + 1) * kTileRows * 4 : off0, v1);
@@ -588,22 +828,27 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
                                                 lds_addr(dsw + (j * 16 + rq) * GPT),
                                                 lds_addr(dsw + ((j + 1) * 16 + rq) * GPT), lds_addr(dsw + (j * 16 + r) * GPT),
                                                 lds_addr(dsw + ((j + 1) * 16 + r) * GPT), acc0, acc1);
-                advance(i, 2 * KTG + j, nx, MORE);
-                advance(i, 2 * KTG + j + 1, nx, MORE);
+                advance(wi, 2 * KTG + j, wnx, MORE);
+                advance(wi, 2 * KTG + j + 1, wnx, MORE);
                 store_pair(j, acc0, acc1);
             }
             // the next item's down scales (this wave's down MMA is done)
             asm volatile("" ::: "memory");
-            if constexpr (MORE) dn_scales(nx);
+            if constexpr (MORE) dn_scales(wnx);
             asm volatile("" ::: "memory");
         };
         int i = w;
-        for (; i + PW < NI; i += PW) item(i, i == w, std::true_type{});
-        item(i, i == w, std::false_type{});
+        StreamItem cur = first_item, nxt = first_item;
+        for (; i + PW < NTOT; i += PW) {
+            item(i, cur, nxt, i == w, std::true_type{});
+            cur = WIDE ? nxt : sitem(i + PW);
+        }
+        item(i, cur, nxt, i == w, std::false_type{});
         report_f16_overflow(a.status, ovf);
         // the last item: its stores, then the step
         store_fence();
         publish_now();
+      }
     }
 
     // ---- 3. combine units (token t, column block cb), one per workgroup from
@@ -616,6 +861,54 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
         int* ids_c = misc;                                   // [K]
         float* wts_c = reinterpret_cast<float*>(misc + kMaxTopK);
         float* ys = reinterpret_cast<float*>(smem + Lay::o_ad);  // (K + 1) x 128 floats (Ad, Ds)
+        if constexpr (WIDE) {
+            if (!wide_ready) wide_setup();
+            // the exact routing of token t
+            wait_steps([&](int, int& owner, int& step) { owner = t; step = 1; }, 1);
+            bool bad = false;
+            // the partial rows and first items of token t's picks and of the
+            // shared groups; an exact pick outside the token's candidates has
+            // no rows (status bit 2, NaN output)
+            if (wave == 0) {
+                const int idl = lane < K ? load_cg(a.ids + (size_t)t * K + lane) : 0;
+                const float wtl = lane < K ? load_cg(a.wts + (size_t)t * K + lane) : 0.0f;
+                for (int jj = 0; jj < K + V; ++jj) {
+                    const int g = jj < K ? __shfl(idl, jj, 64) : E + jj - K;
+                    int slot = t;
+                    if (jj < K) {
+                        const uint64_t bal = __ballot((my_mask >> g) & 1);
+                        slot = (int)__popcll(bal & ((1ull << t) - 1ull));
+                        bad |= !((bal >> t) & 1);
+                    }
+                    const int tb = slot >> 4;
+                    if (lane == 0) {
+                        cuL[jj] = baseL[g] + slot;
+                        cuL[kMaxTopK + kMaxExperts + jj] = tb == 0 ? g * NS : NI + (extL[g] + tb - 1) * NS;
+                    }
+                }
+                if (lane < K) {
+                    ids_c[lane] = idl;
+                    wts_c[lane] = wtl;
+                }
+                if (lane == 0) {
+                    misc[2 * kMaxTopK] = bad;
+                    if (bad) __hip_atomic_fetch_or(a.status, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            __syncthreads();
+            bad = misc[2 * kMaxTopK] != 0;
+            const int* ib = cuL + kMaxTopK + kMaxExperts;
+            wait_steps(
+                [&](int q, int& owner, int& step) {
+                    const int i = ib[q / NS] + q % NS;
+                    owner = T + i % PW;
+                    step = i / PW + 1;
+                },
+                (K + V) * NS);
+            bad |= load_cg(&sy->call_fault) == rtag;
+            stream_combine<NS>(a, t, cb, ids_c, wts_c, cuL, bad, ys);
+            continue;
+        }
         need_cand();
         // the exact routing of token t
         wait_steps([&](int, int& owner, int& step) { owner = t; step = 1; }, 1);
@@ -644,7 +937,7 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
                 bad = true;
             }
         }
-        stream_combine<NS>(a, t, cb, ids_c, wts_c, bad, ys);
+        stream_combine<NS>(a, t, cb, ids_c, wts_c, nullptr, bad, ys);
     }
 
     // ---- leave: every workgroup ends the call at S + kFusedSteps
@@ -652,26 +945,25 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
     if (tid == 0) store_sc1(prog + b, S + kFusedSteps);
 }
 
-template <int GPT, int KTG, int KTD, bool ZP>
+template <int GPT, int KTG, int KTD, bool ZP, bool WIDE>
 static hipError_t launch_stream(const DecodeArgs& a, hipStream_t st) {
     using Lay = StreamLds<GPT, KTG, KTD, ZP>;
     constexpr size_t lds = Lay::bytes;
     static_assert(lds <= 160 * 1024, "stream kernel LDS");
     static_assert((KTG * kTileK / kTileRows) % kStreamWaves == 0 && Lay::NTD % 2 == 0, "down tiles per wave");
-    static hipError_t attr = hipFuncSetAttribute((const void*)decode_stream_kernel<GPT, KTG, KTD, ZP>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    auto kern = decode_stream_kernel<GPT, KTG, KTD, ZP, WIDE>;
+    static hipError_t attr = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return attr;
-    static int resident = [] {
+    static int resident = [&] {
         int dev = 0, cus = 0, per_cu = 0;
         (void)hipGetDevice(&dev);
         (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_stream_kernel<GPT, KTG, KTD, ZP>,
-                                                           kStreamThreads, lds);
+        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kStreamThreads, lds);
         return std::max(1, cus * std::max(1, per_cu));
     }();
     const int grid = std::min(resident, kFusedMaxGrid);
     if (grid <= a.seq) return hipErrorInvalidConfiguration;
-    launch_k((decode_stream_kernel<GPT, KTG, KTD, ZP>), dim3(grid), dim3(kStreamThreads), (uint32_t)lds, st, a);
+    launch_k(kern, dim3(grid), dim3(kStreamThreads), (uint32_t)lds, st, a);
     return hipGetLastError();
 }
 
@@ -679,18 +971,28 @@ bool decode_stream_ok(int hidden, int inter, int group) {
     return hidden == 1280 && inter == 896 && (group == 32 || group == 64 || group == 128);
 }
 
+bool decode_stream_wide(const DecodeArgs& a) { return a.seq > kStreamMaxSeq || !a.x_bf16 || a.rms_weight; }
+
+template <bool WIDE>
+static hipError_t launch_stream_g(const DecodeArgs& a, hipStream_t st) {
+    const bool zp = a.gate_z != nullptr;
+    switch (a.group) {
+        case 32: return zp ? launch_stream<4, 10, 7, true, WIDE>(a, st) : launch_stream<4, 10, 7, false, WIDE>(a, st);
+        case 64: return zp ? launch_stream<2, 10, 7, true, WIDE>(a, st) : launch_stream<2, 10, 7, false, WIDE>(a, st);
+        default: return zp ? launch_stream<1, 10, 7, true, WIDE>(a, st) : launch_stream<1, 10, 7, false, WIDE>(a, st);
+    }
+}
+
 hipError_t launch_decode_stream(const DecodeArgs& a, hipStream_t st) {
-    if (a.seq < 1 || a.seq > kStreamMaxSeq || !a.x_bf16 || a.rms_weight || !a.sync || !a.router_t || !a.status)
+    const bool wide = decode_stream_wide(a);
+    if (a.seq < 1 || a.seq > (wide ? kStreamWideMaxSeq : kStreamMaxSeq) || !a.sync || !a.router_t || !a.status)
         return hipErrorInvalidValue;
+    // wide mode: the f16 expert input rows; with an RMSNorm the residual is the f32 input
+    if (wide && (!a.x16 || (a.rms_weight && a.x_bf16))) return hipErrorInvalidValue;
     if (!a.down_skt || !a.sw || (a.gate_z && !a.down_zkt)) return hipErrorInvalidValue;
     if (a.n_experts + a.n_virtual > kMaxExperts || a.n_experts > 64 || a.top_k > kMaxTopK) return hipErrorInvalidValue;
     if (!decode_stream_ok(a.hidden, a.inter, a.group)) return hipErrorInvalidValue;
-    const bool zp = a.gate_z != nullptr;
-    switch (a.group) {
-        case 32: return zp ? launch_stream<4, 10, 7, true>(a, st) : launch_stream<4, 10, 7, false>(a, st);
-        case 64: return zp ? launch_stream<2, 10, 7, true>(a, st) : launch_stream<2, 10, 7, false>(a, st);
-        default: return zp ? launch_stream<1, 10, 7, true>(a, st) : launch_stream<1, 10, 7, false>(a, st);
-    }
+    return wide ? launch_stream_g<true>(a, st) : launch_stream_g<false>(a, st);
 }
 
 }  // namespace uocr_hip

@@ -149,7 +149,16 @@ __device__ __forceinline__ uint64_t candidate_mask(const DecodeArgs& a, float S,
 // 16-byte reads one 8-column block ahead, so a column costs the weight's
 // widening and the fmac. The router waves run at raised issue priority (the
 // other workgroup on the CU dequantises expert weights meanwhile).
-template <int KT, int NW = 4>
+// PREP: the token row is f32 or bf16 (a.x_bf16), RMS-normalised when
+// a.rms_weight is set (src/kernels/cpu_ops.cpp:58-67). The expert input
+// (a.x16, f16, agent-coherent stores) and the candidates come first, from a
+// scale whose sum of squares is added in parallel (it differs from the
+// reference's column-order sum by at most about H unit roundoffs, which the
+// candidate bound takes in, and the f16 input far less than its own
+// rounding); then the reference's sequential sum, the exact row and the
+// exact chain. part then needs kMaxHidden + 2 * H + 64 floats beyond its
+// NW * 128 (rounded squares, the estimate's row).
+template <int KT, int NW = 4, bool PREP = false>
 __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, float* hand, float* sc, float* topv,
                                                   uint64_t* etab, float* xs, float* part, unsigned rtag) {
     constexpr int SEG = KT * 128 / NW;  // columns per wave (H = KT * 128)
@@ -162,9 +171,14 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
     constexpr int NXT = (KT * 128 + 64 * NW - 1) / (64 * NW);  // token-row passes of the workgroup
     __builtin_amdgcn_s_setprio(3);
     const uint16_t* x = static_cast<const uint16_t*>(a.x) + (size_t)t * H;
-    uint32_t xb[NXT];
+    const float* xf = static_cast<const float*>(a.x) + (size_t)t * H;
+    const bool xbf = !PREP || a.x_bf16;
+    uint32_t xb[NXT];  // bf16 bits, or (PREP, f32 x) the float's bits
 #pragma unroll
-    for (int i = 0; i < NXT; ++i) xb[i] = tid + 64 * NW * i < H ? x[tid + 64 * NW * i] : 0;
+    for (int i = 0; i < NXT; ++i) {
+        const int c = tid + 64 * NW * i;
+        xb[i] = c < H ? (xbf ? (uint32_t)x[c] : __float_as_uint(xf[c])) : 0u;
+    }
     const uint16_t* wbase = a.router_t + ((size_t)wave * NL * E + e) * 8;
     u32x4 wr[NL];
 #pragma unroll
@@ -173,10 +187,47 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
 #pragma unroll
     for (int i = 0; i < NXT; ++i) {
         asm volatile("" : "+v"(xb[i]));
-        if (tid + 64 * NW * i < H) xs[tid + 64 * NW * i] = __uint_as_float(xb[i] << 16);
+        if (tid + 64 * NW * i < H) xs[tid + 64 * NW * i] = __uint_as_float(xbf ? xb[i] << 16 : xb[i]);
     }
     lds_barrier();
+    float* pq = part + NW * 128;      // PREP + RMSNorm: rounded squares [H + 64]
+    float* xe = pq + kMaxHidden + 64;  // the estimate's row
+    const bool rms = PREP && a.rms_weight;
+    if constexpr (PREP) {
+        const float* xin = xs;
+        if (rms) {
+            float ps = 0.0f;
+            for (int c = tid; c < H; c += 64 * NW) {
+                const float q = __fmul_rn(xs[c], xs[c]);
+                pq[c] = q;
+                ps += q;
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) ps += __shfl_xor(ps, o, 64);
+            if (lane == 0) hand[wave] = ps;
+            __syncthreads();
+            float ssa = 0.0f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) ssa += hand[w];
+            const float inv_a = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ssa, (float)H), a.rms_eps)));
+            for (int c = tid; c < H; c += 64 * NW) xe[c] = __fmul_rn(__fmul_rn(xs[c], inv_a), a.rms_weight[c]);
+            __syncthreads();
+            xin = xe;
+        }
+        // the f16 expert input, written through to the coherence point
+        for (int c = tid * 8; c < H; c += 64 * NW * 8) {
+            const f32x4 p = *reinterpret_cast<const f32x4*>(xin + c);
+            const f32x4 q = *reinterpret_cast<const f32x4*>(xin + c + 4);
+            const f16x8 h = {(f16)p[0], (f16)p[1], (f16)p[2], (f16)p[3], (f16)q[0], (f16)q[1], (f16)q[2], (f16)q[3]};
+            // (the nops: wait states the hazard recognizer does not add around asm)
+            asm volatile("s_nop 4\n\tglobal_store_dwordx4 %0, %1, off sc1\n\ts_nop 4" ::"v"(a.x16 + (size_t)t * H + c),
+                         "v"(h)
+                         : "memory");
+        }
+        store_fence();  // complete before the candidates are published
+    }
     const uint32_t xa = lds_addr(xs + wave * SEG);
+    const uint32_t xea = rms ? lds_addr(xe + wave * SEG) : xa;  // the estimate's row
 
     // Candidate experts of the token, ahead of the exact chain: this wave's
     // segment as a blocked sum (8 chains) and the sum of |x w| (part[wave]).
@@ -186,7 +237,7 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
         for (int i = 0; i < NL; ++i) {
             f32x4 c0, c1, w0, w1;
             asm volatile("ds_read_b128 %0, %2 offset:%3\n\tds_read_b128 %1, %2 offset:%4\n\ts_waitcnt lgkmcnt(0)"
-                         : "=&v"(c0), "=&v"(c1) : "v"(xa), "i"(i * 32), "i"(i * 32 + 16) : "memory");
+                         : "=&v"(c0), "=&v"(c1) : "v"(xea), "i"(i * 32), "i"(i * 32 + 16) : "memory");
             asm volatile(
                 "v_lshlrev_b32 %0, 16, %8\n\tv_and_b32 %1, 0xffff0000, %8\n\t"
                 "v_lshlrev_b32 %2, 16, %9\n\tv_and_b32 %3, 0xffff0000, %9\n\t"
@@ -215,7 +266,8 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
             S += part[w * 128 + lane];
             SA += part[w * 128 + 64 + lane];
         }
-        const uint64_t m = candidate_mask(a, S, SA, (float)(H + SEG / 8 + 64));
+        // (+ H + 16 terms: the approximate RMSNorm scale of the estimate's row)
+        const uint64_t m = candidate_mask(a, S, SA, (float)(H + SEG / 8 + 64 + (rms ? H + 16 : 0)));
         if (lane < 2) {
             const uint64_t w = ((uint64_t)rtag << 32) | (uint32_t)(lane == 0 ? m : (m >> 32));
             __hip_atomic_store(a.sync->cand + 2 * t + lane, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -223,13 +275,28 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
     };
 
     // every wave estimates its segment first (in parallel); wave NW - 1 selects
-    // the candidates beside wave 0's chain segment
+    // the candidates beside wave 0's chain segment (PREP: before the exact
+    // RMSNorm sum, which lane 0 adds meanwhile)
     early_partial();
     lds_barrier();
+    if constexpr (PREP) {
+        if (wave == NW - 1) early_finish();
+        if (rms) {
+            if (tid == 0) {
+                const float ss = rms_sum_chain(pq, H);
+                sc[0] = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)H), a.rms_eps)));
+            }
+            __syncthreads();
+            const float inv = sc[0];
+            for (int c = tid; c < H; c += 64 * NW) xs[c] = __fmul_rn(__fmul_rn(xs[c], inv), a.rms_weight[c]);
+            __syncthreads();
+        }
+    }
     float acc = 0.0f;
     for (int w = 0; w < NW; ++w) {
         if (wave != w) {
-            if (w == 0 && wave == NW - 1) early_finish();
+            if constexpr (!PREP)
+                if (w == 0 && wave == NW - 1) early_finish();
         } else {
             if (w > 0) acc = hand[lane];
             f32x4 c0, c1, n0, n1;

@@ -117,7 +117,11 @@ constexpr int kFusedMaxSeq = 16;
 constexpr int kFusedDenseMinSeq = 12;  // fewer tokens: gate/up over the candidate groups only
 constexpr int kFusedEstMaxSeq = 4;     // up to this many: candidates from per-expert estimate workgroups
 constexpr int kFusedMaxGrid = 4096;
-constexpr int kStreamMaxSeq = 16;      // streamed decode kernel (decode_stream.hip)
+constexpr int kStreamMaxSeq = 16;      // streamed decode kernel (decode_stream.hip), bf16 input
+constexpr int kStreamWideMaxSeq = 64;  // its wide mode (any input, RMSNorm prologue): token masks are 64-bit
+// wide mode: partial rows per token for the routed candidates (more candidates:
+// the kernel takes the exact picks instead; >= kMaxTopK)
+constexpr int kStreamCandRows = 10;
 struct FusedSync {
     int progress[kFusedMaxGrid];
     int error;  // sticky: bit 0 a bounded wait timed out, bit 1 an exact pick outside the candidates
@@ -126,7 +130,7 @@ struct FusedSync {
     // exact routing) as (tag << 32) | mask half, experts 0..31 at 2t and 32..63
     // at 2t + 1; tag = (base >> 12) + 1 (24 bits): a reader validates each word
     // by its tag, with no separate wait for the router
-    unsigned long long cand[2 * kFusedMaxSeq];
+    unsigned long long cand[2 * kStreamWideMaxSeq];
     // up to kFusedEstMaxSeq tokens: logit estimates of (token t, expert e),
     // one workgroup per expert, as (tag << 32) | float bits: [t][e][2] =
     // estimate, sum of |x w|
