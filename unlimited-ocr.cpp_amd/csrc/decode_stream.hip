@@ -75,12 +75,10 @@ struct StreamLds {
     static constexpr size_t o_ad = o_ss + ss_bytes;
     static constexpr size_t o_ds = o_ad + ad_bytes;
     static constexpr size_t o_int = o_ds + ds_bytes;
-    // wide mode: every token's expert mask, the routing ids, per group its
-    // token count, first partial row, 16-token blocks and first extra block,
+    // wide mode: every token's expert mask, per group its token count, first partial row, 16-token blocks and first extra block,
     // each wave's token list, a combine unit's rows and items
     static constexpr size_t o_mask = align_up_c(o_int + (size_t)n_ints * 4, 8);
-    static constexpr size_t o_ids = o_mask + (size_t)kStreamWideMaxSeq * 8;
-    static constexpr size_t o_tab = o_ids + (size_t)kStreamWideMaxSeq * kMaxTopK * 4;
+    static constexpr size_t o_tab = o_mask + (size_t)kStreamWideMaxSeq * 8;
     static constexpr size_t o_wl = o_tab + (size_t)4 * kMaxExperts * 4;
     static constexpr size_t o_cu = o_wl + (size_t)kStreamWaves * 16 * 4;
     static constexpr size_t bytes = o_cu + (size_t)2 * (kMaxTopK + kMaxExperts) * 4 + 16;
@@ -288,6 +286,75 @@ __device__ __forceinline__ void stream_combine(const DecodeArgs& a, int t, int c
     __syncthreads();
 }
 
+// Wide-mode combine of token t, output columns c0 .. c0 + ncol: first every
+// (slot jj, column quad) -- slot j < K the routed pick j, K + v shared group v
+// -- sums its partial rows over the slices in order (row rows[jj] of
+// [row][slice], agent-coherent reads, two tasks per thread with all their
+// loads in flight) into ys [K + V][ncol]; then out = sum_j w_j * ys[j] in j
+// order + (ys[K] + ys[K + 1] + ...) (+ shared_y) (+ the residual).
+template <int NS>
+__device__ __forceinline__ void stream_combine_wide(const DecodeArgs& a, int t, int c0, int ncol, const float* wts_t,
+                                                    const int* rows, bool bad, float* ys) {
+    const int tid = threadIdx.x;
+    const int V = a.n_virtual, K = a.top_k, H = a.hidden;
+    const int nq = ncol >> 2, ntask = (K + V) * nq;
+    for (int k0 = tid; k0 < ntask; k0 += 2 * kStreamThreads) {
+        const int k1 = min(k0 + kStreamThreads, ntask - 1);  // (a repeat of the last task when past the end)
+        const int j0 = k0 / nq, q0 = k0 - j0 * nq, j1 = k1 / nq, q1 = k1 - j1 * nq;
+        const size_t o0 = ((size_t)rows[j0] * NS * H + c0 + 4 * q0) * 4, o1 = ((size_t)rows[j1] * NS * H + c0 + 4 * q1) * 4;
+        f32x4 v0[NS], v1[NS];
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            v0[s] = load16_cg(a.y, o0 + (size_t)s * H * 4);
+            v1[s] = load16_cg(a.y, o1 + (size_t)s * H * 4);
+        }
+        f32x4 y0 = {0.f, 0.f, 0.f, 0.f}, y1 = y0;
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                y0[i] += v0[s][i];
+                y1[i] += v1[s][i];
+            }
+        *reinterpret_cast<f32x4*>(ys + (size_t)j0 * ncol + 4 * q0) = y0;
+        *reinterpret_cast<f32x4*>(ys + (size_t)j1 * ncol + 4 * q1) = y1;
+    }
+    __syncthreads();
+    for (int q = tid; q < nq; q += kStreamThreads) {
+        const int c = c0 + 4 * q;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < K; ++j) {
+            const float w = wts_t[j];
+            const f32x4 y = *reinterpret_cast<const f32x4*>(ys + (size_t)j * ncol + 4 * q);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = fmaf(w, y[i], acc[i]);
+        }
+        if (V > 0) {
+            f32x4 sh = *reinterpret_cast<const f32x4*>(ys + (size_t)K * ncol + 4 * q);
+            for (int v = 1; v < V; ++v) {
+                const f32x4 y = *reinterpret_cast<const f32x4*>(ys + (size_t)(K + v) * ncol + 4 * q);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sh[i] += y[i];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] += sh[i];
+        }
+        if (a.shared_y) {
+            const f32x4 sv = *reinterpret_cast<const f32x4*>(a.shared_y + (size_t)t * H + c);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] += sv[i];
+        }
+        if (a.rms_weight) {  // the residual (f32 input)
+            const f32x4 rv = *reinterpret_cast<const f32x4*>(static_cast<const float*>(a.x) + (size_t)t * H + c);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = rv[i] + acc[i];
+        }
+        if (bad) acc = f32x4{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")};
+        *reinterpret_cast<f32x4*>(a.out + (size_t)t * H + c) = acc;
+    }
+    __syncthreads();
+}
+
 // One item of a worker: expert group g, slice s, and in wide mode the
 // 16-token block tb of the group's tokens (n of them, partial rows row0 ..);
 // wi = g * NS + s indexes the weights; tok: the token of the lane's row
@@ -313,7 +380,6 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
     int* misc = tokmask + kMaxExperts;
     // wide mode tables
     uint64_t* masks = reinterpret_cast<uint64_t*>(smem + Lay::o_mask);  // [token] picked experts
-    int* idsL = reinterpret_cast<int*>(smem + Lay::o_ids);               // [token][K]
     int* cntL = reinterpret_cast<int*>(smem + Lay::o_tab);               // [group] tokens
     int* baseL = cntL + kMaxExperts;                                     // [group] first partial row
     int* nbL = baseL + kMaxExperts;                                      // [group] 16-token blocks
@@ -334,6 +400,9 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
 
     const int S = load_cg(prog + b);
     const unsigned rtag = (((unsigned)S >> 12) + 1u) & 0xFFFFFFu;
+    // wide mode: this call's item tickets; the other counter is cleared for the next call
+    unsigned long long* queue = sy->queue + (((unsigned)S >> 12) & 1u);
+    if (WIDE && b == 0 && tid == 0) store_cg(sy->queue + ((((unsigned)S >> 12) & 1u) ^ 1u), 0ull);
     int k = 0;  // steps published by this workgroup
     auto publish_now = [&]() {
         __syncthreads();
@@ -436,8 +505,10 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
             }
         }
         __syncthreads();
-        NTOT = ntotL[0];
-        return ntotL[1];
+        // (readfirstlane: values read from LDS look divergent to the compiler, and a
+        // loop bound on them made it place wave-uniform values in vector registers)
+        NTOT = __builtin_amdgcn_readfirstlane(ntotL[0]);
+        return __builtin_amdgcn_readfirstlane(ntotL[1]);
     };
     auto wide_setup = [&]() {
         if (wave == 0) {
@@ -459,8 +530,7 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
         }
         __syncthreads();
         fence_wg_acquire();  // the expert input rows published with the words
-        // (readfirstlane: the branch is uniform, which the compiler cannot see through LDS)
-        if (__builtin_amdgcn_readfirstlane(wide_tables()) > T * kStreamCandRows) {
+        if (wide_tables() > T * kStreamCandRows) {
             // the exact picks (all routers done)
             if (wave == 0) {
                 int it = 0;
@@ -638,17 +708,39 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
         }
     };
 
-    if (b >= T && (WIDE || b - T < NI)) {
+    // Wide mode: the routers join the workers once their routing is done.
+    // Worker w's first item is item w; every further item (routers: every
+    // item) comes from a ticket of the call's counter, drawn one item ahead:
+    // workers take items PW, PW + 1, ... from the front, routers (late) take
+    // them from the end, NTOT - 1, NTOT - 2, ... A ticket is the counter
+    // before the draw (front draws in the low half, end draws in the high
+    // half), so the two sides never take the same item.
+    int* tkL = ntotL + 2;          // a drawn item, shared through LDS
+    unsigned long long tkn = 0;    // thread 0: the ticket drawn during the current item
+    const unsigned long long tk_step = b < T ? (1ull << 32) : 1ull;
+    auto draw = [&]() { return __hip_atomic_fetch_add(queue, tk_step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    auto tk_item = [&](unsigned long long tk) -> int {  // (after wide_setup: NTOT)
+        const int lo = (int)(uint32_t)tk, hi = (int)(tk >> 32);
+        if (lo + hi >= NTOT - PW) return NTOT;
+        return b < T ? NTOT - 1 - hi : PW + lo;
+    };
+    if (WIDE || (b >= T && b - T < NI)) {
         const int w = b - T;
         StreamItem first_item;
+        int i0 = w;  // the first item
         if constexpr (WIDE) {
             // weights first (block 0 items exist whatever the routing), then
             // the routing, then this item's token rows
-            if (w < NI) prefetch(w);
+            if (b >= T && w < NI) prefetch(w);
+            unsigned long long tk0 = 0;
+            if (tid == 0 && b < T) tk0 = draw();  // a router's first item
             wide_setup();
-            if (w < NTOT) {
-                first_item = witem(w);
-                if (w >= NI) prefetch(first_item.wi);
+            if (tid == 0) tkL[0] = tk_item(tk0);
+            __syncthreads();
+            i0 = __builtin_amdgcn_readfirstlane(b >= T ? w : tkL[0]);
+            if (i0 < NTOT) {
+                first_item = witem(i0);
+                if (b < T || i0 >= NI) prefetch(first_item.wi);
                 x_rows(first_item.tok);
             }
         } else {
@@ -662,7 +754,7 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
             prefetch(w);
             first_item = sitem(w);
         }
-      if (w < NTOT) {
+      if (i0 < NTOT) {
 
         // candidates: wave 0 requests the tagged words here, ahead of their
         // use in the first item's down phase, so waiting for them is part of
@@ -707,12 +799,15 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
         // One item; MORE: a next item exists (its weights stream under this
         // item's work). The last item is a separate copy, so that the
         // compiler's own counter waits see one fixed issue order.
-        auto item = [&](int i, const StreamItem& cur, StreamItem& nxt, bool first, auto more_tag) {
-            constexpr bool MORE = decltype(more_tag)::value;
+        // item i (list position) with nx after it and pi before it (-1: none)
+        // The first half of an item: up to its gate/up MMA (wide mode: thread 0
+        // draws the ticket of the next item at the start and shares it before
+        // the closing barrier). The gate/up phase takes ring units of this
+        // item only (kRing <= NTD).
+        static_assert(kRing <= NTD, "the gate/up phase stays within its item's units");
+        auto item_a = [&](const StreamItem& cur, bool first, f32x4& acc0, f32x4& acc1) {
             fresh_indices();
-            const int g = cur.g, s = cur.s, wi = cur.wi;
-            const int nx = i + PW;
-            int wnx = WIDE ? 0 : nx;  // the next item's weight index (wide: known from the down phase on)
+            const int wi = cur.wi;
             // this item's gate/up scales (and, first item, the token rows and
             // down scales): older than the last kRing ops (first item: the
             // ring's loads) or 2 * NTD ops (later items: the previous down
@@ -729,6 +824,8 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
             }
             if constexpr (WIDE) {
                 lds_barrier();  // every wave's token-row DMA has landed
+                // (its counter wait, the compiler's, lets this phase's 2 * KTG unit loads run on)
+                if (tid == 0) tkn = draw();
             } else if (first) {
                 // this wave's DMA'd rows -> f16 in place
                 for (int kt = wave >> 2; kt < KTG; kt += 2) {
@@ -748,21 +845,37 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
             // gate/up of the wave's 16 rows -> act (f16) into Ad in the down
             // A layout (inter column kl = 16 * wave + r of the slice); each
             // consumed k-tile's registers take the next item's k-tile
+            acc0 = f32x4{0.f, 0.f, 0.f, 0.f};
+            acc1 = acc0;
+            item_mma_f<GPT, KTG, true, ZP, Lay::ZOFF_G, !ZP, false>(
+                [&](int kt) -> const u32x4& { return ring[(2 * kt) % kRing]; },
+                [&](int kt) -> const u32x4& { return ring[(2 * kt + 1) % kRing]; }, lds_addr(As + (size_t)lane * 8),
+                lds_addr(ssw + r * NGG), lds_addr(ssw + Lay::SRM + r * NGG), 0u,
+                acc0, acc1, [&](int kt) {
+                    advance(wi, 2 * kt, 0, false);
+                    advance(wi, 2 * kt + 1, 0, false);
+                });
+            if constexpr (WIDE) {
+                if (tid == 0) lds_write_u32(tkL, tk_item(tkn));
+                // every wave is past this item's gate/up (As reads) and the
+                // previous item's down (Ad reads); the next item is known
+                lds_barrier();
+            }
+        };
+        // The second half: act, the next item's scales and token rows, the
+        // down phase. MORE: a next item nx exists.
+        auto item_b = [&](int i, int nx, int pi, const StreamItem& cur, StreamItem& nxt, bool first, const f32x4& acc0,
+                          const f32x4& acc1, auto more_tag) {
+            constexpr bool MORE = decltype(more_tag)::value;
+            fresh_indices();
+            const int g = cur.g, s = cur.s, wi = cur.wi;
+            int wnx = WIDE ? 0 : nx;  // the next item's weight index
+            (void)i;
             {
-                f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-                item_mma_f<GPT, KTG, true, ZP, Lay::ZOFF_G, !ZP, false>(
-                    [&](int kt) -> const u32x4& { return ring[(2 * kt) % kRing]; },
-                    [&](int kt) -> const u32x4& { return ring[(2 * kt + 1) % kRing]; }, lds_addr(As + (size_t)lane * 8),
-                    lds_addr(ssw + r * NGG), lds_addr(ssw + Lay::SRM + r * NGG), 0u,
-                    acc0, acc1, [&](int kt) {
-                        advance(wi, 2 * kt, wnx, MORE);
-                        advance(wi, 2 * kt + 1, wnx, MORE);
-                    });
                 const int kl = 16 * wave + r;
                 const int sp = kl >> 5, cp = (kl & 31) >> 3, ip = kl & 7;
-                // every wave is past the previous item's down (Ad reads) and,
-                // wide mode, this item's gate/up (As reads)
-                if (WIDE || !first) lds_barrier();
+                // every wave is past the previous item's down (Ad reads)
+                if (!WIDE && !first) lds_barrier();
                 if constexpr (WIDE && MORE) {
                     nxt = witem(nx);
                     wnx = nxt.wi;
@@ -792,8 +905,13 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
             if (!WIDE && first) cand_resolve();
             lds_barrier();  // Ad, cm32 / tokmask complete; every wave's older stores done
             if (!first) {
-                ++k;  // the previous item
-                if (tid == 0) store_sc1(prog + b, S + k);  // (no fence: the counter waits ordered the stores)
+                // the previous item (no fence: the counter waits ordered its stores)
+                if constexpr (WIDE) {
+                    if (tid == 0) store_sc1(reinterpret_cast<int*>(sy->item_done + pi), (int)rtag);
+                } else {
+                    ++k;
+                    if (tid == 0) store_sc1(prog + b, S + k);
+                }
             }
             have_cand = true;
             const int tm = WIDE ? 0 : (g < E ? (int)lds_read_u32(tokmask + g) : (int)((1u << T) - 1u));
@@ -837,27 +955,51 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
             if constexpr (MORE) dn_scales(wnx);
             asm volatile("" ::: "memory");
         };
-        int i = w;
+        int i = i0;
         StreamItem cur = first_item, nxt = first_item;
-        for (; i + PW < NTOT; i += PW) {
-            item(i, cur, nxt, i == w, std::true_type{});
-            cur = WIDE ? nxt : sitem(i + PW);
+        f32x4 acc0, acc1;
+        if constexpr (WIDE) {
+            int pi = -1;
+            bool first = true;
+            while (true) {
+                item_a(cur, first, acc0, acc1);
+                const int nx = __builtin_amdgcn_readfirstlane((int)lds_read_u32(tkL));  // (uniform: see NTOT)
+                if (nx >= NTOT) break;
+                item_b(i, nx, pi, cur, nxt, first, acc0, acc1, std::true_type{});
+                pi = i;
+                i = nx;
+                cur = nxt;
+                first = false;
+            }
+            item_b(i, NTOT, pi, cur, nxt, first, acc0, acc1, std::false_type{});
+        } else {
+            for (; i + PW < NTOT; i += PW) {
+                item_a(cur, i == i0, acc0, acc1);
+                item_b(i, i + PW, i - PW, cur, nxt, i == i0, acc0, acc1, std::true_type{});
+                cur = sitem(i + PW);
+            }
+            item_a(cur, i == i0, acc0, acc1);
+            item_b(i, i + PW, i - PW, cur, nxt, i == i0, acc0, acc1, std::false_type{});
         }
-        item(i, cur, nxt, i == w, std::false_type{});
         report_f16_overflow(a.status, ovf);
         // the last item: its stores, then the step
         store_fence();
         publish_now();
+        if (WIDE && tid == 0) store_sc1(reinterpret_cast<int*>(sy->item_done + i), (int)rtag);
       }
     }
 
     // ---- 3. combine units (token t, column block cb), one per workgroup from
     // the grid's end; the routers are the last to get one
+    // (wide mode: CPU column blocks per unit, so that every workgroup has one
+    // unit where the LDS for the unit's sums allows)
     const int NCB = (H + 127) / 128;
-    const int n_units = T * NCB;
+    const int CPU = WIDE ? max(1, min((NCB * T + P - 1) / P, (int)(Lay::as_bytes / (512 * (K + V))))) : 1;
+    const int UPT = (NCB + CPU - 1) / CPU;  // units per token
+    const int n_units = T * UPT;
     for (int u = P - 1 - b; u < n_units; u += P) {
         fresh_indices();
-        const int t = u / NCB, cb = u % NCB;
+        const int t = u / UPT, cb = u % UPT;
         int* ids_c = misc;                                   // [K]
         float* wts_c = reinterpret_cast<float*>(misc + kMaxTopK);
         float* ys = reinterpret_cast<float*>(smem + Lay::o_ad);  // (K + 1) x 128 floats (Ad, Ds)
@@ -898,15 +1040,27 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
             __syncthreads();
             bad = misc[2 * kMaxTopK] != 0;
             const int* ib = cuL + kMaxTopK + kMaxExperts;
-            wait_steps(
-                [&](int q, int& owner, int& step) {
-                    const int i = ib[q / NS] + q % NS;
-                    owner = T + i % PW;
-                    step = i / PW + 1;
-                },
-                (K + V) * NS);
+            if (wave == 0) {
+                const int nq = (K + V) * NS;
+                for (int q0 = 0; q0 < nq; q0 += 64) {
+                    const int q = q0 + lane;
+                    const bool want = q < nq;
+                    const int i = want ? ib[q / NS] + q % NS : 0;
+                    int it = 0;
+                    while (__ballot(want && load_cg(sy->item_done + i) != rtag)) {
+                        if (++it > kSpinLimit) {
+                            if (lane == 0) report_timeout_to(a.status, sy, rtag);
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(1);
+                    }
+                }
+            }
+            __syncthreads();
+            fence_wg_acquire();
             bad |= load_cg(&sy->call_fault) == rtag;
-            stream_combine<NS>(a, t, cb, ids_c, wts_c, cuL, bad, ys);
+            const int c0 = cb * CPU * 128;
+            stream_combine_wide<NS>(a, t, c0, min(H - c0, CPU * 128), wts_c, cuL, bad, reinterpret_cast<float*>(smem));
             continue;
         }
         need_cand();

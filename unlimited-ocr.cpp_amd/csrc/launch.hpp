@@ -122,6 +122,7 @@ constexpr int kStreamWideMaxSeq = 64;  // its wide mode (any input, RMSNorm prol
 // wide mode: partial rows per token for the routed candidates (more candidates:
 // the kernel takes the exact picks instead; >= kMaxTopK)
 constexpr int kStreamCandRows = 10;
+constexpr int kStreamMaxItems = 4096;  // wide mode items per call (at most 896 + 296 * 7 at 64 tokens)
 struct FusedSync {
     int progress[kFusedMaxGrid];
     int error;  // sticky: bit 0 a bounded wait timed out, bit 1 an exact pick outside the candidates
@@ -135,6 +136,12 @@ struct FusedSync {
     // one workgroup per expert, as (tag << 32) | float bits: [t][e][2] =
     // estimate, sum of |x w|
     unsigned long long est[kFusedEstMaxSeq * 64 * 2];
+    // streamed kernel, wide mode: the item tickets of calls of even / odd
+    // base (a call clears the other one; low half: drawn from the front of
+    // the list, high half: from its end), and per item the tag of the last
+    // call whose partial rows of it are stored
+    unsigned long long queue[2];
+    unsigned item_done[kStreamMaxItems];
 };
 
 // Decode-sized layer (seq < 256): router_decode / expert passes / combine with
