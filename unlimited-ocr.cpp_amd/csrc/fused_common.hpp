@@ -174,10 +174,16 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
     const float* xf = static_cast<const float*>(a.x) + (size_t)t * H;
     const bool xbf = !PREP || a.x_bf16;
     uint32_t xb[NXT];  // bf16 bits, or (PREP, f32 x) the float's bits
+    float rw[NXT];     // PREP + RMSNorm: the weights of the thread's columns
 #pragma unroll
     for (int i = 0; i < NXT; ++i) {
         const int c = tid + 64 * NW * i;
-        xb[i] = c < H ? (xbf ? (uint32_t)x[c] : __float_as_uint(xf[c])) : 0u;
+        if (!PREP || a.x_bf16) {
+            xb[i] = c < H ? (uint32_t)x[c] : 0u;
+        } else {
+            xb[i] = c < H ? __float_as_uint(xf[c]) : 0u;
+        }
+        rw[i] = PREP && a.rms_weight && c < H ? a.rms_weight[c] : 0.0f;
     }
     const uint16_t* wbase = a.router_t + ((size_t)wave * NL * E + e) * 8;
     u32x4 wr[NL];
@@ -197,10 +203,14 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
         const float* xin = xs;
         if (rms) {
             float ps = 0.0f;
-            for (int c = tid; c < H; c += 64 * NW) {
-                const float q = __fmul_rn(xs[c], xs[c]);
-                pq[c] = q;
-                ps += q;
+#pragma unroll
+            for (int i = 0; i < NXT; ++i) {
+                const int c = tid + 64 * NW * i;
+                if (c < H) {
+                    const float q = __fmul_rn(xs[c], xs[c]);
+                    pq[c] = q;
+                    ps += q;
+                }
             }
 #pragma unroll
             for (int o = 32; o > 0; o >>= 1) ps += __shfl_xor(ps, o, 64);
@@ -210,7 +220,11 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
 #pragma unroll
             for (int w = 0; w < NW; ++w) ssa += hand[w];
             const float inv_a = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ssa, (float)H), a.rms_eps)));
-            for (int c = tid; c < H; c += 64 * NW) xe[c] = __fmul_rn(__fmul_rn(xs[c], inv_a), a.rms_weight[c]);
+#pragma unroll
+            for (int i = 0; i < NXT; ++i) {
+                const int c = tid + 64 * NW * i;
+                if (c < H) xe[c] = __fmul_rn(__fmul_rn(xs[c], inv_a), rw[i]);
+            }
             __syncthreads();
             xin = xe;
         }
@@ -288,7 +302,11 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
             }
             __syncthreads();
             const float inv = sc[0];
-            for (int c = tid; c < H; c += 64 * NW) xs[c] = __fmul_rn(__fmul_rn(xs[c], inv), a.rms_weight[c]);
+#pragma unroll
+            for (int i = 0; i < NXT; ++i) {
+                const int c = tid + 64 * NW * i;
+                if (c < H) xs[c] = __fmul_rn(__fmul_rn(xs[c], inv), rw[i]);
+            }
             __syncthreads();
         }
     }
