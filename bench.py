@@ -199,6 +199,15 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False, fmt="int4"):
         tb = sum(layer_bytes(L, c, seq)["total"] for L, c in zip(layers_np, counts))
         res.update(tokens_per_s=seq / (ms * 1e-3), layers=len(layers), stage_ms=stage,
                    hbm_gbs=tb / (ms * 1e-3) / 1e9, hbm_frac=tb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS)
+        if stage and "fused" in stage:
+            # one single-launch decode call per layer: its bytes are the layer's
+            kind = layers[0].decode_kernel(seq, "f32")
+            res["decode_kernel"] = kind
+            lb = tb / len(layers)
+            res["dominant"] = {"kernel": f"decode_{kind}_kernel<{128 // group}, 10, 7, false, true> (wide mode, one per layer)",
+                               "ms": stage["fused"], "bytes": lb, "gbs": lb / (stage["fused"] * 1e-3) / 1e9,
+                               "traffic_file": f"decode_{kind}_config4_traffic.md" if group == 32 and fmt == "int4" else None,
+                               "profile_file": "decode_layer_config4_kernel_stats.md" if fmt == "int4" else None}
     else:
         lb = [layer_bytes(L, c, seq) for L, c in zip(layers_np, counts)]
         avg = {k: float(np.mean([b[k] for b in lb])) for k in lb[0]}
@@ -238,11 +247,11 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False, fmt="int4"):
                 res["dominant"] = {"kernel": f"experts_prefill_big_kernel<{128 // group}, true, 10> (gate+up)",
                                    "ms": stage["gate_up"], "flops": fl_gu, "tflops": res["gate_up_tflops"],
                                    "mfma_frac": res["gate_up_mfma_frac"],
-                                   "profile_file": "experts_prefill_config3_kernel_stats.md" if cfg == 3 else None}
+                                   "profile_file": {2: "experts_prefill_config2_kernel_stats.md",
+                                                    3: "experts_prefill_config3_kernel_stats.md"}.get(cfg) if group == 32 else None}
             else:
                 res["dominant"] = {"kernel": "expert_decode_kernel<4, 10, true> (gate+up)", "ms": stage["gate_up"],
-                                   "bytes": avg["gate_up"], "gbs": res["gate_up_gbs"],
-                                   "traffic_file": "expert_gate_up_decode_config1_traffic.md"}
+                                   "bytes": avg["gate_up"], "gbs": res["gate_up_gbs"], "traffic_file": None}
     # the fused decode kernel's sticky status (bit 0: a bounded cross-workgroup
     # wait timed out, bit 1: an exact pick outside the candidates): any set bit
     # means some timed call returned NaN rows, so the measurement is void
