@@ -94,7 +94,7 @@ typedef struct {
                                    router_bf16 (the router of an AWQ-folded layer,
                                    weights.cpp:199-207, is f32). Such a layer routes
                                    with the f32-weight router kernel on every path
-                                   and never takes the fused decode kernel. */
+                                   and never takes the single-kernel decode paths. */
     /* The shared MLP unquantised, as the reference loads it (load_linear with
      * quantize = false, src/runtime/weights.cpp:289-292: BF16_EXT views of the
      * checkpoint, F32 gate/up after the AWQ fold, weights.cpp:199-207) and runs
@@ -180,7 +180,7 @@ int uocr_hip_moe_layer_forward_noalloc(const uocr_hip_moe_layer* layer, const vo
  * enabled, forward records HIP events between its stages on its stream.
  * read_timing synchronizes on the last event and returns the accumulated
  * milliseconds per stage (router, group, gate_up, down, combine, fused: the
- * single-kernel decode path, seq <= 16 with bf16 input) and the
+ * single-kernel decode paths, fused or streamed, up to 64 tokens) and the
  * number of forwards accumulated; it then resets the totals. */
 int uocr_hip_moe_layer_set_timing(uocr_hip_moe_layer* layer, int enable);
 int uocr_hip_moe_layer_read_timing(uocr_hip_moe_layer* layer, float* stage_ms, int n_stages,
