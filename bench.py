@@ -71,6 +71,7 @@ FORMATS = {
     "bf16_shared": "INT4 routed experts, bf16 shared MLP (the reference's real INT4 layer: "
                    "weights.cpp:289-292 keeps the shared MLP unquantised)",
     "bf16": "bf16 routed experts and bf16 shared MLP (the reference's default expert format, config.h:111)",
+    "f32_input": "INT4 layer as int4, hidden states passed as f32 (the engine's normed2, gpu_decoder.cu:537-560)",
 }
 
 
@@ -99,7 +100,7 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False, fmt="int4"):
     else:
         base = synth.make_config(cfg, group=group)
         bias = synth.zipf_bias() if cfg == 3 else None
-        if fmt != "int4":
+        if fmt not in ("int4", "f32_input"):
             base.layers = [make_layer(cfg, 1234 + 10 + cfg, group, fmt, bias=bias)]
         layers_np = [base.layers[0]]
         for r in range(1, replicas):
@@ -109,7 +110,8 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False, fmt="int4"):
     seq = wl.seq
     layers = [MoELayerInt4(L) for L in layers_np]
     x = torch.from_numpy(wl.x).to(dev)
-    x_in = x.float() if stack else x.to(torch.bfloat16)
+    x_f32 = stack or fmt == "f32_input"
+    x_in = x.float() if x_f32 else x.to(torch.bfloat16)
     outs = [torch.empty(seq, wl.layers[0].hidden, dtype=torch.float32, device=dev) for _ in range(2)]
     ids = [torch.empty(seq, 6, dtype=torch.int32, device=dev) for _ in layers]
     wts = [torch.empty(seq, 6, dtype=torch.float32, device=dev) for _ in layers]
@@ -222,10 +224,10 @@ def run_config(cfg, steps, warmup, replicas, group=32, graph=False, fmt="int4"):
             # gate/up pass reads every expert by design)
             fu = stage["fused"] * 1e-3
             fb = avg["total"] - avg["shared"]  # the fused launch's own bytes
-            kind = layers[0].decode_kernel(seq, "f32" if stack else "bf16")
+            kind = layers[0].decode_kernel(seq, "f32" if x_f32 else "bf16")
             gpt = 128 // group
             res["decode_kernel"] = kind
-            res["dominant"] = {"kernel": f"decode_{kind}_kernel<{gpt}, 10, 7, false> (router + experts + combine)",
+            res["dominant"] = {"kernel": f"decode_{kind}_kernel<{gpt}, 10, 7, false{', true' if kind == 'stream' and x_f32 else ''}> (router + experts + combine)",
                                "ms": stage["fused"], "bytes": fb,
                                "gbs": fb / fu / 1e9,
                                "traffic_file": f"decode_{kind}_config{cfg}_traffic.md" if fmt == "int4" else None,
@@ -542,7 +544,7 @@ def main():
     ap.add_argument("--graph", default="",
                     help="decode configs (0, 1) replayed from a hipGraph, as a decode engine runs its step; "
                          "their eager rate is reported beside it (config 4 always runs as a graph)")
-    ap.add_argument("--formats", default="1:bf16_shared,1:bf16,3:bf16",
+    ap.add_argument("--formats", default="1:bf16_shared,1:bf16,3:bf16,1:f32_input",
                     help="extra (config:format) lines; formats: " + ", ".join(FORMATS))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",

@@ -78,6 +78,18 @@ def test_wide_rmsnorm_f32(dev, group):
     layer.close()
 
 
+def test_stream_f32_input_16_token_mode(dev):
+    """f32 hidden states without RMSNorm (the engine's normed2) up to 16
+    tokens: the 16-token mode converts the rows to f16 itself; its router reads
+    the f32 row (the fused kernel takes bf16 only, so from 1 token)."""
+    from uocr_hip import MoELayerInt4, synth
+    L = synth.random_layer(6350, group=32)
+    layer = MoELayerInt4(L)
+    for seq in (1, 5, 16, 3):
+        _check(layer, L, _x(seq, L.hidden, 6350 + seq), dev, "f32", f"stream-f32-t{seq}")
+    layer.close()
+
+
 def test_wide_f32_input_no_rms(dev):
     from uocr_hip import MoELayerInt4, synth
     L = synth.random_layer(6300, group=64)

@@ -315,15 +315,18 @@ bool stream_layer_ok(const uocr_hip_moe_layer* L) {
            decode_stream_ok(L->hidden, L->inter, L->group) && L->n_experts + L->n_virtual <= kMaxExperts;
 }
 bool stream_wide(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
-    return seq > kStreamMaxSeq || x_dtype != UOCR_HIP_DTYPE_BF16 || L->rms_weight;
+    (void)x_dtype;
+    return seq > kStreamMaxSeq || L->rms_weight;
 }
 bool use_stream(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
     if (L->decode_kernel == UOCR_HIP_DECODE_FOUR_LAUNCH || L->decode_kernel == UOCR_HIP_DECODE_FUSED) return false;
     if (!stream_layer_ok(L) || seq < 1) return false;
-    // wide mode: an unquantised shared MLP would need the normalised input
-    // before the launch
-    if (stream_wide(L, seq, x_dtype)) return seq <= kStreamWideMaxSeq && !L->shared_dense;
-    const int lo = L->decode_kernel == UOCR_HIP_DECODE_STREAM ? 1 : kStreamMinSeq;
+    // an unquantised shared MLP runs before the launch, on the bf16 input as
+    // the experts see it (no RMSNorm)
+    if (L->shared_dense && (x_dtype != UOCR_HIP_DTYPE_BF16 || L->rms_weight)) return false;
+    if (stream_wide(L, seq, x_dtype)) return seq <= kStreamWideMaxSeq;
+    // (below kStreamMinSeq the fused kernel is faster, for bf16 input)
+    const int lo = L->decode_kernel == UOCR_HIP_DECODE_STREAM || x_dtype != UOCR_HIP_DTYPE_BF16 ? 1 : kStreamMinSeq;
     return seq >= lo && seq <= kStreamMaxSeq;
 }
 

@@ -744,14 +744,45 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
                 x_rows(first_item.tok);
             }
         } else {
-            // the token rows (all T, once): bf16 DMA, then f16 in place. Wave
-            // w stages MFMA step w & 3 of k-tiles w >> 2, (w >> 2) + 2, ...
-            if (r < T) {
-                const uint16_t* src = xb + (size_t)r * H + (wave & 3) * 32 + 8 * (lane >> 4);
-                for (int kt = wave >> 2; kt < KTG; kt += 2) dma16(src + kt * kTileK, As + (size_t)(kt * 4 + (wave & 3)) * 64 * 8);
+            // the token rows (all T, once): bf16 DMA, then f16 in place; f32
+            // input: into registers, f16 into As at the first item. Wave w
+            // stages MFMA step w & 3 of k-tiles w >> 2, (w >> 2) + 2, ...
+            if (a.x_bf16) {
+                if (r < T) {
+                    const uint16_t* src = xb + (size_t)r * H + (wave & 3) * 32 + 8 * (lane >> 4);
+                    for (int kt = wave >> 2; kt < KTG; kt += 2)
+                        dma16(src + kt * kTileK, As + (size_t)(kt * 4 + (wave & 3)) * 64 * 8);
+                }
             }
             // issue order = the order the explicit counter waits assume
             prefetch(w);
+            if (!a.x_bf16) {
+                // f32 input: this wave's rows -> f16 into As, behind the
+                // prefetch (the compiler's wait for them covers it too)
+                constexpr int NKX = (KTG + 1) / 2;
+                f32x4 xf[NKX][2];
+                const float* src = static_cast<const float*>(a.x) + (size_t)min(r, T - 1) * H + (wave & 3) * 32 + 8 * (lane >> 4);
+#pragma unroll
+                for (int q = 0; q < NKX; ++q) {
+                    const int kt = (wave >> 2) + 2 * q;
+                    if (kt < KTG) {
+                        xf[q][0] = *reinterpret_cast<const f32x4*>(src + kt * kTileK);
+                        xf[q][1] = *reinterpret_cast<const f32x4*>(src + kt * kTileK + 4);
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < NKX; ++q) {
+                    const int kt = (wave >> 2) + 2 * q;
+                    if (kt < KTG) {
+                        const f16x8 h = {(f16)xf[q][0][0], (f16)xf[q][0][1], (f16)xf[q][0][2], (f16)xf[q][0][3],
+                                         (f16)xf[q][1][0], (f16)xf[q][1][1], (f16)xf[q][1][2], (f16)xf[q][1][3]};
+                        asm volatile("ds_write_b128 %0, %1" ::"v"(lds_addr(As + (size_t)(kt * 4 + (wave & 3)) * 64 * 8 +
+                                                                          (size_t)lane * 8)),
+                                     "v"(h)
+                                     : "memory");
+                    }
+                }
+            }
             first_item = sitem(w);
         }
       if (i0 < NTOT) {
@@ -826,6 +857,8 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
                 lds_barrier();  // every wave's token-row DMA has landed
                 // (its counter wait, the compiler's, lets this phase's 2 * KTG unit loads run on)
                 if (tid == 0) tkn = draw();
+            } else if (first && !a.x_bf16) {
+                lds_barrier();  // (f32 input: the rows went to As in the prologue)
             } else if (first) {
                 // this wave's DMA'd rows -> f16 in place
                 for (int kt = wave >> 2; kt < KTG; kt += 2) {
@@ -1125,7 +1158,7 @@ bool decode_stream_ok(int hidden, int inter, int group) {
     return hidden == 1280 && inter == 896 && (group == 32 || group == 64 || group == 128);
 }
 
-bool decode_stream_wide(const DecodeArgs& a) { return a.seq > kStreamMaxSeq || !a.x_bf16 || a.rms_weight; }
+bool decode_stream_wide(const DecodeArgs& a) { return a.seq > kStreamMaxSeq || a.rms_weight; }
 
 template <bool WIDE>
 static hipError_t launch_stream_g(const DecodeArgs& a, hipStream_t st) {

@@ -172,13 +172,13 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
     __builtin_amdgcn_s_setprio(3);
     const uint16_t* x = static_cast<const uint16_t*>(a.x) + (size_t)t * H;
     const float* xf = static_cast<const float*>(a.x) + (size_t)t * H;
-    const bool xbf = !PREP || a.x_bf16;
-    uint32_t xb[NXT];  // bf16 bits, or (PREP, f32 x) the float's bits
+    const bool xbf = a.x_bf16;
+    uint32_t xb[NXT];  // bf16 bits, or (f32 x) the float's bits
     float rw[NXT];     // PREP + RMSNorm: the weights of the thread's columns
 #pragma unroll
     for (int i = 0; i < NXT; ++i) {
         const int c = tid + 64 * NW * i;
-        if (!PREP || a.x_bf16) {
+        if (a.x_bf16) {
             xb[i] = c < H ? (uint32_t)x[c] : 0u;
         } else {
             xb[i] = c < H ? __float_as_uint(xf[c]) : 0u;
