@@ -164,3 +164,18 @@ def test_wide_graph_replay(dev):
         _forward(layer, x_np, dev, "f32")
     assert layer.status() == 0
     layer.close()
+
+
+@pytest.mark.parametrize("group", [32, 128])
+def test_wide_reference_quantizers_rmsnorm(dev, group):
+    """Wide mode on a layer from the reference's AWQ quantizer (zeros in
+    [0, 15], arbitrary f32 scales): the zero offsets of the down projection
+    come from the k-tile-ordered copy; with the RMSNorm prologue and f32 input."""
+    from helpers import awq_layer
+    from uocr_hip import MoELayerInt4
+    L = awq_layer(6700 + group, group=group)
+    L.rms_weight = np.random.default_rng(6701).uniform(0.5, 2.0, L.hidden).astype(np.float32)
+    layer = MoELayerInt4(L)
+    for seq in (40, 64, 7):
+        _check(layer, L, _x(seq, L.hidden, 6700 + seq), dev, "f32", f"wide-awq-rms-g{group}-t{seq}")
+    layer.close()
