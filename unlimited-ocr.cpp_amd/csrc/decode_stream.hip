@@ -1,39 +1,50 @@
-// Streamed decode layer (up to kStreamMaxSeq tokens, bf16 input): router,
-// gate/up, down and combine in ONE persistent launch of one 8-wave workgroup
-// per CU, organised so that the weight stream never waits on another
-// workgroup.
+// Streamed decode layer: router, gate/up, down and combine in ONE persistent
+// launch of one 8-wave workgroup per CU (two where the registers and LDS
+// allow), organised so that the weight stream never waits on another
+// workgroup. Two modes:
+//   16-token mode (WIDE = false): up to kStreamMaxSeq tokens, bf16 or f32
+//     input, no RMSNorm; every item covers all T tokens;
+//   wide mode (WIDE = true): up to kStreamWideMaxSeq tokens, any input, the
+//     RMSNorm prologue and the residual; an item covers one 16-token block of
+//     its group's candidate tokens.
 //
 // The work unit is an ITEM (group g, slice s): 128 inter rows of one expert
 // group (a routed expert, or one of the shared MLP's virtual groups). One
-// workgroup computes, for all T tokens,
+// workgroup computes, for its tokens,
 //   act[t, s*128 .. s*128+127] = silu(gate_rows . x_t) * (up_rows . x_t)
 // and right away the down projection restricted to those 128 inter columns,
-//   part[g][s][t][0 .. H) = down[:, s*128 .. s*128+127] . act[t, slice]
+//   part[.][s][t][0 .. H) = down[:, s*128 .. s*128+127] . act[t, slice]
 // (the split-K partial of the expert's output; src/engine/moe_decoder.cpp:62-74
 // sums over all inter columns, here the partials of the slices are added in
 // slice order by the combine). Gate/up rows and the matching down columns
 // stream in together; nothing waits for another item. Routing is needed only
-// (1) to know which tokens' partial rows to store -- the candidate experts
-// that the routers publish before their exact chains -- and (2) by the
-// combine.
+// (1) to know which tokens' partial rows to store (wide mode: which tokens an
+// item computes) -- the candidate experts that the routers publish before
+// their exact chains -- and (2) by the combine.
 //
 //   workgroups [0, T)   the router of token t (candidates, then the exact
-//                       chain, scores and top_k)
-//   workgroups [T, P)   items i = w, w + PW, ... (w = b - T), group-major;
-//                       each worker issues the next item's gate/up weights
-//                       while it computes the current item's down partial
-//   combine units       (token t, 128 output columns), one per workgroup from
-//                       the last one down: after the router of t and the items
-//                       of t's picked groups and the shared groups,
+//                       chain, scores and top_k); wide mode: afterwards they
+//                       take items from the end of the item list
+//   workgroups [T, P)   16-token mode: items i = w, w + PW, ... (w = b - T),
+//                       group-major; wide mode: item w, then items drawn from
+//                       a per-call ticket counter. Each worker issues the
+//                       next item's weights while it computes the current
+//                       item's down partial
+//   combine units       16-token mode: (token t, 128 output columns); wide
+//                       mode: (token t, several column blocks), one per
+//                       workgroup from the last one down: after the exact
+//                       routing of t and the items of t's picks and of the
+//                       shared groups,
 //                       out[t] = sum_j w[t,j] * sum_s part[id_j][s][t]
 //                              + sum_v sum_s part[E+v][s][t] (+ shared_y)
+//                              (+ the residual)
 //                       in the reference's j order (moe_decoder.cpp:88-97,
-//                       110-112).
+//                       110-112, 179).
 //
-// Cross-workgroup data goes through agent-coherent accesses and per-workgroup
-// progress words with bounded waits (fused_common.hpp), the protocol of the
-// fused decode kernel: a workgroup publishes S + steps, every word ends the
-// call at S + kFusedSteps.
+// Cross-workgroup data goes through agent-coherent accesses with bounded
+// waits (fused_common.hpp): per-workgroup progress words (a workgroup
+// publishes S + steps, every word ends the call at S + kFusedSteps), tagged
+// candidate words and, in wide mode, tagged per-item completion words.
 #include <hip/hip_runtime.h>
 #include "fused_common.hpp"
 
