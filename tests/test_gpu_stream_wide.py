@@ -78,16 +78,34 @@ def test_wide_rmsnorm_f32(dev, group):
     layer.close()
 
 
-def test_stream_f32_input_16_token_mode(dev):
+@pytest.mark.parametrize("kind", ["fused", "stream"])
+def test_single_kernel_f32_input(dev, kind):
     """f32 hidden states without RMSNorm (the engine's normed2) up to 16
-    tokens: the 16-token mode converts the rows to f16 itself; its router reads
-    the f32 row (the fused kernel takes bf16 only, so from 1 token)."""
+    tokens on both single-kernel decode paths: the routers read the f32 rows
+    and the workers convert them to f16 themselves (the default choice takes
+    the fused kernel below 6 tokens, the streamed one from 6)."""
     from uocr_hip import MoELayerInt4, synth
     L = synth.random_layer(6350, group=32)
     layer = MoELayerInt4(L)
+    layer.set_decode_kernel(kind)
     for seq in (1, 5, 16, 3):
-        _check(layer, L, _x(seq, L.hidden, 6350 + seq), dev, "f32", f"stream-f32-t{seq}")
+        x = _x(seq, L.hidden, 6350 + seq)
+        got = layer.decode_kernel(seq, "f32")
+        assert got == kind, f"f32 t{seq}: decode kernel {got}"
+        import oracle as O
+        print(f"[wide] {kind}-f32-t{seq}", flush=True)
+        ids, w, out = _forward(layer, x, dev, "f32")
+        ids_o, w_o, out_o = O.moe_layer(L, x, threads=16)
+        assert np.array_equal(ids, ids_o), f"{kind}-f32-t{seq}: routing ids"
+        assert np.array_equal(w.view(np.uint32), w_o.view(np.uint32)), f"{kind}-f32-t{seq}: routing weights"
+        r, m = rel_l2(out, out_o), max_abs(out, out_o)
+        print(f"[wide] {kind}-f32-t{seq}: rel_l2={r:.3e} max_abs={m:.3e}", flush=True)
+        assert r <= REL_L2_TOL and m <= MAX_ABS_TOL
+    assert layer.status() == 0
     layer.close()
+    auto = MoELayerInt4(L)
+    assert auto.decode_kernel(3, "f32") == "fused" and auto.decode_kernel(8, "f32") == "stream"
+    auto.close()
 
 
 def test_wide_f32_input_no_rms(dev):

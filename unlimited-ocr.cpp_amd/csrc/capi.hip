@@ -298,8 +298,9 @@ constexpr int kFusedMinSeq = 1;
 
 bool use_fused(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
     if (L->decode_kernel == UOCR_HIP_DECODE_FOUR_LAUNCH || L->decode_kernel == UOCR_HIP_DECODE_STREAM) return false;
-    return L->sync && !L->experts_dense && L->router_t && seq >= kFusedMinSeq && seq <= kFusedMaxSeq && x_dtype == UOCR_HIP_DTYPE_BF16 &&
-           !L->rms_weight &&
+    // (an unquantised shared MLP runs before the launch, on bf16 input only)
+    return L->sync && !L->experts_dense && L->router_t && seq >= kFusedMinSeq && seq <= kFusedMaxSeq &&
+           (x_dtype == UOCR_HIP_DTYPE_BF16 || !L->shared_dense) && !L->rms_weight &&
            decode_fused_ok(L->hidden, L->inter, L->group) && L->n_experts + L->n_virtual <= kMaxExperts;
 }
 
@@ -326,7 +327,7 @@ bool use_stream(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
     if (L->shared_dense && (x_dtype != UOCR_HIP_DTYPE_BF16 || L->rms_weight)) return false;
     if (stream_wide(L, seq, x_dtype)) return seq <= kStreamWideMaxSeq;
     // (below kStreamMinSeq the fused kernel is faster, for bf16 input)
-    const int lo = L->decode_kernel == UOCR_HIP_DECODE_STREAM || x_dtype != UOCR_HIP_DTYPE_BF16 ? 1 : kStreamMinSeq;
+    const int lo = L->decode_kernel == UOCR_HIP_DECODE_STREAM ? 1 : kStreamMinSeq;
     return seq >= lo && seq <= kStreamMaxSeq;
 }
 

@@ -82,13 +82,30 @@ __device__ __forceinline__ void estimate_expert(const DecodeArgs& a, int e, unsi
             w[2 * i + 1] = __uint_as_float(wv[i] & 0xffff0000u);
         }
         const uint16_t* xb = static_cast<const uint16_t*>(a.x);
+        const float* xf = static_cast<const float*>(a.x);
 #pragma unroll
         for (int t = 0; t < kFusedEstMaxSeq; ++t) {
             if (t < T) {
-                const u32x4 xv = *reinterpret_cast<const u32x4*>(xb + (size_t)t * H + tid * 8);
+                float xv[8];  // the token's 8 columns (bf16 or f32 input)
+                if (a.x_bf16) {
+                    const u32x4 u = *reinterpret_cast<const u32x4*>(xb + (size_t)t * H + tid * 8);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        xv[2 * i] = __uint_as_float(u[i] << 16);
+                        xv[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+                    }
+                } else {
+                    const f32x4 u0 = *reinterpret_cast<const f32x4*>(xf + (size_t)t * H + tid * 8);
+                    const f32x4 u1 = *reinterpret_cast<const f32x4*>(xf + (size_t)t * H + tid * 8 + 4);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        xv[i] = u0[i];
+                        xv[4 + i] = u1[i];
+                    }
+                }
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float x0 = __uint_as_float(xv[i] << 16), x1 = __uint_as_float(xv[i] & 0xffff0000u);
+                    const float x0 = xv[2 * i], x1 = xv[2 * i + 1];
                     s[t] = fmaf(x0, w[2 * i], s[t]);
                     s[t] = fmaf(x1, w[2 * i + 1], s[t]);
                     sa[t] = fmaf(fabsf(x0), fabsf(w[2 * i]), sa[t]);
@@ -334,9 +351,35 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
         const int rbl = min(rbw, I / kTileRows - 1);
         const bool stage = !have_x;
         if (stage && r < cnt) {
-            const uint16_t* src = xb + (size_t)r * H + wave * 32 + 8 * (lane >> 4);
+            if (a.x_bf16) {
+                const uint16_t* src = xb + (size_t)r * H + wave * 32 + 8 * (lane >> 4);
 #pragma unroll
-            for (int kt = 0; kt < KT; ++kt) load_lds16(src + kt * kTileK, As + (size_t)(kt * 4 + wave) * 64 * 8);
+                for (int kt = 0; kt < KT; ++kt) load_lds16(src + kt * kTileK, As + (size_t)(kt * 4 + wave) * 64 * 8);
+            } else {
+                // f32 input: this wave's rows -> f16 into As before the weights are
+                // requested (5 k-tiles of registers at a time)
+                const float* src = static_cast<const float*>(a.x) + (size_t)r * H + wave * 32 + 8 * (lane >> 4);
+#pragma unroll
+                for (int k0 = 0; k0 < KT; k0 += 5) {
+                    f32x4 v[5][2];
+#pragma unroll
+                    for (int i = 0; i < 5; ++i)
+                        if (k0 + i < KT) {
+                            v[i][0] = *reinterpret_cast<const f32x4*>(src + (k0 + i) * kTileK);
+                            v[i][1] = *reinterpret_cast<const f32x4*>(src + (k0 + i) * kTileK + 4);
+                        }
+#pragma unroll
+                    for (int i = 0; i < 5; ++i)
+                        if (k0 + i < KT) {
+                            const f16x8 h = {(f16)v[i][0][0], (f16)v[i][0][1], (f16)v[i][0][2], (f16)v[i][0][3],
+                                             (f16)v[i][1][0], (f16)v[i][1][1], (f16)v[i][1][2], (f16)v[i][1][3]};
+                            asm volatile("ds_write_b128 %0, %1" ::"v"(lds_addr(As + (size_t)((k0 + i) * 4 + wave) * 64 * 8 +
+                                                                              (size_t)lane * 8)),
+                                         "v"(h)
+                                         : "memory");
+                        }
+                }
+            }
         }
         f16* ssw = Ss + (size_t)wave * Lay::SROWS * Lay::SRM;
         const size_t sb = (size_t)g * a.gu_sstride + (size_t)rbl * SROW;
@@ -358,7 +401,7 @@ __global__ __launch_bounds__(256, kFusedWGPerCU) void decode_fused_kernel(Decode
         flush(2 * KT);  // the previous item: its stores are older than the A rows and scales
         if (prefetch_cand) cand_prefetch();  // behind the weights: consumed after the item
         wait_vm_n(2 * KT + (prefetch_cand && wave == 0 ? 1 : 0));  // A rows and scales
-        if (stage) convert_own_rows<KT>(As, wave, lane);
+        if (stage && a.x_bf16) convert_own_rows<KT>(As, wave, lane);
         lds_barrier();
         if (stage && !ZP) {
             bias_seeds<KT, GPT>(As, Cs, tid);
@@ -647,7 +690,7 @@ bool decode_fused_ok(int hidden, int inter, int group) {
 }
 
 hipError_t launch_decode_fused(const DecodeArgs& a, hipStream_t st) {
-    if (a.seq < 1 || a.seq > kFusedMaxSeq || !a.x_bf16 || a.rms_weight || !a.sync) return hipErrorInvalidValue;
+    if (a.seq < 1 || a.seq > kFusedMaxSeq || a.rms_weight || !a.sync) return hipErrorInvalidValue;
     if (a.n_experts + a.n_virtual > kMaxExperts || a.n_experts > 64 || a.top_k > kMaxTopK) return hipErrorInvalidValue;
     if (!decode_fused_ok(a.hidden, a.inter, a.group)) return hipErrorInvalidValue;
     const bool zp = a.gate_z != nullptr;
