@@ -332,24 +332,6 @@ __device__ __forceinline__ void item_mma_f(W0 w0, W1 w1, uint32_t a_base, uint32
 }
 
 
-// Maximum of v over the 64 lanes, in every lane: DPP steps inside each 16-lane
-// row (quad swaps, half-row and row mirrors), then the four row maxima. fmaxf
-// drops NaN like the reference's strict '>' scan never picks one.
-__device__ __forceinline__ float wave_max64(float v) {
-    // (bound_ctrl off and every row enabled: each lane reads its partner)
-#define UOCR_MAXSTEP(CTRL) \
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false)))
-    UOCR_MAXSTEP(0xB1);   // quad_perm [1,0,3,2]
-    UOCR_MAXSTEP(0x4E);   // quad_perm [2,3,0,1]
-    UOCR_MAXSTEP(0x141);  // row_half_mirror
-    UOCR_MAXSTEP(0x140);  // row_mirror
-#undef UOCR_MAXSTEP
-    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
-}
 
 // Scoring (src/kernels/cpu_ops.cpp:93-106 softmax, or sigmoid) and greedy
 // top-k (src/engine/moe_decoder.cpp:264-287) of token t by ONE wave, lane e
@@ -363,39 +345,11 @@ __device__ __forceinline__ void router_select(const DecodeArgs& a, int t, float 
                                               const uint64_t* etab) {
     (void)topv;
     const int lane = threadIdx.x & 63;
-    const int E = a.n_experts, K = a.top_k;
-    float p;
-    if (a.scoring_sigmoid) {
-        p = __fdiv_rn(1.0f, 1.0f + ref_expf(-acc, etab));
-    } else {
-        const float mx = wave_max64(lane < E ? acc : -INFINITY);
-        const float ev = lane < E ? ref_expf(acc - mx, etab) : 0.0f;
-        sc[lane] = ev;
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        const float sum = ordered_sum64(sc, E);  // expert order
-        p = ev * __fdiv_rn(1.0f, sum);
-    }
-    float rem = lane < E ? p : -INFINITY;
-    float wsel = 0.0f, wsum = 0.0f;
-    int rank = kMaxTopK;
-    for (int j = 0; j < K; ++j) {
-        const float m = wave_max64(rem);
-        const uint64_t tie = __ballot(rem == m);
-        const int win = (int)__builtin_ctzll(tie);
-        if (lane == win) {
-            rank = j;
-            rem = -INFINITY;
-        }
-        if (lane == j) wsel = m;
-        wsum += m;  // moe_decoder.cpp:280-281, selection order
-    }
+    const int K = a.top_k;
+    const WaveTopk pick = wave_topk(acc, a.n_experts, K, a.scoring_sigmoid, a.norm_topk_prob, a.scaling, sc, etab);
+    const int rank = pick.rank;
     if (lane < K) {
-        float wj = wsel;
-        if (K > 1 && a.norm_topk_prob) {  // moe_decoder.cpp:280-284
-            wj = __fdiv_rn(wj, wsum + 1e-20f) * a.scaling;
-        } else {
-            wj *= a.scaling;
-        }
+        const float wj = pick.w;
         if constexpr (COHERENT) {
             __hip_atomic_store(a.wts + (size_t)t * K + lane, wj, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         } else {

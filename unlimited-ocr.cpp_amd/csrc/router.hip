@@ -385,8 +385,7 @@ constexpr int kChunkC8 = 16;  // 128 columns per chunk
 __host__ __device__ constexpr size_t router_lds_bytes(int H, int waves) {
     return (size_t)waves * H * 4          // xs
            + 2ull * kChunkC8 * 64 * 16    // W chunks (E <= 64)
-           + (size_t)waves * 64 * 4       // per-wave scores
-           + (size_t)waves * 16 * 4;      // per-wave top-k values
+           + (size_t)waves * 64 * 4;      // per-wave scores
 }
 
 constexpr int kMaxChunks = 14;  // hidden <= 1792
@@ -401,7 +400,6 @@ __global__ __launch_bounds__(WAVES * 64) void router_kernel(RouterArgs a) {
     float* xs = reinterpret_cast<float*>(smem) + (size_t)wave * H;
     u32x4* wb = reinterpret_cast<u32x4*>(smem + (size_t)WAVES * H * 4);
     float* scr = reinterpret_cast<float*>(wb + 2 * kChunkC8 * 64) + wave * 64;
-    float* topv = reinterpret_cast<float*>(wb + 2 * kChunkC8 * 64) + WAVES * 64 + wave * 16;
     __shared__ uint64_t etab[32];
     if (threadIdx.x < 32) etab[threadIdx.x] = uocr_exp2_tab[threadIdx.x];
     const int t = blockIdx.x * WAVES + wave;
@@ -465,6 +463,67 @@ __global__ __launch_bounds__(WAVES * 64) void router_kernel(RouterArgs a) {
 
     // logits: lane e runs the sequential fmaf chain over all H columns
     float acc = 0.0f;
+    if constexpr (!RMS && WAVES == 16) {
+        // The token row is the same for every lane of the wave: it comes in
+        // through scalar loads (16 dwords per block, the next block requested
+        // while this one is consumed), so LDS serves only the weight reads.
+        constexpr int DW = 2 * (int)sizeof(XT);  // dwords per 8 columns
+        constexpr int BC = 16 / DW;               // 8-column steps per block
+        constexpr int NB = kChunkC8 / BC;         // blocks per chunk
+        const int n_blocks = n_chunks * NB;
+        const int tu = min(__builtin_amdgcn_readfirstlane(t), a.seq - 1);
+        const uint64_t row = (uint64_t)(x + (size_t)tu * H);
+        auto block_load = [&](int b, u32x16& q) {
+            const uint64_t ad = row + (uint64_t)min(b, n_blocks - 1) * 64u;
+            asm volatile("s_load_dwordx16 %0, %1, 0x0" : "=s"(q) : "s"(ad) : "memory");
+        };
+        u32x16 c0;
+        block_load(0, c0);
+#pragma unroll
+        for (int ch = 0; ch < kMaxChunks; ++ch) {
+            if (ch < n_chunks) {
+                const u32x4* cur = wb + (ch & 1) * kChunkC8 * 64;
+#pragma unroll
+                for (int bl = 0; bl < NB; ++bl) {
+                    // (acc ties the previous block's chain to this point, so
+                    // the loads are not all hoisted to the chunk's start)
+                    asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(c0), "+v"(acc)::"memory");
+                    u32x16 n0;
+                    block_load(ch * NB + bl + 1, n0);
+#pragma unroll
+                    for (int i = 0; i < BC; ++i) {
+                        const u32x4 wv = cur[(bl * BC + i) * E + lane];
+                        float xv[8];
+#pragma unroll
+                        for (int k = 0; k < DW; ++k) {
+                            const uint32_t d = c0[DW * i + k];
+                            if constexpr (sizeof(XT) == 2) {
+                                xv[2 * k] = __uint_as_float(d << 16);
+                                xv[2 * k + 1] = __uint_as_float(d & 0xffff0000u);
+                            } else {
+                                xv[k] = __uint_as_float(d);
+                            }
+                        }
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            acc = fmaf(xv[2 * k], __uint_as_float(wv[k] << 16), acc);
+                            acc = fmaf(xv[2 * k + 1], __uint_as_float(wv[k] & 0xffff0000u), acc);
+                        }
+                    }
+                    c0 = n0;
+                }
+                if (ch + 1 < kMaxChunks && ch + 1 < n_chunks) {
+#pragma unroll
+                    for (int j = 0; j < UPT; ++j)
+                        if (tid + j * NT < chunk_units)
+                            wb[((ch + 1) & 1) * kChunkC8 * 64 + tid + j * NT] = wreg[ch + 1][j];
+                }
+                __syncthreads();
+            }
+        }
+        // the last block's (clamped, repeated) loads must land before exit
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(c0)::"memory");
+    } else
 #pragma unroll
     for (int ch = 0; ch < kMaxChunks; ++ch) {
         if (ch < n_chunks) {
@@ -495,37 +554,10 @@ __global__ __launch_bounds__(WAVES * 64) void router_kernel(RouterArgs a) {
         }
     }
 
-    // scoring (softmax over experts in index order, or sigmoid)
-    float p;
-    if (a.scoring_sigmoid) {
-        p = __fdiv_rn(1.0f, 1.0f + ref_expf(-acc, etab));
-    } else {
-        const float mx = wave_max(lane < E ? acc : -INFINITY);
-        const float ev = ref_expf(acc - mx, etab);
-        scr[lane] = ev;
-        __syncthreads();
-        float sum = 0.0f;
-        for (int e = 0; e < E; ++e) sum += scr[e];  // expert order, same bits in every lane
-        p = ev * __fdiv_rn(1.0f, sum);
-        __syncthreads();
-    }
-    scr[lane] = p;
-    __syncthreads();
-    const int rank = lane < E ? greedy_rank(scr, E, lane, p) : 64;
-    if (rank < K) topv[rank] = p;
-    __syncthreads();
-    if (live && lane < K) {
-        float wj = topv[lane];
-        if (K > 1 && a.norm_topk_prob) {  // moe_decoder.cpp:280-284
-            float sum = 0.0f;
-            for (int j = 0; j < K; ++j) sum += topv[j];
-            wj = __fdiv_rn(wj, sum + 1e-20f) * a.scaling;
-        } else {
-            wj *= a.scaling;
-        }
-        a.weights[(size_t)t * K + lane] = wj;
-    }
-    if (live && rank < K) a.ids[(size_t)t * K + rank] = lane;
+    // scoring and greedy top-k by the wave alone (no workgroup barrier)
+    const WaveTopk pick = wave_topk(acc, E, K, a.scoring_sigmoid, a.norm_topk_prob, a.scaling, scr, etab);
+    if (live && lane < K) a.weights[(size_t)t * K + lane] = pick.w;
+    if (live && pick.rank < K) a.ids[(size_t)t * K + pick.rank] = lane;
 }
 
 // Router from precomputed logits [seq, E] (mirror of moe_router_topk,

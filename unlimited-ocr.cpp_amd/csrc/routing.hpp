@@ -44,35 +44,6 @@ __device__ __forceinline__ float ref_expf(float x, const uint64_t* tab) {
 // 2^(i/32) table of the expf restatement, for staging into LDS
 __device__ __constant__ static const uint64_t uocr_exp2_tab[32] = UOCR_EXP2_TAB32;
 
-// Greedy top-k of the reference (strict '>' scan, first maximum wins,
-// moe_decoder.cpp:264-277) selects experts in order of (p descending, index
-// ascending); lane e's position in that order is the number of experts that
-// beat it. p[] holds the scores in LDS; returns the rank of `pe` (lane e).
-__device__ __forceinline__ int greedy_rank(const float* p, int E, int e, float pe) {
-    int rank = 0;
-    for (int j = 0; j < E; ++j) {
-        const float q = p[j];
-        rank += (q > pe || (q == pe && j < e)) ? 1 : 0;
-    }
-    return rank;
-}
-
-// The same rank over exactly 64 scores in LDS (16-byte aligned): the reads are
-// independent 16-byte broadcasts, issued together.
-__device__ __forceinline__ int greedy_rank64(const float* p, int e, float pe) {
-    int part[4] = {0, 0, 0, 0};  // four independent counting chains
-#pragma unroll
-    for (int j4 = 0; j4 < 16; ++j4) {
-        const f32x4 q = reinterpret_cast<const f32x4*>(p)[j4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int j = 4 * j4 + i;
-            part[i] += (q[i] > pe || (q[i] == pe && j < e)) ? 1 : 0;
-        }
-    }
-    return (part[0] + part[1]) + (part[2] + part[3]);
-}
-
 // sum of p[0..E) in index order (E <= 64; p 16-byte aligned, zero-padded to 64)
 __device__ __forceinline__ float ordered_sum64(const float* p, int E) {
     f32x4 q[16];
@@ -85,6 +56,76 @@ __device__ __forceinline__ float ordered_sum64(const float* p, int E) {
         for (int i = 0; i < 4; ++i)
             if (4 * j4 + i < E) s += q[j4][i];
     return s;
+}
+
+
+// Maximum of v over the 64 lanes, in every lane: DPP steps inside each 16-lane
+// row (quad swaps, half-row and row mirrors), then the four row maxima. fmaxf
+// drops NaN like the reference's strict '>' scan never picks one.
+__device__ __forceinline__ float wave_max64(float v) {
+    // (bound_ctrl off and every row enabled: each lane reads its partner)
+#define UOCR_MAXSTEP(CTRL) \
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false)))
+    UOCR_MAXSTEP(0xB1);   // quad_perm [1,0,3,2]
+    UOCR_MAXSTEP(0x4E);   // quad_perm [2,3,0,1]
+    UOCR_MAXSTEP(0x141);  // row_half_mirror
+    UOCR_MAXSTEP(0x140);  // row_mirror
+#undef UOCR_MAXSTEP
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// Scoring (src/kernels/cpu_ops.cpp:93-106 softmax, or sigmoid) and greedy
+// top-k (src/engine/moe_decoder.cpp:264-287) of one token by ONE wave, lane e
+// holding expert e's logit `acc` (E <= 64). The greedy scan (strict '>', so
+// the lowest index wins a tie; the pick is then removed) is K rounds of a wave
+// maximum and the lowest lane holding it. sc: 64 floats of LDS, 16-byte
+// aligned, private to the wave. Returns the lane's position in the selection
+// (kTopkNone if not picked) and, in lanes j < K, the j-th pick's weight after
+// the optional renormalisation and the scaling factor.
+constexpr int kTopkNone = 64;
+struct WaveTopk {
+    int rank;
+    float w;
+};
+__device__ __forceinline__ WaveTopk wave_topk(float acc, int E, int K, bool sigmoid, bool norm_topk_prob,
+                                              float scaling, float* sc, const uint64_t* etab) {
+    const int lane = threadIdx.x & 63;
+    float p;
+    if (sigmoid) {
+        p = __fdiv_rn(1.0f, 1.0f + ref_expf(-acc, etab));
+    } else {
+        const float mx = wave_max64(lane < E ? acc : -INFINITY);
+        const float ev = lane < E ? ref_expf(acc - mx, etab) : 0.0f;
+        sc[lane] = ev;
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        const float sum = ordered_sum64(sc, E);  // expert order
+        p = ev * __fdiv_rn(1.0f, sum);
+    }
+    float rem = lane < E ? p : -INFINITY;
+    float wsel = 0.0f, wsum = 0.0f;
+    int rank = kTopkNone;
+    for (int j = 0; j < K; ++j) {
+        const float m = wave_max64(rem);
+        const uint64_t tie = __ballot(rem == m);
+        const int win = (int)__builtin_ctzll(tie);
+        if (lane == win) {
+            rank = j;
+            rem = -INFINITY;
+        }
+        if (lane == j) wsel = m;
+        wsum += m;  // moe_decoder.cpp:280-281, selection order
+    }
+    float wj = wsel;
+    if (K > 1 && norm_topk_prob) {  // moe_decoder.cpp:280-284
+        wj = __fdiv_rn(wj, wsum + 1e-20f) * scaling;
+    } else {
+        wj *= scaling;
+    }
+    return WaveTopk{rank, wj};
 }
 
 }  // namespace uocr_hip
