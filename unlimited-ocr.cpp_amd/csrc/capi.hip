@@ -925,6 +925,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
             ra.rms_weight = L->rms_weight;
             ra.rms_eps = L->rms_eps;
             ra.router_t = L->router_t;
+    ra.router_f32 = L->router_f32;
             ra.norm_topk_prob = L->norm_topk_prob;
             ra.scoring_sigmoid = L->scoring_sigmoid;
             ra.scaling = L->scaling;
@@ -954,6 +955,7 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     ra.rms_weight = L->rms_weight;
     ra.rms_eps = L->rms_eps;
     ra.router_t = L->router_t;
+    ra.router_f32 = L->router_f32;
     ra.norm_topk_prob = L->norm_topk_prob;
     ra.scoring_sigmoid = L->scoring_sigmoid;
     ra.scaling = L->scaling;

@@ -53,9 +53,6 @@ template <int OFF>
 __device__ __forceinline__ void lds_read16(f16x8& d, uint32_t addr) {
     asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(d) : "v"(addr), "n"(OFF));
 }
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
 // 16-byte LDS write issued by inline asm
 template <int OFF>
 __device__ __forceinline__ void lds_write16(uint32_t addr, f16x8 v) {

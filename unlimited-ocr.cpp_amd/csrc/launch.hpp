@@ -40,6 +40,7 @@ struct RouterArgs {
     const float* rms_weight;  // optional [hidden]
     float rms_eps;
     const uint16_t* router_t; // router W as [hidden/8][n_experts][8] bf16
+    const float* router_f32;  // the same W as f32 [hidden/4][64][4] (experts padded to 64), or null
     int norm_topk_prob, scoring_sigmoid;
     float scaling;
     f16* x16;                 // out [seq, hidden] f16 expert input

@@ -560,6 +560,102 @@ __global__ __launch_bounds__(WAVES * 64) void router_kernel(RouterArgs a) {
     if (live && pick.rank < K) a.ids[(size_t)t * K + pick.rank] = lane;
 }
 
+
+// Router without the RMSNorm prologue for fewer than 4096 tokens: one token
+// per wave, one wave per SIMD, where a wave issues one VALU op every several
+// cycles whatever the dependences. The weights therefore come from the f32
+// copy of the router ([H/4][64][4]: a 128-column chunk is one contiguous
+// 32 KiB block), so a column costs one FMA and no widening; the chunks stream
+// through LDS from a register ring as in router_kernel.
+constexpr int kF32ChunkUnits = kChunkC8 * 2 * 64;  // 16-byte units per 128-column chunk
+
+__host__ __device__ constexpr size_t router_f32w_lds_bytes(int H) {
+    return (size_t)4 * H * 4                     // xs
+           + 2ull * kF32ChunkUnits * 16         // W chunks
+           + (size_t)4 * 64 * 4;                // per-wave scores
+}
+
+template <typename XT>
+__global__ __launch_bounds__(256) void router_f32w_kernel(RouterArgs a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    constexpr int WAVES = 4, NT = 256;
+    constexpr int UPT = kF32ChunkUnits / NT;  // 8
+    constexpr int RING = 3;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, tid = threadIdx.x;
+    const int H = a.hidden, E = a.n_experts, K = a.top_k;
+    float* xs = reinterpret_cast<float*>(smem) + (size_t)wave * H;
+    f32x4* wb = reinterpret_cast<f32x4*>(smem + (size_t)WAVES * H * 4);
+    float* scr = reinterpret_cast<float*>(wb + 2 * kF32ChunkUnits) + wave * 64;
+    __shared__ uint64_t etab[32];
+    if (threadIdx.x < 32) etab[threadIdx.x] = uocr_exp2_tab[threadIdx.x];
+    const int t = blockIdx.x * WAVES + wave;
+    const bool live = t < a.seq;
+    const XT* x = static_cast<const XT*>(a.x);
+    const f32x4* wsrc = reinterpret_cast<const f32x4*>(a.router_f32);
+    const int n_chunks = H / (kChunkC8 * 8);
+
+    f32x4 wreg[RING][UPT];
+    auto issue_chunk = [&](int ch) {
+#pragma unroll
+        for (int j = 0; j < UPT; ++j)
+            if (ch < n_chunks) wreg[ch % RING][j] = wsrc[(size_t)ch * kF32ChunkUnits + tid + j * NT];
+    };
+#pragma unroll
+    for (int ch = 0; ch < RING; ++ch) issue_chunk(ch);
+    // this wave's token row, as f32 (and as f16 for the experts)
+    for (int c = lane * 8; c < H; c += 64 * 8) {
+        float v[8];
+        if (live) {
+            load8_f32<XT>(x + (size_t)t * H + c, v);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+        }
+        *reinterpret_cast<f32x4*>(xs + c) = f32x4{v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<f32x4*>(xs + c + 4) = f32x4{v[4], v[5], v[6], v[7]};
+        if (live)
+            *reinterpret_cast<f16x8*>(a.x16 + (size_t)t * H + c) =
+                f16x8{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3], (f16)v[4], (f16)v[5], (f16)v[6], (f16)v[7]};
+    }
+#pragma unroll
+    for (int j = 0; j < UPT; ++j) wb[tid + j * NT] = wreg[0][j];
+    if (RING < kMaxChunks) issue_chunk(RING);
+    __syncthreads();
+
+    // logits: lane e runs the sequential fmaf chain over all H columns (lanes
+    // >= E run the zero padding)
+    float acc = 0.0f;
+#pragma unroll
+    for (int ch = 0; ch < kMaxChunks; ++ch) {
+        if (ch < n_chunks) {
+            const f32x4* cur = wb + (ch & 1) * kF32ChunkUnits;
+            const float* xc = xs + ch * kChunkC8 * 8;
+            // 32 steps of 4 columns; the LDS reads run 6 steps ahead of the
+            // FMAs with explicit lgkmcnt waits (the compiler's schedule waits
+            // on every read pair or hoists every read of the chunk)
+            const uint32_t w_addr = lds_addr(cur) + lane * 16;
+            const uint32_t x_addr = lds_addr(xc);
+            asm volatile(UOCR_RCHUNK(UOCR_RMAC_FMA)
+                : [acc] "+v"(acc)
+                : [w] "v"(w_addr), [x] "v"(x_addr)
+                : "v64", "v65", "v66", "v67", "v68", "v69", "v70", "v71", "v72", "v73", "v74", "v75", "v76", "v77",
+                  "v78", "v79", "v80", "v81", "v82", "v83", "v84", "v85", "v86", "v87", "v88", "v89", "v90", "v91",
+                  "v92", "v93", "v94", "v95", "v96", "v97", "v98", "v99", "v100", "v101", "v102", "v103", "v104",
+                  "v105", "v106", "v107", "v108", "v109", "v110", "v111", "memory");
+            if (ch + 1 < kMaxChunks && ch + 1 < n_chunks) {
+#pragma unroll
+                for (int j = 0; j < UPT; ++j) wb[((ch + 1) & 1) * kF32ChunkUnits + tid + j * NT] = wreg[(ch + 1) % RING][j];
+                if (ch + 1 + RING < kMaxChunks) issue_chunk(ch + 1 + RING);
+            }
+            __syncthreads();
+        }
+    }
+
+    const WaveTopk pick = wave_topk(acc, E, K, a.scoring_sigmoid, a.norm_topk_prob, a.scaling, scr, etab);
+    if (live && lane < K) a.weights[(size_t)t * K + lane] = pick.w;
+    if (live && pick.rank < K) a.ids[(size_t)t * K + pick.rank] = lane;
+}
+
 // Router from precomputed logits [seq, E] (mirror of moe_router_topk,
 // src/kernels/cuda/moe_device.cu:24-98), any E: one wave per token, experts
 // strided over lanes; reduction orders match the CPU reference.
@@ -640,8 +736,20 @@ static hipError_t launch_router_t(const RouterArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
+template <typename XT>
+static hipError_t launch_router_f32w(const RouterArgs& a, hipStream_t st) {
+    static hipError_t attr = hipFuncSetAttribute((const void*)router_f32w_kernel<XT>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
+    if (attr != hipSuccess) return attr;
+    launch_k((router_f32w_kernel<XT>), dim3((a.seq + 3) / 4), dim3(256), router_f32w_lds_bytes(a.hidden), st, a);
+    return hipGetLastError();
+}
+
 template <typename XT, bool RMS>
 static hipError_t launch_router_w(const RouterArgs& a, hipStream_t st) {
+    if constexpr (!RMS) {
+        if (a.seq < 4096 && a.router_f32) return launch_router_f32w<XT>(a, st);
+    }
     // 4 tokens per workgroup spread the FMA chains over the CUs; once that
     // gives 4+ workgroups per CU (4096 tokens on 256 CUs), 16 tokens per
     // workgroup amortise the router-weight stream

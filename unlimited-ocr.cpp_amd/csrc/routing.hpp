@@ -128,4 +128,238 @@ __device__ __forceinline__ WaveTopk wave_topk(float acc, int E, int K, bool sigm
     return WaveTopk{rank, wj};
 }
 
+// One 128-column chunk of the router chain (lane e: its expert, columns
+// ascending) with the multiply-accumulate step MAC(x, w) spelled by the caller.
+#define UOCR_RCHUNK(MAC) \
+    "s_waitcnt lgkmcnt(0)\n" \
+    "ds_read_b128 v[64:67], %[w] offset:0\n" \
+    "ds_read_b128 v[68:71], %[x] offset:0\n" \
+    "ds_read_b128 v[72:75], %[w] offset:1024\n" \
+    "ds_read_b128 v[76:79], %[x] offset:16\n" \
+    "ds_read_b128 v[80:83], %[w] offset:2048\n" \
+    "ds_read_b128 v[84:87], %[x] offset:32\n" \
+    "ds_read_b128 v[88:91], %[w] offset:3072\n" \
+    "ds_read_b128 v[92:95], %[x] offset:48\n" \
+    "ds_read_b128 v[96:99], %[w] offset:4096\n" \
+    "ds_read_b128 v[100:103], %[x] offset:64\n" \
+    "ds_read_b128 v[104:107], %[w] offset:5120\n" \
+    "ds_read_b128 v[108:111], %[x] offset:80\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v68", "v64") \
+    MAC("v69", "v65") \
+    MAC("v70", "v66") \
+    MAC("v71", "v67") \
+    "ds_read_b128 v[64:67], %[w] offset:6144\n" \
+    "ds_read_b128 v[68:71], %[x] offset:96\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v76", "v72") \
+    MAC("v77", "v73") \
+    MAC("v78", "v74") \
+    MAC("v79", "v75") \
+    "ds_read_b128 v[72:75], %[w] offset:7168\n" \
+    "ds_read_b128 v[76:79], %[x] offset:112\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v84", "v80") \
+    MAC("v85", "v81") \
+    MAC("v86", "v82") \
+    MAC("v87", "v83") \
+    "ds_read_b128 v[80:83], %[w] offset:8192\n" \
+    "ds_read_b128 v[84:87], %[x] offset:128\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v92", "v88") \
+    MAC("v93", "v89") \
+    MAC("v94", "v90") \
+    MAC("v95", "v91") \
+    "ds_read_b128 v[88:91], %[w] offset:9216\n" \
+    "ds_read_b128 v[92:95], %[x] offset:144\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v100", "v96") \
+    MAC("v101", "v97") \
+    MAC("v102", "v98") \
+    MAC("v103", "v99") \
+    "ds_read_b128 v[96:99], %[w] offset:10240\n" \
+    "ds_read_b128 v[100:103], %[x] offset:160\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v108", "v104") \
+    MAC("v109", "v105") \
+    MAC("v110", "v106") \
+    MAC("v111", "v107") \
+    "ds_read_b128 v[104:107], %[w] offset:11264\n" \
+    "ds_read_b128 v[108:111], %[x] offset:176\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v68", "v64") \
+    MAC("v69", "v65") \
+    MAC("v70", "v66") \
+    MAC("v71", "v67") \
+    "ds_read_b128 v[64:67], %[w] offset:12288\n" \
+    "ds_read_b128 v[68:71], %[x] offset:192\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v76", "v72") \
+    MAC("v77", "v73") \
+    MAC("v78", "v74") \
+    MAC("v79", "v75") \
+    "ds_read_b128 v[72:75], %[w] offset:13312\n" \
+    "ds_read_b128 v[76:79], %[x] offset:208\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v84", "v80") \
+    MAC("v85", "v81") \
+    MAC("v86", "v82") \
+    MAC("v87", "v83") \
+    "ds_read_b128 v[80:83], %[w] offset:14336\n" \
+    "ds_read_b128 v[84:87], %[x] offset:224\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v92", "v88") \
+    MAC("v93", "v89") \
+    MAC("v94", "v90") \
+    MAC("v95", "v91") \
+    "ds_read_b128 v[88:91], %[w] offset:15360\n" \
+    "ds_read_b128 v[92:95], %[x] offset:240\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v100", "v96") \
+    MAC("v101", "v97") \
+    MAC("v102", "v98") \
+    MAC("v103", "v99") \
+    "ds_read_b128 v[96:99], %[w] offset:16384\n" \
+    "ds_read_b128 v[100:103], %[x] offset:256\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v108", "v104") \
+    MAC("v109", "v105") \
+    MAC("v110", "v106") \
+    MAC("v111", "v107") \
+    "ds_read_b128 v[104:107], %[w] offset:17408\n" \
+    "ds_read_b128 v[108:111], %[x] offset:272\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v68", "v64") \
+    MAC("v69", "v65") \
+    MAC("v70", "v66") \
+    MAC("v71", "v67") \
+    "ds_read_b128 v[64:67], %[w] offset:18432\n" \
+    "ds_read_b128 v[68:71], %[x] offset:288\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v76", "v72") \
+    MAC("v77", "v73") \
+    MAC("v78", "v74") \
+    MAC("v79", "v75") \
+    "ds_read_b128 v[72:75], %[w] offset:19456\n" \
+    "ds_read_b128 v[76:79], %[x] offset:304\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v84", "v80") \
+    MAC("v85", "v81") \
+    MAC("v86", "v82") \
+    MAC("v87", "v83") \
+    "ds_read_b128 v[80:83], %[w] offset:20480\n" \
+    "ds_read_b128 v[84:87], %[x] offset:320\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v92", "v88") \
+    MAC("v93", "v89") \
+    MAC("v94", "v90") \
+    MAC("v95", "v91") \
+    "ds_read_b128 v[88:91], %[w] offset:21504\n" \
+    "ds_read_b128 v[92:95], %[x] offset:336\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v100", "v96") \
+    MAC("v101", "v97") \
+    MAC("v102", "v98") \
+    MAC("v103", "v99") \
+    "ds_read_b128 v[96:99], %[w] offset:22528\n" \
+    "ds_read_b128 v[100:103], %[x] offset:352\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v108", "v104") \
+    MAC("v109", "v105") \
+    MAC("v110", "v106") \
+    MAC("v111", "v107") \
+    "ds_read_b128 v[104:107], %[w] offset:23552\n" \
+    "ds_read_b128 v[108:111], %[x] offset:368\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v68", "v64") \
+    MAC("v69", "v65") \
+    MAC("v70", "v66") \
+    MAC("v71", "v67") \
+    "ds_read_b128 v[64:67], %[w] offset:24576\n" \
+    "ds_read_b128 v[68:71], %[x] offset:384\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v76", "v72") \
+    MAC("v77", "v73") \
+    MAC("v78", "v74") \
+    MAC("v79", "v75") \
+    "ds_read_b128 v[72:75], %[w] offset:25600\n" \
+    "ds_read_b128 v[76:79], %[x] offset:400\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v84", "v80") \
+    MAC("v85", "v81") \
+    MAC("v86", "v82") \
+    MAC("v87", "v83") \
+    "ds_read_b128 v[80:83], %[w] offset:26624\n" \
+    "ds_read_b128 v[84:87], %[x] offset:416\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v92", "v88") \
+    MAC("v93", "v89") \
+    MAC("v94", "v90") \
+    MAC("v95", "v91") \
+    "ds_read_b128 v[88:91], %[w] offset:27648\n" \
+    "ds_read_b128 v[92:95], %[x] offset:432\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v100", "v96") \
+    MAC("v101", "v97") \
+    MAC("v102", "v98") \
+    MAC("v103", "v99") \
+    "ds_read_b128 v[96:99], %[w] offset:28672\n" \
+    "ds_read_b128 v[100:103], %[x] offset:448\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v108", "v104") \
+    MAC("v109", "v105") \
+    MAC("v110", "v106") \
+    MAC("v111", "v107") \
+    "ds_read_b128 v[104:107], %[w] offset:29696\n" \
+    "ds_read_b128 v[108:111], %[x] offset:464\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v68", "v64") \
+    MAC("v69", "v65") \
+    MAC("v70", "v66") \
+    MAC("v71", "v67") \
+    "ds_read_b128 v[64:67], %[w] offset:30720\n" \
+    "ds_read_b128 v[68:71], %[x] offset:480\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v76", "v72") \
+    MAC("v77", "v73") \
+    MAC("v78", "v74") \
+    MAC("v79", "v75") \
+    "ds_read_b128 v[72:75], %[w] offset:31744\n" \
+    "ds_read_b128 v[76:79], %[x] offset:496\n" \
+    "s_waitcnt lgkmcnt(10)\n" \
+    MAC("v84", "v80") \
+    MAC("v85", "v81") \
+    MAC("v86", "v82") \
+    MAC("v87", "v83") \
+    "s_waitcnt lgkmcnt(8)\n" \
+    MAC("v92", "v88") \
+    MAC("v93", "v89") \
+    MAC("v94", "v90") \
+    MAC("v95", "v91") \
+    "s_waitcnt lgkmcnt(6)\n" \
+    MAC("v100", "v96") \
+    MAC("v101", "v97") \
+    MAC("v102", "v98") \
+    MAC("v103", "v99") \
+    "s_waitcnt lgkmcnt(4)\n" \
+    MAC("v108", "v104") \
+    MAC("v109", "v105") \
+    MAC("v110", "v106") \
+    MAC("v111", "v107") \
+    "s_waitcnt lgkmcnt(2)\n" \
+    MAC("v68", "v64") \
+    MAC("v69", "v65") \
+    MAC("v70", "v66") \
+    MAC("v71", "v67") \
+    "s_waitcnt lgkmcnt(0)\n" \
+    MAC("v76", "v72") \
+    MAC("v77", "v73") \
+    MAC("v78", "v74") \
+    MAC("v79", "v75")
+// fused step: acc = fma(x, w, acc) (the reference's contracted bf16 chain)
+#define UOCR_RMAC_FMA(X, W) "v_fmac_f32 %[acc], " X ", " W "\n"
+// unfused step: acc = acc + round(x * w) (the reference's f32 matmul_t, whose
+// build does not contract the loop; src/kernels/cpu_ops.cpp:11-24)
+#define UOCR_RMAC_SEP(X, W) "v_mul_f32 v112, " X ", " W "\nv_add_f32 %[acc], %[acc], v112\n"
+
 }  // namespace uocr_hip
