@@ -352,6 +352,86 @@ __global__ __launch_bounds__(kGroupThreads) void group_scan_kernel(GroupArgs g, 
             }
 }
 
+// Scan and place in one launch, for up to kGroupFusedMaxChunks chunks: every
+// workgroup (one per 1024-entry chunk) reduces the per-(chunk, expert) counts
+// itself (n_chunks x E ints from L2), so its bases need no other workgroup;
+// workgroup 0 also writes the expert totals, offsets and tile list, and the
+// virtual groups' slots are spread over all of them. All loads come before
+// the first store.
+constexpr int kGroupFusedMaxChunks = 64;
+
+__global__ __launch_bounds__(kGroupThreads) void group_scan_place_kernel(GroupArgs g, int n_chunks) {
+    extern __shared__ int cc[];  // [n_chunks][E] counts
+    __shared__ int hist[kMaxExperts], offs[kMaxExperts + 1], base[kMaxExperts];
+    __shared__ int ntl[kMaxExperts], tile0[kMaxExperts + 1], nsh[kMaxExperts], short0[kMaxExperts + 1];
+    const int tid = threadIdx.x, wave = tid >> 6;
+    const int E = g.n_experts, Ev = E + g.n_virtual, N = g.seq * g.top_k;
+    const int b = blockIdx.x;
+    const int i = b * kGroupThreads + tid;
+    const int e_i = i < N ? g.ids[i] : -1;
+    const bool valid = e_i >= 0 && e_i < E;
+    const int lr = valid ? g.lrank[i] : 0;
+    const float w_i = valid ? g.weights[i] : 0.0f;
+    for (int k = tid; k < n_chunks * E; k += kGroupThreads) cc[k] = g.chunk_count[k];
+    __syncthreads();
+    for (int e = tid; e < Ev; e += kGroupThreads) {
+        int acc = 0;
+        if (e < E) {
+            int mine = 0;
+            for (int c = 0; c < n_chunks; ++c) {
+                if (c == b) mine = acc;
+                acc += cc[c * E + e];
+            }
+            base[e] = mine;  // entries of expert e in the chunks before this one
+        } else {
+            acc = g.seq;
+        }
+        hist[e] = acc;
+        ntl[e] = long_tiles(acc, g.bm);
+        nsh[e] = short_tiles(acc, g.bm);
+    }
+    __syncthreads();
+    if (wave == 0) wave0_exclusive_scan(hist, offs, Ev);
+    if (b == 0 && g.tile_e && wave == 1) wave0_exclusive_scan(ntl, tile0, Ev);
+    if (b == 0 && g.tile_e && wave == 2) wave0_exclusive_scan(nsh, short0, Ev);
+    __syncthreads();
+    if (valid) {
+        if (g.slot_tok) {  // the slot
+            const int r = offs[e_i] + base[e_i] + lr;
+            g.slot_tok[r] = i / g.top_k;
+            g.slot_w[r] = w_i;
+            if (g.pos) g.pos[i] = r;
+        } else if (g.assign_token) {  // the position within expert e_i
+            const int r = base[e_i] + lr;
+            if (r < g.cap) {
+                g.assign_token[(size_t)e_i * g.cap + r] = i / g.top_k;
+                g.assign_w[(size_t)e_i * g.cap + r] = w_i;
+            }
+        }
+    }
+    if (b == 0) {
+        for (int e = tid; e < Ev; e += kGroupThreads) {
+            if (g.counts) {
+                g.counts[e] = hist[e];
+                g.offsets[e] = offs[e];
+            }
+            if (g.assign_count && e < E) {
+                g.assign_count[e] = min(hist[e], g.cap);
+                if (hist[e] > g.cap) atomicOr(&g_router_overflow, 1);
+            }
+        }
+        if (tid == 0 && g.counts) g.offsets[Ev] = offs[Ev];
+        if (g.tile_e) write_tile_list(g, hist, offs, tile0, short0, Ev);
+    }
+    // virtual (shared-expert) groups: every token, weight 1
+    if (g.slot_tok)
+        for (int v = 0; v < g.n_virtual; ++v)
+            for (int t = i; t < g.seq; t += n_chunks * kGroupThreads) {
+                g.slot_tok[offs[E + v] + t] = t;
+                g.slot_w[offs[E + v] + t] = 1.0f;
+            }
+}
+
 __global__ __launch_bounds__(256) void group_place_kernel(GroupArgs g) {
     const int E = g.n_experts, N = g.seq * g.top_k;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -824,6 +904,10 @@ hipError_t launch_group(const GroupArgs& g, hipStream_t st) {
     const size_t lds = (size_t)n_chunks * g.n_experts * sizeof(int);
     if (lds > kGroupScanLds) return hipErrorInvalidValue;
     launch_k(group_rank_kernel, dim3(n_chunks), dim3(kGroupThreads), 0, st, g);
+    if (n_chunks <= kGroupFusedMaxChunks) {
+        launch_k(group_scan_place_kernel, dim3(n_chunks), dim3(kGroupThreads), lds, st, g, n_chunks);
+        return hipGetLastError();
+    }
     static hipError_t attr = hipFuncSetAttribute((const void*)group_scan_kernel,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, kGroupScanLds);
     if (attr != hipSuccess) return attr;
