@@ -72,6 +72,8 @@ FORMATS = {
                    "weights.cpp:289-292 keeps the shared MLP unquantised)",
     "bf16": "bf16 routed experts and bf16 shared MLP (the reference's default expert format, config.h:111)",
     "f32_input": "INT4 layer as int4, hidden states passed as f32 (the engine's normed2, gpu_decoder.cu:537-560)",
+    "f32_router": "INT4 layer as int4 with an f32 router (the AWQ-folded router, weights.cpp:199-207: the bf16 "
+                  "router times a per-column scale in [0.5, 2)), routed by the uncontracted f32 chain",
 }
 
 
@@ -82,6 +84,11 @@ def make_layer(cfg, seed, group, fmt, bias=None, rms=False):
     L = synth.random_layer(seed, group=group, router_bias=bias, rms=rms)
     if fmt == "bf16_shared":
         synth.with_bf16_shared(L, seed + 1)
+    if fmt == "f32_router":
+        import numpy as np
+        s = np.random.default_rng(seed + 2).uniform(0.5, 2.0, L.hidden).astype(np.float32)
+        w = (L.router_bf16.astype(np.uint32) << 16).view(np.float32)
+        L.router_f32 = (w * s[None, :]).astype(np.float32)
     return L
 
 
@@ -544,7 +551,7 @@ def main():
     ap.add_argument("--graph", default="",
                     help="decode configs (0, 1) replayed from a hipGraph, as a decode engine runs its step; "
                          "their eager rate is reported beside it (config 4 always runs as a graph)")
-    ap.add_argument("--formats", default="1:bf16_shared,1:bf16,3:bf16,1:f32_input",
+    ap.add_argument("--formats", default="1:bf16_shared,1:bf16,3:bf16,1:f32_input,1:f32_router,4:f32_router",
                     help="extra (config:format) lines; formats: " + ", ".join(FORMATS))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",

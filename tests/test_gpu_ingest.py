@@ -73,18 +73,22 @@ def test_gptq_file_fold_into_bf16_shared_mlp(dev, tmp_path, seq):
 
 
 @pytest.mark.parametrize("seq", [16, 300])
-def test_f32_router_bf16_input_skips_fused_kernel(dev, seq):
-    """An f32 router with bf16 input and no norm: 16 tokens would take the fused
-    kernel (bf16 router only); the layer routes with the f32 chain instead."""
+def test_f32_router_bf16_input(dev, seq):
+    """An f32 router with bf16 input and no norm: 16 tokens run the streamed
+    kernel's f32-router instantiation (the fused kernel takes only a bf16
+    router), 300 the grouped prefill path with the f32 chain."""
     from test_gpu_layer import run_layer
     from uocr_hip import MoELayerInt4, synth
     L = awq_layer(4300 + seq, group=32, n_experts=64)
     L.router_f32 = np.random.default_rng(seq).standard_normal((64, L.hidden)).astype(np.float32) * np.float32(0.03)
     x = synth.bf16_normal(np.random.default_rng(seq + 1), (seq, L.hidden), 1.0)
     layer = MoELayerInt4(L)
-    layer.set_timing(True)
-    run_layer(layer, x, "bf16", dev)
-    t, n = layer.read_timing()
-    assert n == 1 and t["fused"] == 0.0 and t["router"] > 0.0, t
+    if seq <= 16:
+        assert layer.decode_kernel(seq, "bf16") == "stream"
+    else:
+        layer.set_timing(True)
+        run_layer(layer, x, "bf16", dev)
+        t, n = layer.read_timing()
+        assert n == 1 and t["fused"] == 0.0 and t["router"] > 0.0, t
     layer.close()
     check_parity(L, x, dev, sample=32 if seq > 64 else None, label=f"f32router-bf16-t{seq}")

@@ -197,3 +197,37 @@ def test_wide_reference_quantizers_rmsnorm(dev, group):
     for seq in (40, 64, 7):
         _check(layer, L, _x(seq, L.hidden, 6700 + seq), dev, "f32", f"wide-awq-rms-g{group}-t{seq}")
     layer.close()
+
+
+def _f32_router(L, seed):
+    L.router_f32 = (np.random.default_rng(seed).standard_normal((L.n_experts, L.hidden)) * 0.03).astype(np.float32)
+    return L
+
+
+@pytest.mark.parametrize("group", [32, 128])
+def test_wide_f32_router_rmsnorm(dev, group):
+    """The engine's AWQ-folded layer form: an f32 router (the reference's
+    uncontracted f32 chain), the RMSNorm prologue on f32 hidden states, through
+    the streamed kernel's f32-router instantiation at 17 to 64 tokens and below."""
+    from helpers import awq_layer
+    from uocr_hip import MoELayerInt4
+    L = _f32_router(awq_layer(6800 + group, group=group), 6801)
+    L.rms_weight = np.random.default_rng(6802).uniform(0.5, 2.0, L.hidden).astype(np.float32)
+    layer = MoELayerInt4(L)
+    for seq in (17, 32, 64, 1, 8):
+        _check(layer, L, _x(seq, L.hidden, 6800 + seq), dev, "f32", f"wide-f32router-g{group}-t{seq}")
+    layer.close()
+
+
+@pytest.mark.parametrize("group", [32, 64])
+def test_f32_router_16_token_mode(dev, group):
+    """An f32 router without RMSNorm, bf16 and f32 input, 1 to 16 tokens: the
+    16-token mode's f32-router instantiation (every batch size, as the fused
+    kernel needs the bf16 router)."""
+    from helpers import awq_layer
+    from uocr_hip import MoELayerInt4
+    L = _f32_router(awq_layer(6900 + group, group=group), 6901)
+    layer = MoELayerInt4(L)
+    for seq, dt in ((16, "bf16"), (3, "bf16"), (9, "f32"), (1, "f32")):
+        _check(layer, L, _x(seq, L.hidden, 6900 + seq), dev, dt, f"f32router-g{group}-t{seq}-{dt}")
+    layer.close()

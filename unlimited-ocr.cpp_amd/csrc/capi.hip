@@ -312,7 +312,7 @@ bool use_fused(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
 // any input, with the RMSNorm prologue, up to kStreamWideMaxSeq tokens.
 constexpr int kStreamMinSeq = 6;
 bool stream_layer_ok(const uocr_hip_moe_layer* L) {
-    return L->sync && !L->experts_dense && L->router_t && L->down_skt && L->sw &&
+    return L->sync && !L->experts_dense && (L->router_t || L->router_f32) && L->down_skt && L->sw &&
            decode_stream_ok(L->hidden, L->inter, L->group) && L->n_experts + L->n_virtual <= kMaxExperts;
 }
 bool stream_wide(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
@@ -326,8 +326,9 @@ bool use_stream(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
     // the experts see it (no RMSNorm)
     if (L->shared_dense && (x_dtype != UOCR_HIP_DTYPE_BF16 || L->rms_weight)) return false;
     if (stream_wide(L, seq, x_dtype)) return seq <= kStreamWideMaxSeq;
-    // (below kStreamMinSeq the fused kernel is faster, for bf16 input)
-    const int lo = L->decode_kernel == UOCR_HIP_DECODE_STREAM ? 1 : kStreamMinSeq;
+    // (below kStreamMinSeq the fused kernel is faster, for bf16 input; it
+    // needs the bf16 router)
+    const int lo = L->decode_kernel == UOCR_HIP_DECODE_STREAM || !L->router_t ? 1 : kStreamMinSeq;
     return seq >= lo && seq <= kStreamMaxSeq;
 }
 

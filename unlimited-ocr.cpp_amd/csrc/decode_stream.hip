@@ -373,7 +373,7 @@ struct StreamItem {
     int g, s, tb, wi, n, row0, tok;
 };
 
-template <int GPT, int KTG, int KTD, bool ZP, bool WIDE>
+template <int GPT, int KTG, int KTD, bool ZP, bool WIDE, bool F32R>
 __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(DecodeArgs a) {
     using Lay = StreamLds<GPT, KTG, KTD, ZP>;
     constexpr int kRing = ring_units<GPT, WIDE>();
@@ -574,7 +574,7 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
         float* topv = sc + 64;
         uint64_t* etab = reinterpret_cast<uint64_t*>(topv + kMaxTopK);
         float* xs = hand + 256;
-        router_token_regs<KTG, kStreamWaves, WIDE>(a, b, hand, sc, topv, etab, xs, xs + kMaxHidden, rtag);
+        router_token_regs<KTG, kStreamWaves, WIDE, F32R>(a, b, hand, sc, topv, etab, xs, xs + kMaxHidden, rtag);
         store_fence();
         publish_now();
     }
@@ -1143,13 +1143,13 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
     if (tid == 0) store_sc1(prog + b, S + kFusedSteps);
 }
 
-template <int GPT, int KTG, int KTD, bool ZP, bool WIDE>
+template <int GPT, int KTG, int KTD, bool ZP, bool WIDE, bool F32R>
 static hipError_t launch_stream(const DecodeArgs& a, hipStream_t st) {
     using Lay = StreamLds<GPT, KTG, KTD, ZP>;
     constexpr size_t lds = Lay::bytes;
     static_assert(lds <= 160 * 1024, "stream kernel LDS");
     static_assert((KTG * kTileK / kTileRows) % kStreamWaves == 0 && Lay::NTD % 2 == 0, "down tiles per wave");
-    auto kern = decode_stream_kernel<GPT, KTG, KTD, ZP, WIDE>;
+    auto kern = decode_stream_kernel<GPT, KTG, KTD, ZP, WIDE, F32R>;
     static hipError_t attr = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return attr;
     static int resident = [&] {
@@ -1171,26 +1171,32 @@ bool decode_stream_ok(int hidden, int inter, int group) {
 
 bool decode_stream_wide(const DecodeArgs& a) { return a.seq > kStreamMaxSeq || a.rms_weight; }
 
-template <bool WIDE>
+// F32R: the layer's router is f32 (no bf16 copy): its own instantiation,
+// since the f32 weights need twice the router registers
+template <bool WIDE, bool F32R>
 static hipError_t launch_stream_g(const DecodeArgs& a, hipStream_t st) {
     const bool zp = a.gate_z != nullptr;
     switch (a.group) {
-        case 32: return zp ? launch_stream<4, 10, 7, true, WIDE>(a, st) : launch_stream<4, 10, 7, false, WIDE>(a, st);
-        case 64: return zp ? launch_stream<2, 10, 7, true, WIDE>(a, st) : launch_stream<2, 10, 7, false, WIDE>(a, st);
-        default: return zp ? launch_stream<1, 10, 7, true, WIDE>(a, st) : launch_stream<1, 10, 7, false, WIDE>(a, st);
+        case 32:
+            return zp ? launch_stream<4, 10, 7, true, WIDE, F32R>(a, st) : launch_stream<4, 10, 7, false, WIDE, F32R>(a, st);
+        case 64:
+            return zp ? launch_stream<2, 10, 7, true, WIDE, F32R>(a, st) : launch_stream<2, 10, 7, false, WIDE, F32R>(a, st);
+        default:
+            return zp ? launch_stream<1, 10, 7, true, WIDE, F32R>(a, st) : launch_stream<1, 10, 7, false, WIDE, F32R>(a, st);
     }
 }
 
 hipError_t launch_decode_stream(const DecodeArgs& a, hipStream_t st) {
     const bool wide = decode_stream_wide(a);
-    if (a.seq < 1 || a.seq > (wide ? kStreamWideMaxSeq : kStreamMaxSeq) || !a.sync || !a.router_t || !a.status)
+    if (a.seq < 1 || a.seq > (wide ? kStreamWideMaxSeq : kStreamMaxSeq) || !a.sync || !(a.router_t || a.router_f32) || !a.status)
         return hipErrorInvalidValue;
     // wide mode: the f16 expert input rows; with an RMSNorm the residual is the f32 input
     if (wide && (!a.x16 || (a.rms_weight && a.x_bf16))) return hipErrorInvalidValue;
     if (!a.down_skt || !a.sw || (a.gate_z && !a.down_zkt)) return hipErrorInvalidValue;
     if (a.n_experts + a.n_virtual > kMaxExperts || a.n_experts > 64 || a.top_k > kMaxTopK) return hipErrorInvalidValue;
     if (!decode_stream_ok(a.hidden, a.inter, a.group)) return hipErrorInvalidValue;
-    return wide ? launch_stream_g<true>(a, st) : launch_stream_g<false>(a, st);
+    if (!a.router_t) return wide ? launch_stream_g<true, true>(a, st) : launch_stream_g<false, true>(a, st);
+    return wide ? launch_stream_g<true, false>(a, st) : launch_stream_g<false, false>(a, st);
 }
 
 }  // namespace uocr_hip

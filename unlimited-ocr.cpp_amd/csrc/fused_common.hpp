@@ -158,7 +158,10 @@ __device__ __forceinline__ uint64_t candidate_mask(const DecodeArgs& a, float S,
 // rounding); then the reference's sequential sum, the exact row and the
 // exact chain. part then needs kMaxHidden + 2 * H + 64 floats beyond its
 // NW * 128 (rounded squares, the estimate's row).
-template <int KT, int NW = 4, bool PREP = false>
+// F32R: an f32 router (a.router_f32, [H/4][64][4]), held as f32 in registers;
+// its chain is the reference's uncontracted f32 matmul_t, acc + round(x * w)
+// (src/kernels/cpu_ops.cpp:11-24).
+template <int KT, int NW = 4, bool PREP = false, bool F32R = false>
 __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, float* hand, float* sc, float* topv,
                                                   uint64_t* etab, float* xs, float* part, unsigned rtag) {
     constexpr int SEG = KT * 128 / NW;  // columns per wave (H = KT * 128)
@@ -185,10 +188,18 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
         }
         rw[i] = PREP && a.rms_weight && c < H ? a.rms_weight[c] : 0.0f;
     }
-    const uint16_t* wbase = a.router_t + ((size_t)wave * NL * E + e) * 8;
-    u32x4 wr[NL];
+    // bf16: 8 columns per 16-byte load; f32: 4 (two loads per 8 columns)
+    constexpr int NLW = F32R ? 2 * NL : NL;
+    u32x4 wr[NLW];
+    if constexpr (F32R) {
+        const float* wbase = a.router_f32 + ((size_t)wave * NLW * 64 + lane) * 4;
 #pragma unroll
-    for (int i = 0; i < NL; ++i) wr[i] = *reinterpret_cast<const u32x4*>(wbase + (size_t)i * E * 8);
+        for (int i = 0; i < NLW; ++i) wr[i] = *reinterpret_cast<const u32x4*>(wbase + (size_t)i * 64 * 4);
+    } else {
+        const uint16_t* wbase = a.router_t + ((size_t)wave * NL * E + e) * 8;
+#pragma unroll
+        for (int i = 0; i < NL; ++i) wr[i] = *reinterpret_cast<const u32x4*>(wbase + (size_t)i * E * 8);
+    }
     asm volatile("" ::: "memory");  // the whole burst is issued before the row is waited for
 #pragma unroll
     for (int i = 0; i < NXT; ++i) {
@@ -252,14 +263,19 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
             f32x4 c0, c1, w0, w1;
             asm volatile("ds_read_b128 %0, %2 offset:%3\n\tds_read_b128 %1, %2 offset:%4\n\ts_waitcnt lgkmcnt(0)"
                          : "=&v"(c0), "=&v"(c1) : "v"(xea), "i"(i * 32), "i"(i * 32 + 16) : "memory");
-            asm volatile(
-                "v_lshlrev_b32 %0, 16, %8\n\tv_and_b32 %1, 0xffff0000, %8\n\t"
-                "v_lshlrev_b32 %2, 16, %9\n\tv_and_b32 %3, 0xffff0000, %9\n\t"
-                "v_lshlrev_b32 %4, 16, %10\n\tv_and_b32 %5, 0xffff0000, %10\n\t"
-                "v_lshlrev_b32 %6, 16, %11\n\tv_and_b32 %7, 0xffff0000, %11"
-                : "=&v"(w0[0]), "=&v"(w0[1]), "=&v"(w0[2]), "=&v"(w0[3]), "=&v"(w1[0]), "=&v"(w1[1]), "=&v"(w1[2]),
-                  "=&v"(w1[3])
-                : "v"(wr[i][0]), "v"(wr[i][1]), "v"(wr[i][2]), "v"(wr[i][3]));
+            if constexpr (F32R) {
+                w0 = __builtin_bit_cast(f32x4, wr[2 * i]);
+                w1 = __builtin_bit_cast(f32x4, wr[2 * i + 1]);
+            } else {
+                asm volatile(
+                    "v_lshlrev_b32 %0, 16, %8\n\tv_and_b32 %1, 0xffff0000, %8\n\t"
+                    "v_lshlrev_b32 %2, 16, %9\n\tv_and_b32 %3, 0xffff0000, %9\n\t"
+                    "v_lshlrev_b32 %4, 16, %10\n\tv_and_b32 %5, 0xffff0000, %10\n\t"
+                    "v_lshlrev_b32 %6, 16, %11\n\tv_and_b32 %7, 0xffff0000, %11"
+                    : "=&v"(w0[0]), "=&v"(w0[1]), "=&v"(w0[2]), "=&v"(w0[3]), "=&v"(w1[0]), "=&v"(w1[1]),
+                      "=&v"(w1[2]), "=&v"(w1[3])
+                    : "v"(wr[i][0]), "v"(wr[i][1]), "v"(wr[i][2]), "v"(wr[i][3]));
+            }
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 s8[c] = fmaf(c0[c], w0[c], s8[c]);
@@ -280,8 +296,10 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
             S += part[w * 128 + lane];
             SA += part[w * 128 + 64 + lane];
         }
-        // (+ H + 16 terms: the approximate RMSNorm scale of the estimate's row)
-        const uint64_t m = candidate_mask(a, S, SA, (float)(H + SEG / 8 + 64 + (rms ? H + 16 : 0)));
+        // (+ H + 16 terms: the approximate RMSNorm scale of the estimate's row;
+        // F32R: + 16, the chain's rounded products add at most 2^-24 * SA)
+        const uint64_t m =
+            candidate_mask(a, S, SA, (float)(H + SEG / 8 + 64 + (rms ? H + 16 : 0) + (F32R ? 16 : 0)));
         if (lane < 2) {
             const uint64_t w = ((uint64_t)rtag << 32) | (uint32_t)(lane == 0 ? m : (m >> 32));
             __hip_atomic_store(a.sync->cand + 2 * t + lane, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -325,20 +343,29 @@ __device__ __forceinline__ void router_token_regs(const DecodeArgs& a, int t, fl
                 if (i + 1 < NL)
                     asm volatile("ds_read_b128 %0, %2 offset:%3\n\tds_read_b128 %1, %2 offset:%4"
                                  : "=&v"(n0), "=&v"(n1) : "v"(xa), "i"((i + 1) * 32), "i"((i + 1) * 32 + 16));
-                // widen at the point of use (volatile: not hoisted into a spill)
                 f32x4 w0, w1;
-                asm volatile(
-                    "v_lshlrev_b32 %0, 16, %8\n\tv_and_b32 %1, 0xffff0000, %8\n\t"
-                    "v_lshlrev_b32 %2, 16, %9\n\tv_and_b32 %3, 0xffff0000, %9\n\t"
-                    "v_lshlrev_b32 %4, 16, %10\n\tv_and_b32 %5, 0xffff0000, %10\n\t"
-                    "v_lshlrev_b32 %6, 16, %11\n\tv_and_b32 %7, 0xffff0000, %11"
-                    : "=&v"(w0[0]), "=&v"(w0[1]), "=&v"(w0[2]), "=&v"(w0[3]), "=&v"(w1[0]), "=&v"(w1[1]),
-                      "=&v"(w1[2]), "=&v"(w1[3])
-                    : "v"(wr[i][0]), "v"(wr[i][1]), "v"(wr[i][2]), "v"(wr[i][3]));
+                if constexpr (F32R) {
+                    w0 = __builtin_bit_cast(f32x4, wr[2 * i]);
+                    w1 = __builtin_bit_cast(f32x4, wr[2 * i + 1]);
 #pragma unroll
-                for (int c = 0; c < 4; ++c) acc = fmaf(c0[c], w0[c], acc);
+                    for (int c = 0; c < 4; ++c) acc = __fadd_rn(acc, __fmul_rn(c0[c], w0[c]));
 #pragma unroll
-                for (int c = 0; c < 4; ++c) acc = fmaf(c1[c], w1[c], acc);
+                    for (int c = 0; c < 4; ++c) acc = __fadd_rn(acc, __fmul_rn(c1[c], w1[c]));
+                } else {
+                    // widen at the point of use (volatile: not hoisted into a spill)
+                    asm volatile(
+                        "v_lshlrev_b32 %0, 16, %8\n\tv_and_b32 %1, 0xffff0000, %8\n\t"
+                        "v_lshlrev_b32 %2, 16, %9\n\tv_and_b32 %3, 0xffff0000, %9\n\t"
+                        "v_lshlrev_b32 %4, 16, %10\n\tv_and_b32 %5, 0xffff0000, %10\n\t"
+                        "v_lshlrev_b32 %6, 16, %11\n\tv_and_b32 %7, 0xffff0000, %11"
+                        : "=&v"(w0[0]), "=&v"(w0[1]), "=&v"(w0[2]), "=&v"(w0[3]), "=&v"(w1[0]), "=&v"(w1[1]),
+                          "=&v"(w1[2]), "=&v"(w1[3])
+                        : "v"(wr[i][0]), "v"(wr[i][1]), "v"(wr[i][2]), "v"(wr[i][3]));
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) acc = fmaf(c0[c], w0[c], acc);
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) acc = fmaf(c1[c], w1[c], acc);
+                }
                 if (i + 1 < NL) {
                     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(n0), "+v"(n1), "+v"(acc));
                     c0 = n0;
