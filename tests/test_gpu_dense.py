@@ -39,16 +39,28 @@ def test_bf16_shared_mlp_configs(dev, cfg):
 
 
 def test_bf16_shared_paths(dev):
-    """16 tokens: bf16 input takes the single-kernel decode (shared MLP launched
-    before it), f32 input the four-launch path; both run the shared stage."""
+    """16 tokens: bf16 and f32 input both take the single-kernel decode with
+    the shared MLP launched before it (f32 input: on f16 rows of the input)."""
     from uocr_hip import synth
     w = synth.make_config(1)
     L = synth.with_bf16_shared(w.layers[0], 511)
-    t = _stages(L, w.x, "bf16", dev)
-    assert t["fused"] > 0 and t["shared"] > 0, t
-    t = _stages(L, w.x, "f32", dev)
-    assert t["fused"] == 0 and t["shared"] > 0 and t["gate_up"] > 0, t
+    for dt in ("bf16", "f32"):
+        t = _stages(L, w.x, dt, dev)
+        assert t["fused"] > 0 and t["shared"] > 0 and t["gate_up"] == 0, (dt, t)
     check_parity(L, w.x, dev, dtype="f32", label="cfg1-bf16-shared-f32")
+
+
+@pytest.mark.parametrize("seq", [1, 16, 40])
+def test_bf16_shared_rmsnorm_single_kernel(dev, seq):
+    """The engine's layer form (f32 hidden states, RMSNorm prologue, residual,
+    bf16 shared MLP) up to 64 tokens: the shared MLP runs on f16 rows of the
+    normalised input, then the streamed kernel's wide mode adds its rows."""
+    from uocr_hip import synth
+    L = synth.with_bf16_shared(synth.random_layer(540 + seq, group=32, rms=True), 541 + seq)
+    x = synth.bf16_normal(np.random.default_rng(seq + 7), (seq, L.hidden), 1.0)
+    t = _stages(L, x, "f32", dev)
+    assert t["fused"] > 0 and t["shared"] > 0 and t["gate_up"] == 0, t
+    check_parity(L, x, dev, dtype="f32", label=f"rms-bf16-shared-single-t{seq}")
 
 
 @pytest.mark.parametrize("seq", [64, 200])

@@ -322,9 +322,8 @@ bool stream_wide(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
 bool use_stream(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
     if (L->decode_kernel == UOCR_HIP_DECODE_FOUR_LAUNCH || L->decode_kernel == UOCR_HIP_DECODE_FUSED) return false;
     if (!stream_layer_ok(L) || seq < 1) return false;
-    // an unquantised shared MLP runs before the launch, on the bf16 input as
-    // the experts see it (no RMSNorm)
-    if (L->shared_dense && (x_dtype != UOCR_HIP_DTYPE_BF16 || L->rms_weight)) return false;
+    // (an unquantised shared MLP runs before the launch, on f16 rows of the
+    // normalised input when the input is f32 or takes the RMSNorm)
     if (stream_wide(L, seq, x_dtype)) return seq <= kStreamWideMaxSeq;
     // (below kStreamMinSeq the fused kernel is faster, for bf16 input; it
     // needs the bf16 router)
@@ -896,7 +895,15 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
             da.down_skt = L->down_skt;
             da.sw = L->sw;
             da.down_zkt = L->down_zkt;
-            if ((rc = run_shared(x, 1))) return rc;
+            if (L->shared_dense && (x_dtype != UOCR_HIP_DTYPE_BF16 || L->rms_weight)) {
+                stage(6);
+                HIP_TRY(launch_x16_prep(x, x_dtype == UOCR_HIP_DTYPE_BF16, L->rms_weight, L->rms_eps, seq, L->hidden,
+                                        x16, st),
+                        "shared-MLP input launch");
+                if ((rc = run_shared(x16, 0))) return rc;
+            } else if ((rc = run_shared(x, 1))) {
+                return rc;
+            }
             da.shared_y = shared_y;
             stage(5);
             HIP_TRY(launch_decode_stream(da, st), "streamed decode launch");

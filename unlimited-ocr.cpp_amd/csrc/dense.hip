@@ -313,6 +313,58 @@ static hipError_t launch_skinny(const DenseArgs& a, int n_tiles, hipStream_t st)
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// The f16 input rows of an unquantised shared MLP that runs ahead of the
+// single-kernel decode, for f32 hidden states or the RMSNorm prologue
+// (src/kernels/cpu_ops.cpp:58-67: (x * inv) * w with inv = 1 / sqrt(mean(x^2)
+// + eps)). One workgroup per token; the sum of squares is added in parallel,
+// which moves inv by a few units of f32 roundoff, far below the f16 rounding
+// of the result.
+// ---------------------------------------------------------------------------
+constexpr int kPrepThreads = 256;
+constexpr int kPrepCols = 8;  // columns per thread (hidden <= 2048)
+
+__global__ __launch_bounds__(kPrepThreads) void x16_prep_kernel(const void* x, int x_bf16, const float* rms_w,
+                                                                float eps, int H, f16* x16) {
+    __shared__ float wsum[kPrepThreads / 64];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    float v[kPrepCols];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPrepCols; ++i) {
+        const int c = tid + kPrepThreads * i;
+        v[i] = 0.0f;
+        if (c < H)
+            v[i] = x_bf16 ? __uint_as_float((uint32_t)static_cast<const uint16_t*>(x)[(size_t)t * H + c] << 16)
+                          : static_cast<const float*>(x)[(size_t)t * H + c];
+        ss += v[i] * v[i];
+    }
+    float inv = 1.0f;
+    if (rms_w) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        if ((tid & 63) == 0) wsum[tid >> 6] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kPrepThreads / 64; ++w) tot += wsum[w];
+        inv = 1.0f / sqrtf(tot / (float)H + eps);
+    }
+#pragma unroll
+    for (int i = 0; i < kPrepCols; ++i) {
+        const int c = tid + kPrepThreads * i;
+        if (c < H) x16[(size_t)t * H + c] = (f16)(rms_w ? (v[i] * inv) * rms_w[c] : v[i]);
+    }
+}
+
+hipError_t launch_x16_prep(const void* x, bool x_bf16, const float* rms_w, float eps, int seq, int H, f16* x16,
+                           hipStream_t st) {
+    if (seq <= 0) return hipSuccess;
+    if (H > kPrepThreads * kPrepCols || !x || !x16) return hipErrorInvalidValue;
+    launch_k(x16_prep_kernel, dim3(seq), dim3(kPrepThreads), 0, st, x, x_bf16 ? 1 : 0, rms_w, eps, H, x16);
+    return hipGetLastError();
+}
+
 hipError_t launch_dense(const DenseArgs& a, bool gate_up, int bm, int max_tiles, hipStream_t st) {
     if (!dense_shapes_ok(a.k, a.n_out, gate_up, bm)) return hipErrorInvalidValue;
     if (gate_up ? !(a.out16 && a.w1) : !(a.out16 || a.out32)) return hipErrorInvalidValue;

@@ -236,6 +236,9 @@ struct DenseArgs {
 };
 bool dense_shapes_ok(int k, int n_out, bool gate_up, int bm);
 hipError_t launch_dense(const DenseArgs& a, bool gate_up, int bm, int max_tiles, hipStream_t st);
+// f16 rows of x (bf16 or f32), RMS-normalised when rms_w is set, for a dense shared MLP
+hipError_t launch_x16_prep(const void* x, bool x_bf16, const float* rms_w, float eps, int seq, int H, f16* x16,
+                           hipStream_t st);
 
 // reference-layout operator mirrors (mirrors.hip)
 int set_error(int code, const std::string& msg);  // capi.hip: thread's last error text
