@@ -335,7 +335,10 @@ bool use_stream(const uocr_hip_moe_layer* L, int seq, int x_dtype) {
 // Tile rows of the unquantised expert kernels: decode-sized tiles below the
 // prefill threshold, 128-slot MFMA tiles from there (when the shapes allow)
 int dense_experts_bm(const uocr_hip_moe_layer* L, int seq) {
-    return (seq >= kPrefillMinSeq && dense_shapes_ok(L->hidden, L->inter, true, kDenseTiledBM) &&
+    if (seq < kPrefillMinSeq) return kDenseSkinnyBM;
+    // the large-tile kernel with f16 weight fragments DMA'd to LDS (K in {896, 1280})
+    if (prefill_big_ok(L->hidden, L->inter)) return kPrefillBigTileRows;
+    return (dense_shapes_ok(L->hidden, L->inter, true, kDenseTiledBM) &&
             dense_shapes_ok(L->inter, L->hidden, false, kDenseTiledBM))
                ? kDenseTiledBM
                : kDenseSkinnyBM;
@@ -1021,7 +1024,38 @@ int uocr_hip_moe_layer_forward(const uocr_hip_moe_layer* L, const void* x, int x
     HIP_TRY(launch_group(g, st), "group launch");
     stage(2);
     const f16* y16 = (const f16*)(ws + p.y);
-    if (L->experts_dense) {
+    if (L->experts_dense && p.bm == kPrefillBigTileRows) {
+        ExpertArgs gu{};
+        gu.a = x16;
+        gu.gather = 1;
+        gu.w0 = reinterpret_cast<const uint8_t*>(L->egate);
+        gu.w1 = reinterpret_cast<const uint8_t*>(L->eup);
+        gu.w_stride = (long long)L->inter * L->hidden * 2;
+        gu.n_rows = L->inter;
+        gu.k = L->hidden;
+        gu.bm = p.bm;
+        gu.slot_tok = g.slot_tok;
+        gu.counts = g.counts;
+        gu.offsets = g.offsets;
+        gu.tile_e = g.tile_e;
+        gu.tile_m0 = g.tile_m0;
+        gu.tile_info = g.tile_info;
+        gu.n_tiles = g.n_tiles;
+        gu.act_out = (f16*)(ws + p.act);
+        gu.status = &L->sync->error;
+        HIP_TRY(launch_experts_prefill_dense(gu, true, p.max_tiles, st), "gate/up launch");
+        stage(3);
+        ExpertArgs dn = gu;
+        dn.a = gu.act_out;
+        dn.gather = 0;
+        dn.w0 = reinterpret_cast<const uint8_t*>(L->edown);
+        dn.w1 = nullptr;
+        dn.n_rows = L->hidden;
+        dn.k = L->inter;
+        dn.act_out = nullptr;
+        dn.y_out = (f16*)(ws + p.y);
+        HIP_TRY(launch_experts_prefill_dense(dn, false, p.max_tiles, st), "down launch");
+    } else if (L->experts_dense) {
         DenseArgs gu{};
         gu.a = x16;
         gu.a_kind = 0;

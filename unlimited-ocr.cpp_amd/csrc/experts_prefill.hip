@@ -259,7 +259,13 @@ constexpr int kRingAhead = 4;               // B fragments read ahead of their u
 constexpr int kRing = kRingAhead + 2;       // register ring size
 constexpr int lds_reads_after(int f) { return 63 - f < kRingAhead - 1 ? 63 - f : kRingAhead - 1; }
 
-template <int GPT, bool GU, int KT, bool ZP>
+// DW: unquantised experts (the reference's BF16 expert format, uploaded as
+// f16, row-major [rows][K], a.w_stride bytes per expert): the B fragments go
+// global -> LDS by 16-byte DMA, one k-tile ahead, in the same fragment order
+// (lane l of fragment (k-step, n-block): weight row n-block * 32 + l % 32,
+// columns k-step * 16 + 8 * (l / 32) ..), so there is no dequantisation and no
+// weight register; GPT and ZP are unused.
+template <int GPT, bool GU, int KT, bool ZP, bool DW = false>
 __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) {
     // B fragments: [buffer][k-step 0..7][n-block 0..7][64 lanes][8 f16]
     __shared__ __attribute__((aligned(16))) f16 Bs[2][8 * kBigNB * kFragHalfs];
@@ -330,6 +336,25 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
             const int n = wave * 16 + (lane & 15), q4 = lane >> 4;
             bdst0 = (uint32_t)((((q4 >> 1) * kBigNB + (n >> 5)) * 64 + (n & 31) + 32 * (q4 & 1)) * 16);
         }
+        // DW: this wave DMAs the fragments of n-blocks 2 * wave and 2 * wave + 1
+        // (all 8 k-steps); the lane's row of each and its first column
+        const f16* drow[2];
+        if constexpr (DW) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int n = (2 * wave + h) * 32 + (lane & 31);  // local weight row
+                const f16* base;
+                int grow;
+                if constexpr (GU) {
+                    base = reinterpret_cast<const f16*>((n < kBigBN / 2 ? a.w0 : a.w1) + (size_t)e * a.w_stride);
+                    grow = ntile * (kBigBN / 2) + (n & (kBigBN / 2 - 1));
+                } else {
+                    base = reinterpret_cast<const f16*>(a.w0 + (size_t)e * a.w_stride);
+                    grow = ntile * kBigBN + n;
+                }
+                drow[h] = base + (size_t)grow * K + 8 * (lane >> 5);
+            }
+        }
 
         // The k-tile pipeline keeps its own load schedule: every global load is
         // issued by inline asm at a fixed point and every wait is an explicit
@@ -344,7 +369,7 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
         //     start of k-tile kt, staged into LDS during k-tile kt+1.
         // Issue order within k-tile kt: B(kt+2), then A(kt+1, ks) after k-step ks.
         constexpr int AK = JN;         // activation loads per k-step
-        constexpr int NB = (ZP ? 3 : 2) * UNITS;  // loads per k-tile of weights
+        constexpr int NB = DW ? 16 : (ZP ? 3 : 2) * UNITS;  // loads (DW: DMAs) per k-tile of weights
         u32x4 braw[2][UNITS];
         typename std::conditional<GPT == 4, u32x2, uint32_t>::type bscr[2][UNITS], bzr[2][UNITS];
         f16x8 areg[JN][8];
@@ -355,6 +380,16 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
             for (int j = 0; j < JN; ++j) {
                 gload<kt * kTileK * 2 + ks * 32>(areg[j][ks], arow[j]);
             }
+        };
+        // DW: the 16 fragment DMAs of k-tile kt into buffer kt & 1
+        auto issue_bd = [&](auto ktc) {
+            constexpr int kt = decltype(ktc)::value;
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    load_lds16(drow[h] + kt * kTileK + ks * 16,
+                               reinterpret_cast<uint8_t*>(&Bs[kt & 1][0]) + (ks * kBigNB + 2 * wave + h) * 1024);
         };
         auto issue_b = [&](auto ktc) {
             constexpr int kt = decltype(ktc)::value;
@@ -419,19 +454,32 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
 #pragma unroll
             for (int nb = 0; nb < kBigNB; ++nb) acc[j][nb] = f32x16{};
 
-        // prologue: B(0), B(1), A(0); stage B(0)
-        issue_b(std::integral_constant<int, 0>{});
-        if constexpr (KT > 1) issue_b(std::integral_constant<int, 1>{});
-        static_for<8>([&](auto ksc) { issue_a(std::integral_constant<int, 0>{}, ksc); });
-        wait_b(std::integral_constant<int, (KT > 1 ? NB : 0) + 8 * AK>{}, 0);
-        static_for<UNITS>([&](auto ic) { static_for<4>([&](auto sc) { stage_run(0, ic, sc); }); });
-        lgkm_wait<0>();
+        if constexpr (DW) {
+            // prologue: B(0) by DMA, A(0); B(0) landed in every wave's part
+            issue_bd(std::integral_constant<int, 0>{});
+            static_for<8>([&](auto ksc) { issue_a(std::integral_constant<int, 0>{}, ksc); });
+            vm_wait<8 * AK>();
+        } else {
+            // prologue: B(0), B(1), A(0); stage B(0)
+            issue_b(std::integral_constant<int, 0>{});
+            if constexpr (KT > 1) issue_b(std::integral_constant<int, 1>{});
+            static_for<8>([&](auto ksc) { issue_a(std::integral_constant<int, 0>{}, ksc); });
+            wait_b(std::integral_constant<int, (KT > 1 ? NB : 0) + 8 * AK>{}, 0);
+            static_for<UNITS>([&](auto ic) { static_for<4>([&](auto sc) { stage_run(0, ic, sc); }); });
+            lgkm_wait<0>();
+        }
         __syncthreads();
         static_for<KT>([&](auto ktc) {
             constexpr int kt = decltype(ktc)::value;
             constexpr bool more = kt + 1 < KT;
-            constexpr int nB2 = kt + 2 < KT ? NB : 0;
-            if constexpr (kt + 2 < KT) issue_b(std::integral_constant<int, kt + 2>{});
+            // weight loads issued after A(kt, *) and before A(kt + 1, *): DW the
+            // DMAs of B(kt + 1) (into the buffer the last k-tile read), else B(kt + 2)
+            constexpr int nB2 = DW ? (more ? NB : 0) : (kt + 2 < KT ? NB : 0);
+            if constexpr (DW) {
+                if constexpr (more) issue_bd(std::integral_constant<int, kt + 1>{});
+            } else {
+                if constexpr (kt + 2 < KT) issue_b(std::integral_constant<int, kt + 2>{});
+            }
             // B fragments stream from LDS through a 6-deep register ring, read
             // 4 fragments (8 MFMAs) ahead of their use: fragment f = ks * 8 + nb
             const uint32_t bb = lds_addr(Bs[kt & 1]) + lane * 16;
@@ -453,13 +501,15 @@ __global__ __launch_bounds__(256) void experts_prefill_big_kernel(ExpertArgs a) 
                 // every third fragment from fragment 8 on, so the VALU work
                 // interleaves with the MFMAs in flight
                 constexpr int run = (f - 8) / 3;
-                if constexpr (more && f >= 8 && (f - 8) % 3 == 0 && run < 4 * UNITS) {
+                if constexpr (!DW && more && f >= 8 && (f - 8) % 3 == 0 && run < 4 * UNITS) {
                     // B(kt+1) was issued before A(kt), B(kt+2) and A(kt+1, 0)
                     if constexpr (run == 0) wait_b(std::integral_constant<int, 8 * AK + nB2 + AK>{}, (kt + 1) & 1);
                     stage_run(kt + 1, std::integral_constant<int, run / 4>{}, std::integral_constant<int, run % 4>{});
                 }
             });
             lgkm_wait<0>();  // this k-tile's staging writes (asm, not tracked by the compiler)
+            // DW: B(kt + 1)'s DMAs, older than A(kt + 1, *), have landed
+            if constexpr (DW && more) vm_wait<8 * AK>();
             __syncthreads();
         });
 
@@ -558,6 +608,27 @@ static hipError_t launch_prefill_g(const ExpertArgs& a, int max_tiles, hipStream
         case 32: launch_k((experts_prefill_kernel<4, GU, ZP>), grid, dim3(256), 0, st, a); break;
         case 64: launch_k((experts_prefill_kernel<2, GU, ZP>), grid, dim3(256), 0, st, a); break;
         case 128: launch_k((experts_prefill_kernel<1, GU, ZP>), grid, dim3(256), 0, st, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// unquantised experts (f16 weights) on the large-tile kernel, 256-slot tiles
+hipError_t launch_experts_prefill_dense(const ExpertArgs& a, bool gate_up, int max_tiles, hipStream_t st) {
+    if (max_tiles <= 0) return hipSuccess;
+    if (a.bm != kBigBM || !a.w0 || (gate_up && !a.w1)) return hipErrorInvalidValue;
+    const int n_ntiles = gate_up ? (a.n_rows / (kBigBN / 2)) : (a.n_rows / kBigBN);
+    if (n_ntiles * (gate_up ? kBigBN / 2 : kBigBN) != a.n_rows) return hipErrorInvalidValue;
+    const dim3 grid(((max_tiles + 7) / 8) * 8 * n_ntiles);
+    switch (a.k / kTileK) {
+        case 7:
+            if (gate_up) launch_k((experts_prefill_big_kernel<4, true, 7, false, true>), grid, dim3(256), 0, st, a);
+            else launch_k((experts_prefill_big_kernel<4, false, 7, false, true>), grid, dim3(256), 0, st, a);
+            break;
+        case 10:
+            if (gate_up) launch_k((experts_prefill_big_kernel<4, true, 10, false, true>), grid, dim3(256), 0, st, a);
+            else launch_k((experts_prefill_big_kernel<4, false, 10, false, true>), grid, dim3(256), 0, st, a);
+            break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -212,6 +212,7 @@ constexpr size_t kGroupScanLds = 96 * 1024;  // per-(chunk, expert) counts of th
 bool group_fits(int seq, int top_k, int n_experts);  // the grouping scan's LDS holds seq * top_k entries
 hipError_t router_overflow_read(int clear, int* flag);  // sticky count > cap flag of the router mirror
 hipError_t launch_experts_prefill(const ExpertArgs& a, bool gate_up, int max_tiles, hipStream_t st);
+hipError_t launch_experts_prefill_dense(const ExpertArgs& a, bool gate_up, int max_tiles, hipStream_t st);
 hipError_t launch_combine(const CombineArgs& c, hipStream_t st);
 
 // Unquantised (bf16 / f32 checkpoint) matrices held as f16 row-major
