@@ -25,11 +25,13 @@
 //   workgroups [0, T)   the router of token t (candidates, then the exact
 //                       chain, scores and top_k); wide mode: afterwards they
 //                       take items from the end of the item list
-//   workgroups [T, P)   16-token mode: items i = w, w + PW, ... (w = b - T),
-//                       group-major; wide mode: item w, then items drawn from
-//                       a per-call ticket counter. Each worker issues the
-//                       next item's weights while it computes the current
-//                       item's down partial
+//   workgroups [T, P)   16-token mode: item w (w = b - T), group-major,
+//                       then the w-th, (w + PW)-th, ... item from PW on whose
+//                       group some token's candidates name (or a shared
+//                       group); wide mode: item w, then items drawn from a
+//                       per-call ticket counter. Each worker issues the next
+//                       item's weights while it computes the current item's
+//                       down partial
 //   combine units       16-token mode: (token t, 128 output columns); wide
 //                       mode: (token t, several column blocks), one per
 //                       workgroup from the last one down: after the exact
@@ -44,7 +46,7 @@
 // Cross-workgroup data goes through agent-coherent accesses with bounded
 // waits (fused_common.hpp): per-workgroup progress words (a workgroup
 // publishes S + steps, every word ends the call at S + kFusedSteps), tagged
-// candidate words and, in wide mode, tagged per-item completion words.
+// candidate words and tagged per-item completion words.
 #include <hip/hip_runtime.h>
 #include "fused_common.hpp"
 
@@ -735,6 +737,34 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
         if (lo + hi >= NTOT - PW) return NTOT;
         return b < T ? NTOT - 1 - hi : PW + lo;
     };
+    // 16-token mode: the first PW items are static (worker w: item w); worker
+    // w's k-th further item is the (w + (k - 1) PW)-th item from PW on whose
+    // group is live (a candidate token, or a shared group), so a group that no
+    // token can pick is not streamed past the first round. Wave 0, after the
+    // candidates are resolved (tokmask).
+    auto live_item = [&](int j) -> int {
+        int base = 0;
+        for (int g0 = 0; g0 < G; g0 += 64) {
+            const int g = g0 + lane;
+            int n = 0;
+            if (g < G && (g >= E || (int)lds_read_u32(tokmask + g) != 0)) n = max(0, (g + 1) * NS - max(PW, g * NS));
+            int sn = n;
+            for (int d = 1; d < 64; d <<= 1) {
+                const int u = __shfl_up(sn, d, 64);
+                if (lane >= d) sn += u;
+            }
+            const int tot = __builtin_amdgcn_readfirstlane(__shfl(sn, 63, 64));
+            if (j < base + tot) {
+                const uint64_t hit = __ballot(n > 0 && j < base + sn);
+                const int l = (int)__builtin_ctzll(hit);
+                const int before = __builtin_amdgcn_readfirstlane(__shfl(sn - n, l, 64));
+                return max(PW, (g0 + l) * NS) + (j - base - before);
+            }
+            base += tot;
+        }
+        return NTOT;
+    };
+    int n_more = 0;  // 16-token mode: further items taken so far
     if (WIDE || (b >= T && b - T < NI)) {
         const int w = b - T;
         StreamItem first_item;
@@ -904,6 +934,14 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
                 // every wave is past this item's gate/up (As reads) and the
                 // previous item's down (Ad reads); the next item is known
                 lds_barrier();
+            } else {
+                if (first) cand_resolve();
+                if (wave == 0) {
+                    const int nx = live_item((b - T) + n_more * PW);
+                    if (lane == 0) lds_write_u32(tkL, nx);
+                }
+                ++n_more;
+                lds_barrier();  // (also shares cm32 / tokmask)
             }
         };
         // The second half: act, the next item's scales and token rows, the
@@ -946,17 +984,9 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
             // older than the 2 * KTG unit loads of this gate/up phase (and the
             // next item's token rows and gate/up scales)
             wait_vm<2 * KTG + (WIDE && MORE ? NXD : 0)>();
-            if (!WIDE && first) cand_resolve();
-            lds_barrier();  // Ad, cm32 / tokmask complete; every wave's older stores done
-            if (!first) {
-                // the previous item (no fence: the counter waits ordered its stores)
-                if constexpr (WIDE) {
-                    if (tid == 0) store_sc1(reinterpret_cast<int*>(sy->item_done + pi), (int)rtag);
-                } else {
-                    ++k;
-                    if (tid == 0) store_sc1(prog + b, S + k);
-                }
-            }
+            lds_barrier();  // Ad complete; every wave's older stores done
+            // the previous item (no fence: the counter waits ordered its stores)
+            if (!first && tid == 0) store_sc1(reinterpret_cast<int*>(sy->item_done + pi), (int)rtag);
             have_cand = true;
             const int tm = WIDE ? 0 : (g < E ? (int)lds_read_u32(tokmask + g) : (int)((1u << T) - 1u));
             // down: the act fragments (B operand) once for the item, then the
@@ -1002,34 +1032,28 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
         int i = i0;
         StreamItem cur = first_item, nxt = first_item;
         f32x4 acc0, acc1;
-        if constexpr (WIDE) {
-            int pi = -1;
-            bool first = true;
-            while (true) {
-                item_a(cur, first, acc0, acc1);
-                const int nx = __builtin_amdgcn_readfirstlane((int)lds_read_u32(tkL));  // (uniform: see NTOT)
-                if (nx >= NTOT) break;
-                item_b(i, nx, pi, cur, nxt, first, acc0, acc1, std::true_type{});
-                pi = i;
-                i = nx;
+        int pi = -1;
+        bool first = true;
+        while (true) {
+            item_a(cur, first, acc0, acc1);
+            const int nx = __builtin_amdgcn_readfirstlane((int)lds_read_u32(tkL));  // (uniform: see NTOT)
+            if (nx >= NTOT) break;
+            item_b(i, nx, pi, cur, nxt, first, acc0, acc1, std::true_type{});
+            pi = i;
+            i = nx;
+            if constexpr (WIDE) {
                 cur = nxt;
-                first = false;
+            } else {
+                cur = sitem(nx);
             }
-            item_b(i, NTOT, pi, cur, nxt, first, acc0, acc1, std::false_type{});
-        } else {
-            for (; i + PW < NTOT; i += PW) {
-                item_a(cur, i == i0, acc0, acc1);
-                item_b(i, i + PW, i - PW, cur, nxt, i == i0, acc0, acc1, std::true_type{});
-                cur = sitem(i + PW);
-            }
-            item_a(cur, i == i0, acc0, acc1);
-            item_b(i, i + PW, i - PW, cur, nxt, i == i0, acc0, acc1, std::false_type{});
+            first = false;
         }
+        item_b(i, NTOT, pi, cur, nxt, first, acc0, acc1, std::false_type{});
         report_f16_overflow(a.status, ovf);
-        // the last item: its stores, then the step
+        // the last item: its stores, then the step and its completion word
         store_fence();
         publish_now();
-        if (WIDE && tid == 0) store_sc1(reinterpret_cast<int*>(sy->item_done + i), (int)rtag);
+        if (tid == 0) store_sc1(reinterpret_cast<int*>(sy->item_done + i), (int)rtag);
       }
     }
 
@@ -1115,17 +1139,29 @@ __global__ __launch_bounds__(kStreamThreads, 2) void decode_stream_kernel(Decode
             wts_c[tid] = load_cg(a.wts + (size_t)t * K + tid);
         }
         __syncthreads();
-        // the items of the picked groups and of the shared groups
-        const int n_wait = (K + V) * NS;
-        wait_steps(
-            [&](int q, int& owner, int& step) {
+        // the items of the picked groups and of the shared groups (a group no
+        // token can pick has only its first-round items: an exact pick there
+        // is outside the candidates, flagged below)
+        if (wave == 0) {
+            const int n_wait = (K + V) * NS;
+            for (int q0 = 0; q0 < n_wait; q0 += 64) {
+                const int q = q0 + lane;
                 const int jj = q / NS, s = q % NS;
-                const int g = jj < K ? ids_c[jj] : E + (jj - K);
+                const int g = q >= n_wait ? 0 : jj < K ? ids_c[jj] : E + (jj - K);
+                const bool want = q < n_wait && (g >= E || g * NS + s < PW || (int)lds_read_u32(tokmask + g) != 0);
                 const int i = g * NS + s;
-                owner = T + i % PW;
-                step = i / PW + 1;
-            },
-            n_wait);
+                int it = 0;
+                while (__ballot(want && load_cg(sy->item_done + i) != rtag)) {
+                    if (++it > kSpinLimit) {
+                        if (lane == 0) report_timeout_to(a.status, sy, rtag);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+            }
+        }
+        __syncthreads();
+        fence_wg_acquire();
         bool bad = load_cg(&sy->call_fault) == rtag;
         for (int j = 0; j < K; ++j) {
             const int id = ids_c[j];
